@@ -1,0 +1,282 @@
+/*
+ * jfh.h -- C ABI of the MI355X (gfx950) native Qwen2 stage engine.
+ *
+ * Plain pointers and sizes only. Every call that can fail returns a
+ * jfh_status by value (code + message), like the reference loader's
+ * jf_status (runtime/engines/native/include/jetsonfabric/engine.h:51-63).
+ * Opaque handles are created/destroyed in pairs; caller-owned input arrays
+ * are read during the call; caller-provided output arrays are written.
+ *
+ * Each entry point names the reference interface it replaces.
+ */
+#ifndef JFH_H
+#define JFH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: 0..5 equal jf_status_code (engine.h:51-58); 6 = device error. */
+typedef enum jfh_status_code {
+    JFH_STATUS_OK = 0,
+    JFH_STATUS_INVALID_ARGUMENT = 1,
+    JFH_STATUS_IO_ERROR = 2,
+    JFH_STATUS_FORMAT_ERROR = 3,
+    JFH_STATUS_NOT_FOUND = 4,
+    JFH_STATUS_OUT_OF_MEMORY = 5,
+    JFH_STATUS_DEVICE_ERROR = 6
+} jfh_status_code;
+
+typedef struct jfh_status {
+    int32_t code;
+    char message[256];
+} jfh_status;
+
+typedef struct jfh_model jfh_model;     /* host-resident weights + hparams */
+typedef struct jfh_engine jfh_engine;   /* device-resident weights, one HIP stream */
+typedef struct jfh_session jfh_session; /* one sequence's F16 KV cache + position */
+
+/* Qwen2 hyper-parameters (runtime/engines/native/src/qwen2_metadata.hpp:10-18). */
+typedef struct jfh_model_params {
+    uint32_t n_layer;
+    uint32_t n_embd;
+    uint32_t n_ff;
+    uint32_t n_head;
+    uint32_t n_head_kv;
+    uint32_t n_ctx;
+    uint32_t n_vocab;
+    uint32_t head_dim;
+    float rope_base;
+    float rms_eps;
+} jfh_model_params;
+
+/* Tensor view (jf_tensor_view, engine.h:85-96). `name` is NUL-terminated and
+ * valid, like `data`, until the model is closed. */
+typedef struct jfh_tensor_view {
+    const char * name;
+    uint32_t type;
+    uint32_t rank;
+    uint64_t shape[4];
+    int32_t layer;
+    const void * data;
+    uint64_t size;
+} jfh_tensor_view;
+
+/* Residency statistics (jf_model_stats, engine.h:74-83). */
+typedef struct jfh_model_stats {
+    uint32_t layer_start;
+    uint32_t layer_end;
+    uint32_t layer_count;
+    uint64_t selected_weight_bytes;
+    uint64_t total_weight_bytes;
+    uint64_t selected_tensor_count;
+    uint64_t total_tensor_count;
+} jfh_model_stats;
+
+/* Synthetic model recipe: N(0, stddev) weights keyed by (seed, tensor name). */
+typedef struct jfh_synth_spec {
+    jfh_model_params params;
+    uint32_t type_linear;
+    uint32_t type_embd;
+    uint32_t type_output;
+    uint32_t tied_output; /* output.weight is a byte copy of token_embd.weight */
+    uint32_t output_bias;
+    uint32_t pad;
+    uint64_t seed;
+    float stddev;
+    int32_t threads; /* 0 = all hardware threads */
+} jfh_synth_spec;
+
+typedef struct jfh_engine_options {
+    int32_t device;     /* HIP device ordinal */
+    int32_t use_graphs; /* capture each step shape in a HIP graph */
+} jfh_engine_options;
+
+typedef struct jfh_engine_info {
+    uint64_t weight_bytes;
+    uint32_t prefill_chunk;
+    char device_name[128];
+} jfh_engine_info;
+
+/* ---------------------------------------------------------------- formats */
+
+/* jf_tensor_type_layout (engine.h:100-104; engine.c:284-310). */
+jfh_status jfh_tensor_type_layout(uint32_t type, uint32_t * block_elements, uint32_t * block_bytes);
+
+/* SHA-256 used for JFM segment integrity (sha256.h:20-23 of the reference loader). */
+jfh_status jfh_sha256(const void * data, size_t size, uint8_t digest[32]);
+
+/* ---------------------------------------------------------------- JFM v2 packages */
+
+typedef struct jfh_package jfh_package; /* mmapped JFM v2 package, no model validation */
+
+/* Residency statistics of an open package (jf_model_stats, engine.h:74-83). */
+typedef struct jfh_package_stats {
+    uint32_t layer_start;
+    uint32_t layer_end;
+    uint32_t layer_count;
+    uint32_t pad;
+    uint64_t selected_weight_bytes;
+    uint64_t total_weight_bytes;
+    uint64_t mapped_bytes;
+    uint64_t selected_tensor_count;
+    uint64_t total_tensor_count;
+} jfh_package_stats;
+
+/* jf_model_open (engine.h:106-111; engine.c:513-757): opens the segments of the
+ * half-open layer range (layer_end UINT32_MAX = all), verifying SHA-256s. */
+jfh_status jfh_package_open(const char * package_path, uint32_t layer_start, uint32_t layer_end,
+                            uint32_t verify_hashes, jfh_package ** out);
+/* jf_model_close (engine.h:113). */
+void jfh_package_close(jfh_package * package);
+/* jf_model_get_stats (engine.h:115). */
+jfh_status jfh_package_get_stats(const jfh_package * package, jfh_package_stats * out);
+/* jf_model_tensor_count / jf_model_tensor_at / jf_model_find_tensor (engine.h:117-129);
+ * tensors are sorted by name. */
+size_t jfh_package_tensor_count(const jfh_package * package);
+jfh_status jfh_package_tensor_at(const jfh_package * package, size_t index, jfh_tensor_view * out);
+jfh_status jfh_package_find_tensor(const jfh_package * package, const char * name, jfh_tensor_view * out);
+/* jf_model_get_gguf_metadata / jf_model_get_source_sha256 (engine.h:141-150). */
+jfh_status jfh_package_gguf_metadata(const jfh_package * package, const void ** data, size_t * size);
+jfh_status jfh_package_source_sha256(const jfh_package * package, uint8_t digest[32]);
+
+/* ---------------------------------------------------------------- host model */
+
+/* jf_model_open (engine.h:107-111) + TensorStore/load_qwen2_hparams
+ * (tensor_store.cpp:57-116; qwen2_metadata.cpp:90-125). layer_end may be
+ * UINT32_MAX for "all layers". */
+jfh_status jfh_model_open(const char * package_path, uint32_t layer_start, uint32_t layer_end,
+                          uint32_t verify_hashes, jfh_model ** out);
+
+/* Synthetic weights for benchmarks (no reference counterpart: the reference
+ * imports real GGUFs, runtime/compiler/jf_model_compile.cpp:549-645). */
+jfh_status jfh_model_synthesize(const jfh_synth_spec * spec, jfh_model ** out);
+
+/* In-memory model builder (the reference's tiny fixture writer,
+ * runtime/compiler/model_fixture.cpp:92-133, builds models tensor by tensor). */
+jfh_status jfh_model_create(const jfh_model_params * params, jfh_model ** out);
+jfh_status jfh_model_add_tensor(jfh_model * model, const char * name, uint32_t type, uint32_t rank,
+                                const uint64_t * shape, const void * data, uint64_t size);
+/* Validates names/shapes (qwen2_architecture.cpp:80-118). */
+jfh_status jfh_model_finalize(jfh_model * model);
+
+/* Writes a JFM v2 package (docs/jfm-v2-format.md; segment grouping
+ * runtime/compiler/jf_model_compile.cpp:612-624). */
+jfh_status jfh_model_write_package(const jfh_model * model, const char * directory);
+
+/* jf_model_close (engine.h:113). */
+void jfh_model_close(jfh_model * model);
+
+jfh_status jfh_model_get_params(const jfh_model * model, jfh_model_params * out);
+/* jf_model_get_stats (engine.h:115). */
+jfh_status jfh_model_get_stats(const jfh_model * model, jfh_model_stats * out);
+/* jf_model_tensor_count / jf_model_tensor_at / jf_model_find_tensor (engine.h:117-129). */
+size_t jfh_model_tensor_count(const jfh_model * model);
+jfh_status jfh_model_tensor_at(const jfh_model * model, size_t index, jfh_tensor_view * out);
+jfh_status jfh_model_find_tensor(const jfh_model * model, const char * name, jfh_tensor_view * out);
+/* Hex SHA-256 of the source GGUF (ModelInfo::source_sha256, native_inference.hpp:34). */
+jfh_status jfh_model_source_sha256(const jfh_model * model, char hex[65]);
+
+/* ---------------------------------------------------------------- engine */
+
+/* NativeEngine(package, EngineOptions) (native_inference.hpp:128-129): weights
+ * are uploaded once; the model may be closed afterwards. */
+jfh_status jfh_engine_create(const jfh_model * model, const jfh_engine_options * options, jfh_engine ** out);
+void jfh_engine_destroy(jfh_engine * engine);
+jfh_status jfh_engine_get_info(const jfh_engine * engine, jfh_engine_info * out);
+
+/* NativeEngine::create_session (native_inference.hpp:143). */
+jfh_status jfh_session_create(jfh_engine * engine, uint32_t capacity, jfh_session ** out);
+void jfh_session_destroy(jfh_session * session);
+/* NativeSession::capacity/position (native_inference.hpp:108-109). */
+uint32_t jfh_session_capacity(const jfh_session * session);
+uint32_t jfh_session_position(const jfh_session * session);
+
+/* NativeSession::prefill_greedy / Qwen2Session::prefill_logits
+ * (native_inference.hpp:110; qwen2_architecture.cpp:825-879). logits may be
+ * NULL; otherwise it receives n_vocab floats for the last row. */
+jfh_status jfh_session_prefill(jfh_session * session, const int32_t * tokens, uint32_t n,
+                               int32_t * out_token, float * logits);
+
+/* NativeSession::decode_greedy / decode_logits (native_inference.hpp:111;
+ * qwen2_architecture.cpp:881-907). */
+jfh_status jfh_session_decode(jfh_session * session, int32_t token, int32_t * out_token, float * logits);
+
+/* Draft verification: tokens = [previous, draft...] decoded at consecutive
+ * positions in one pass; out_tokens gets the greedy id after every row, and
+ * out_accepted the number of leading draft tokens equal to those ids. The
+ * session advances by n; the caller rolls back n - 1 - accepted. Replaces the
+ * llama.cpp multi-row verify (llama_cpp_stage_adapter.cpp:350-386, 388-475).
+ * logits may be NULL, else n * n_vocab floats. */
+jfh_status jfh_session_verify(jfh_session * session, const int32_t * tokens, uint32_t n, int32_t * out_tokens,
+                              uint32_t * out_accepted, float * logits);
+
+/* NativeSession::rollback (native_inference.hpp:116; qwen2_architecture.cpp:818-823). */
+jfh_status jfh_session_rollback(jfh_session * session, uint32_t n);
+
+/* Batched decode/verify over several sessions in one pass
+ * (Executor::execute_batch, runtime/inference/executor.hpp:20-28;
+ * continuous_batching_executor.cpp:60-100). lengths[i] rows for sessions[i],
+ * tokens concatenated; out_tokens receives sum(lengths) ids, out_accepted one
+ * count per session (may be NULL). */
+jfh_status jfh_engine_step_batch(jfh_engine * engine, jfh_session * const * sessions, uint32_t count,
+                                 const int32_t * tokens, const uint32_t * lengths, int32_t * out_tokens,
+                                 uint32_t * out_accepted);
+
+/* Parity entry points: GPU dequantization of tensor rows (bit-exact with the
+ * GGML layouts) and a matmul through the engine's kernels. */
+jfh_status jfh_engine_dequantize(jfh_engine * engine, const char * tensor, uint32_t row0, uint32_t n_rows,
+                                 float * out);
+jfh_status jfh_engine_matmul(jfh_engine * engine, const char * tensor, const float * x, uint32_t n_tok, float * y);
+
+/* Device time of `iterations` back-to-back decode steps (ms, HIP events on the
+ * engine stream) after `warmup` untimed ones; the session is rolled back after
+ * each step, so every step runs at the same position. */
+jfh_status jfh_session_time_steps(jfh_session * session, const int32_t * tokens, uint32_t n, uint32_t all_logits,
+                                  uint32_t warmup, uint32_t iterations, double * ms_per_step);
+
+/* Per-kernel profile of one step (no reference counterpart: the reference
+ * measures with Nsight, docs/benchmarks/evidence/...kernels_cuda_gpu_kern_sum.csv).
+ * The step runs `iterations` times without graphs with HIP events around every
+ * launch on the engine stream; one entry per kernel, sorted by device time. */
+typedef struct jfh_kernel_stat {
+    char label[64];
+    double launches; /* per step */
+    double total_ms; /* device ms per step */
+    double bytes;    /* algorithmic HBM bytes per step */
+} jfh_kernel_stat;
+
+jfh_status jfh_session_profile_step(jfh_session * session, const int32_t * tokens, uint32_t n, uint32_t all_logits,
+                                    uint32_t iterations, jfh_kernel_stat * out, uint32_t capacity, uint32_t * count);
+
+/* ---------------------------------------------------------------- speculation */
+
+/* PromptLookupDraft::propose (runtime/speculative/prompt_lookup_draft.cpp:15-44). */
+jfh_status jfh_prompt_lookup_propose(const uint32_t * history, size_t n, uint32_t max_ngram, uint32_t min_ngram,
+                                     uint32_t max_tokens, uint32_t * out, uint32_t * out_count);
+
+typedef struct jfh_generation_stats {
+    uint32_t completion_tokens;
+    uint32_t target_decode_passes;
+    uint32_t speculative_draft_tokens;
+    uint32_t speculative_accepted_tokens;
+    double time_to_first_token_ms;
+    double decode_ms;
+} jfh_generation_stats;
+
+/* GenerationRunner::run speculative loop (generation_runner.cpp:398-566) over
+ * the HIP stage executor: prefill, prompt-lookup drafts of up to draft_max
+ * tokens, one verify pass per draft, greedy acceptance, rollback, single-token
+ * recovery pass after a rejection. draft_max 0 disables speculation. */
+jfh_status jfh_generate(jfh_engine * engine, const int32_t * prompt, uint32_t n_prompt, uint32_t max_tokens,
+                        uint32_t draft_max, uint32_t max_ngram, uint32_t min_ngram, int32_t * out_tokens,
+                        uint32_t * out_count, jfh_generation_stats * stats);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

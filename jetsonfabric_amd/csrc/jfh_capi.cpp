@@ -1,0 +1,571 @@
+// C ABI of the HIP Qwen2 stage engine (declarations and reference mapping in include/jfh.h).
+#include "jfh.h"
+
+#include "jfh_engine.hpp"
+#include "jfh_runtime.hpp"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <new>
+
+struct jfh_model {
+    std::unique_ptr<jfh::HostModel> model;
+    std::vector<std::string> names;  // stable NUL-terminated copies for views
+    bool finalized = false;
+};
+
+struct jfh_engine {
+    std::shared_ptr<jfh::Engine> engine;
+};
+
+struct jfh_package {
+    std::unique_ptr<jfh::Package> package;
+};
+
+struct jfh_session {
+    jfh_engine* owner;
+    std::unique_ptr<jfh::Session> session;
+};
+
+namespace {
+
+jfh_status ok() {
+    jfh_status s{};
+    s.code = JFH_STATUS_OK;
+    return s;
+}
+
+jfh_status error(int32_t code, const char* message) {
+    jfh_status s{};
+    s.code = code;
+    std::snprintf(s.message, sizeof(s.message), "%s", message);
+    return s;
+}
+
+template <typename F>
+jfh_status guarded(F&& fn) {
+    try {
+        fn();
+        return ok();
+    } catch (const jfh::Error& e) {
+        return error(static_cast<int32_t>(e.code()), e.what());
+    } catch (const std::invalid_argument& e) {
+        return error(JFH_STATUS_INVALID_ARGUMENT, e.what());
+    } catch (const std::bad_alloc&) {
+        return error(JFH_STATUS_OUT_OF_MEMORY, "host allocation failed");
+    } catch (const std::exception& e) {
+        return error(JFH_STATUS_DEVICE_ERROR, e.what());
+    }
+}
+
+void require(bool condition, const char* message) {
+    if (!condition) throw jfh::Error(jfh::Status::InvalidArgument, message);
+}
+
+void fill_view(const jfh_model* m, size_t index, jfh_tensor_view* out) {
+    const jfh::TensorView& t = m->model->tensors()[index];
+    out->name = m->names[index].c_str();
+    out->type = t.type;
+    out->rank = t.rank;
+    for (int d = 0; d < 4; ++d) out->shape[d] = t.shape[d];
+    out->layer = t.layer;
+    out->data = t.data;
+    out->size = t.size;
+}
+
+void refresh_names(jfh_model* m) {
+    m->names.clear();
+    for (const jfh::TensorView& t : m->model->tensors()) m->names.push_back(t.name);
+    m->finalized = true;
+}
+
+jfh::ModelParams to_params(const jfh_model_params& p) {
+    jfh::ModelParams q;
+    q.n_layer = p.n_layer;
+    q.n_embd = p.n_embd;
+    q.n_ff = p.n_ff;
+    q.n_head = p.n_head;
+    q.n_head_kv = p.n_head_kv;
+    q.n_ctx = p.n_ctx;
+    q.n_vocab = p.n_vocab;
+    q.head_dim = p.n_head ? p.n_embd / p.n_head : 0;
+    q.rope_base = p.rope_base;
+    q.rms_eps = p.rms_eps;
+    return q;
+}
+
+}  // namespace
+
+extern "C" {
+
+jfh_status jfh_tensor_type_layout(uint32_t type, uint32_t* block_elements, uint32_t* block_bytes) {
+    if (!block_elements || !block_bytes) return error(JFH_STATUS_INVALID_ARGUMENT, "tensor layout outputs are required");
+    if (!jfh::type_layout(type, block_elements, block_bytes)) {
+        return error(JFH_STATUS_FORMAT_ERROR, "unsupported JFM tensor type");
+    }
+    return ok();
+}
+
+jfh_status jfh_sha256(const void* data, size_t size, uint8_t digest[32]) {
+    if ((!data && size) || !digest) return error(JFH_STATUS_INVALID_ARGUMENT, "data and digest are required");
+    const auto d = jfh::sha256(data, size);
+    std::memcpy(digest, d.data(), 32);
+    return ok();
+}
+
+jfh_status jfh_package_open(const char* package_path, uint32_t layer_start, uint32_t layer_end, uint32_t verify_hashes,
+                            jfh_package** out) {
+    return guarded([&] {
+        require(package_path && package_path[0] && out, "package path and output are required");
+        *out = nullptr;
+        jfh::StagePlan plan;
+        plan.layer_start = layer_start;
+        plan.layer_end = layer_end;
+        plan.verify_hashes = verify_hashes != 0;
+        auto p = std::make_unique<jfh_package>();
+        p->package = jfh::Package::open(package_path, plan);
+        *out = p.release();
+    });
+}
+
+void jfh_package_close(jfh_package* package) { delete package; }
+
+jfh_status jfh_package_get_stats(const jfh_package* package, jfh_package_stats* out) {
+    return guarded([&] {
+        require(package && out, "package and output are required");
+        const jfh::PackageStats& s = package->package->stats();
+        *out = jfh_package_stats{s.layer_start, s.layer_end, s.layer_count, 0, s.selected_weight_bytes,
+                                 s.total_weight_bytes, s.mapped_bytes, s.selected_tensor_count, s.total_tensor_count};
+    });
+}
+
+size_t jfh_package_tensor_count(const jfh_package* package) {
+    return package ? package->package->tensors().size() : 0;
+}
+
+namespace {
+void package_view(const jfh::TensorView& t, jfh_tensor_view* out) {
+    out->name = t.name.c_str();
+    out->type = t.type;
+    out->rank = t.rank;
+    for (int d = 0; d < 4; ++d) out->shape[d] = t.shape[d];
+    out->layer = t.layer;
+    out->data = t.data;
+    out->size = t.size;
+}
+}  // namespace
+
+jfh_status jfh_package_tensor_at(const jfh_package* package, size_t index, jfh_tensor_view* out) {
+    return guarded([&] {
+        require(package && out, "package and output are required");
+        const auto& tensors = package->package->tensors();
+        if (index >= tensors.size()) throw jfh::Error(jfh::Status::NotFound, "tensor index is out of range");
+        package_view(tensors[index], out);
+    });
+}
+
+jfh_status jfh_package_find_tensor(const jfh_package* package, const char* name, jfh_tensor_view* out) {
+    return guarded([&] {
+        require(package && name && out, "package, name and output are required");
+        const jfh::TensorView* t = package->package->find(name);
+        if (!t) throw jfh::Error(jfh::Status::NotFound, std::string("tensor not found: ") + name);
+        package_view(*t, out);
+    });
+}
+
+jfh_status jfh_package_gguf_metadata(const jfh_package* package, const void** data, size_t* size) {
+    return guarded([&] {
+        require(package && data && size, "package and outputs are required");
+        *data = package->package->gguf_metadata();
+        *size = package->package->gguf_metadata_size();
+        if (!*data) throw jfh::Error(jfh::Status::NotFound, "package has no GGUF metadata");
+    });
+}
+
+jfh_status jfh_package_source_sha256(const jfh_package* package, uint8_t digest[32]) {
+    return guarded([&] {
+        require(package && digest, "package and output are required");
+        std::memcpy(digest, package->package->source_sha256().data(), 32);
+    });
+}
+
+jfh_status jfh_model_open(const char* package_path, uint32_t layer_start, uint32_t layer_end, uint32_t verify_hashes,
+                          jfh_model** out) {
+    return guarded([&] {
+        require(package_path && out, "package path and output are required");
+        *out = nullptr;
+        jfh::StagePlan plan;
+        plan.layer_start = layer_start;
+        plan.layer_end = layer_end;
+        plan.verify_hashes = verify_hashes != 0;
+        auto m = std::make_unique<jfh_model>();
+        m->model = jfh::HostModel::open_package(package_path, plan);
+        refresh_names(m.get());
+        *out = m.release();
+    });
+}
+
+jfh_status jfh_model_synthesize(const jfh_synth_spec* spec, jfh_model** out) {
+    return guarded([&] {
+        require(spec && out, "spec and output are required");
+        *out = nullptr;
+        jfh::SynthSpec s;
+        s.params = to_params(spec->params);
+        s.type_linear = spec->type_linear;
+        s.type_embd = spec->type_embd;
+        s.type_output = spec->type_output;
+        s.tied_output = spec->tied_output != 0;
+        s.output_bias = spec->output_bias != 0;
+        s.seed = spec->seed;
+        s.stddev = spec->stddev;
+        s.threads = spec->threads;
+        auto m = std::make_unique<jfh_model>();
+        m->model = jfh::HostModel::synthesize(s);
+        refresh_names(m.get());
+        *out = m.release();
+    });
+}
+
+jfh_status jfh_model_create(const jfh_model_params* params, jfh_model** out) {
+    return guarded([&] {
+        require(params && out, "params and output are required");
+        require(params->n_head > 0 && params->n_embd % params->n_head == 0, "heads must divide the embedding");
+        *out = nullptr;
+        auto m = std::make_unique<jfh_model>();
+        m->model = jfh::HostModel::build(to_params(*params));
+        *out = m.release();
+    });
+}
+
+jfh_status jfh_model_add_tensor(jfh_model* model, const char* name, uint32_t type, uint32_t rank,
+                                const uint64_t* shape, const void* data, uint64_t size) {
+    return guarded([&] {
+        require(model && name && shape && (data || size == 0), "model, name, shape and data are required");
+        require(!model->finalized, "model is already finalized");
+        model->model->add_tensor(name, type, rank, shape, data, size);
+    });
+}
+
+jfh_status jfh_model_finalize(jfh_model* model) {
+    return guarded([&] {
+        require(model, "model is required");
+        require(!model->finalized, "model is already finalized");
+        model->model->finalize();
+        refresh_names(model);
+    });
+}
+
+jfh_status jfh_model_write_package(const jfh_model* model, const char* directory) {
+    return guarded([&] {
+        require(model && directory && model->finalized, "a finalized model and a directory are required");
+        model->model->write_package(directory);
+    });
+}
+
+void jfh_model_close(jfh_model* model) { delete model; }
+
+jfh_status jfh_model_get_params(const jfh_model* model, jfh_model_params* out) {
+    return guarded([&] {
+        require(model && out, "model and output are required");
+        const jfh::ModelParams& p = model->model->params();
+        out->n_layer = p.n_layer;
+        out->n_embd = p.n_embd;
+        out->n_ff = p.n_ff;
+        out->n_head = p.n_head;
+        out->n_head_kv = p.n_head_kv;
+        out->n_ctx = p.n_ctx;
+        out->n_vocab = p.n_vocab;
+        out->head_dim = p.head_dim;
+        out->rope_base = p.rope_base;
+        out->rms_eps = p.rms_eps;
+    });
+}
+
+jfh_status jfh_model_get_stats(const jfh_model* model, jfh_model_stats* out) {
+    return guarded([&] {
+        require(model && out && model->finalized, "a finalized model and an output are required");
+        const jfh::HostModel& m = *model->model;
+        out->layer_start = m.layer_start();
+        out->layer_end = m.layer_end();
+        out->layer_count = m.params().n_layer;
+        out->selected_weight_bytes = m.weight_bytes();
+        out->total_weight_bytes = m.weight_bytes();
+        out->selected_tensor_count = m.tensors().size();
+        out->total_tensor_count = m.tensors().size();
+    });
+}
+
+size_t jfh_model_tensor_count(const jfh_model* model) { return model ? model->names.size() : 0; }
+
+jfh_status jfh_model_tensor_at(const jfh_model* model, size_t index, jfh_tensor_view* out) {
+    return guarded([&] {
+        require(model && out && model->finalized, "a finalized model and an output are required");
+        if (index >= model->names.size()) throw jfh::Error(jfh::Status::NotFound, "tensor index is out of range");
+        fill_view(model, index, out);
+    });
+}
+
+jfh_status jfh_model_find_tensor(const jfh_model* model, const char* name, jfh_tensor_view* out) {
+    return guarded([&] {
+        require(model && name && out && model->finalized, "a finalized model, a name and an output are required");
+        for (size_t i = 0; i < model->names.size(); ++i) {
+            if (model->names[i] == name) {
+                fill_view(model, i, out);
+                return;
+            }
+        }
+        throw jfh::Error(jfh::Status::NotFound, std::string("tensor not found: ") + name);
+    });
+}
+
+jfh_status jfh_model_source_sha256(const jfh_model* model, char hex[65]) {
+    return guarded([&] {
+        require(model && hex && model->finalized, "a finalized model and an output are required");
+        const std::string h = model->model->source_sha256();
+        std::snprintf(hex, 65, "%s", h.c_str());
+    });
+}
+
+jfh_status jfh_engine_create(const jfh_model* model, const jfh_engine_options* options, jfh_engine** out) {
+    return guarded([&] {
+        require(model && out && model->finalized, "a finalized model and an output are required");
+        *out = nullptr;
+        jfh::EngineOptions o;
+        if (options) {
+            o.device = options->device;
+            o.use_graphs = options->use_graphs != 0;
+        }
+        auto e = std::make_unique<jfh_engine>();
+        e->engine = std::make_shared<jfh::Engine>(*model->model, o);
+        *out = e.release();
+    });
+}
+
+void jfh_engine_destroy(jfh_engine* engine) { delete engine; }
+
+jfh_status jfh_engine_get_info(const jfh_engine* engine, jfh_engine_info* out) {
+    return guarded([&] {
+        require(engine && out, "engine and output are required");
+        out->weight_bytes = engine->engine->weight_bytes();
+        out->prefill_chunk = engine->engine->max_prefill_chunk();
+        std::snprintf(out->device_name, sizeof(out->device_name), "%s", engine->engine->device_name().c_str());
+    });
+}
+
+jfh_status jfh_session_create(jfh_engine* engine, uint32_t capacity, jfh_session** out) {
+    return guarded([&] {
+        require(engine && out, "engine and output are required");
+        *out = nullptr;
+        auto s = std::make_unique<jfh_session>();
+        s->owner = engine;
+        s->session = engine->engine->create_session(capacity);
+        *out = s.release();
+    });
+}
+
+void jfh_session_destroy(jfh_session* session) { delete session; }
+
+uint32_t jfh_session_capacity(const jfh_session* session) { return session ? session->session->capacity() : 0; }
+
+uint32_t jfh_session_position(const jfh_session* session) { return session ? session->session->position() : 0; }
+
+jfh_status jfh_session_prefill(jfh_session* session, const int32_t* tokens, uint32_t n, int32_t* out_token,
+                               float* logits) {
+    return guarded([&] {
+        require(session && tokens && out_token, "session, tokens and output are required");
+        *out_token = session->owner->engine->prefill(*session->session, tokens, n, logits);
+    });
+}
+
+jfh_status jfh_session_decode(jfh_session* session, int32_t token, int32_t* out_token, float* logits) {
+    return guarded([&] {
+        require(session && out_token, "session and output are required");
+        jfh::Session& s = *session->session;
+        // qwen2_architecture.cpp:1050-1054
+        if (s.position() == 0 || s.position() >= s.capacity()) {
+            throw jfh::Error(jfh::Status::InvalidArgument, "native Qwen2 decode is outside session capacity");
+        }
+        jfh::SeqStep st;
+        st.session = &s;
+        st.tokens = &token;
+        st.n = 1;
+        st.logits = 1;
+        session->owner->engine->forward({st}, out_token, nullptr, logits);
+    });
+}
+
+jfh_status jfh_session_verify(jfh_session* session, const int32_t* tokens, uint32_t n, int32_t* out_tokens,
+                              uint32_t* out_accepted, float* logits) {
+    return guarded([&] {
+        require(session && tokens && out_tokens && n > 0, "session, tokens and outputs are required");
+        jfh::Session& s = *session->session;
+        if (s.position() == 0) throw jfh::Error(jfh::Status::InvalidArgument, "verification requires a prefilled session");
+        jfh::SeqStep st;
+        st.session = &s;
+        st.tokens = tokens;
+        st.n = n;
+        st.logits = 2;
+        int32_t accepted = 0;
+        session->owner->engine->forward({st}, out_tokens, &accepted, logits);
+        if (out_accepted) *out_accepted = static_cast<uint32_t>(accepted);
+    });
+}
+
+jfh_status jfh_session_rollback(jfh_session* session, uint32_t n) {
+    return guarded([&] {
+        require(session, "session is required");
+        session->session->rollback(n);
+    });
+}
+
+jfh_status jfh_engine_step_batch(jfh_engine* engine, jfh_session* const* sessions, uint32_t count,
+                                 const int32_t* tokens, const uint32_t* lengths, int32_t* out_tokens,
+                                 uint32_t* out_accepted) {
+    return guarded([&] {
+        require(engine && sessions && tokens && lengths && out_tokens && count > 0, "batch arguments are required");
+        std::vector<jfh::SeqStep> steps;
+        size_t offset = 0;
+        for (uint32_t i = 0; i < count; ++i) {
+            require(sessions[i] && sessions[i]->owner == engine, "session does not belong to this engine");
+            require(sessions[i]->session->position() > 0, "batched steps require prefilled sessions");
+            jfh::SeqStep st;
+            st.session = sessions[i]->session.get();
+            st.tokens = tokens + offset;
+            st.n = lengths[i];
+            st.logits = lengths[i] > 1 ? 2 : 1;
+            offset += lengths[i];
+            steps.push_back(st);
+        }
+        std::vector<int32_t> accepted(count);
+        engine->engine->forward(steps, out_tokens, accepted.data(), nullptr);
+        if (out_accepted) {
+            for (uint32_t i = 0; i < count; ++i) out_accepted[i] = static_cast<uint32_t>(accepted[i]);
+        }
+    });
+}
+
+jfh_status jfh_engine_dequantize(jfh_engine* engine, const char* tensor, uint32_t row0, uint32_t n_rows, float* out) {
+    return guarded([&] {
+        require(engine && tensor && out, "engine, tensor and output are required");
+        engine->engine->dequantize(tensor, row0, n_rows, out);
+    });
+}
+
+jfh_status jfh_engine_matmul(jfh_engine* engine, const char* tensor, const float* x, uint32_t n_tok, float* y) {
+    return guarded([&] {
+        require(engine && tensor && x && y, "engine, tensor and buffers are required");
+        engine->engine->matmul(tensor, x, n_tok, y);
+    });
+}
+
+jfh_status jfh_session_time_steps(jfh_session* session, const int32_t* tokens, uint32_t n, uint32_t all_logits,
+                                  uint32_t warmup, uint32_t iterations, double* ms_per_step) {
+    return guarded([&] {
+        require(session && tokens && ms_per_step && n > 0 && iterations > 0, "timing arguments are required");
+        jfh::Engine& e = *session->owner->engine;
+        jfh::Session& s = *session->session;
+        require(s.position() > 0, "timing requires a prefilled session");
+        jfh::SeqStep st;
+        st.session = &s;
+        st.tokens = tokens;
+        st.n = n;
+        st.logits = all_logits ? 2 : 1;
+        std::vector<int32_t> ids(n);
+        for (uint32_t i = 0; i < warmup; ++i) {
+            e.forward({st}, ids.data(), nullptr, nullptr);
+            s.rollback(n);
+        }
+        hipEvent_t a, b;
+        if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) {
+            throw jfh::Error(jfh::Status::DeviceError, "create timing events");
+        }
+        (void) hipEventRecord(a, e.stream());
+        for (uint32_t i = 0; i < iterations; ++i) {
+            e.forward({st}, ids.data(), nullptr, nullptr);
+            s.rollback(n);
+        }
+        (void) hipEventRecord(b, e.stream());
+        (void) hipEventSynchronize(b);
+        float ms = 0.0F;
+        (void) hipEventElapsedTime(&ms, a, b);
+        (void) hipEventDestroy(a);
+        (void) hipEventDestroy(b);
+        *ms_per_step = static_cast<double>(ms) / iterations;
+    });
+}
+
+jfh_status jfh_session_profile_step(jfh_session* session, const int32_t* tokens, uint32_t n, uint32_t all_logits,
+                                    uint32_t iterations, jfh_kernel_stat* out, uint32_t capacity, uint32_t* count) {
+    return guarded([&] {
+        require(session && tokens && out && count && n > 0 && iterations > 0, "profile arguments are required");
+        require(session->session->position() > 0, "profiling requires a prefilled session");
+        jfh::SeqStep st;
+        st.session = session->session.get();
+        st.tokens = tokens;
+        st.n = n;
+        st.logits = all_logits ? 2 : 1;
+        const std::vector<jfh::KernelStat> stats = session->owner->engine->profile({st}, iterations);
+        const uint32_t k = std::min<uint32_t>(capacity, static_cast<uint32_t>(stats.size()));
+        for (uint32_t i = 0; i < k; ++i) {
+            std::snprintf(out[i].label, sizeof(out[i].label), "%s", stats[i].label.c_str());
+            out[i].launches = stats[i].launches;
+            out[i].total_ms = stats[i].total_ms;
+            out[i].bytes = stats[i].bytes;
+        }
+        *count = k;
+    });
+}
+
+jfh_status jfh_prompt_lookup_propose(const uint32_t* history, size_t n, uint32_t max_ngram, uint32_t min_ngram,
+                                     uint32_t max_tokens, uint32_t* out, uint32_t* out_count) {
+    return guarded([&] {
+        require((history || n == 0) && out_count && (out || max_tokens == 0), "history and outputs are required");
+        jfh::runtime::speculative::PromptLookupDraft draft(max_ngram, min_ngram);
+        const std::vector<uint32_t> h(history, history + n);
+        const std::vector<uint32_t> p = draft.propose(h, max_tokens);
+        std::copy(p.begin(), p.end(), out);
+        *out_count = static_cast<uint32_t>(p.size());
+    });
+}
+
+jfh_status jfh_generate(jfh_engine* engine, const int32_t* prompt, uint32_t n_prompt, uint32_t max_tokens,
+                        uint32_t draft_max, uint32_t max_ngram, uint32_t min_ngram, int32_t* out_tokens,
+                        uint32_t* out_count, jfh_generation_stats* stats) {
+    return guarded([&] {
+        require(engine && prompt && n_prompt > 0 && max_tokens > 0 && out_tokens && out_count, "generation arguments are required");
+        require(draft_max <= 8, "draft length must be 0..8");
+        namespace rt = jfh::runtime;
+        const jfh::ModelParams& p = engine->engine->params();
+        rt::adapters::HipStageConfig cfg;
+        cfg.engine = engine->engine;
+        cfg.tokenizer = std::make_shared<rt::tokenization::IdTokenizer>();
+        cfg.ctx_size = static_cast<int>(std::min<uint64_t>(p.n_ctx, static_cast<uint64_t>(n_prompt) + max_tokens));
+        cfg.position = {0, 1};
+        cfg.layers = {0, static_cast<int>(p.n_layer)};
+        cfg.speculative_max_tokens = static_cast<int>(draft_max);
+        rt::adapters::HipStageExecutor executor(cfg);
+        std::unique_ptr<rt::speculative::PromptLookupDraft> draft;
+        if (draft_max > 0) draft = std::make_unique<rt::speculative::PromptLookupDraft>(max_ngram, min_ngram);
+        rt::GenerationRequest req;
+        req.prompt.assign(prompt, prompt + n_prompt);
+        req.max_tokens = static_cast<int>(max_tokens);
+        req.layer_count = static_cast<int>(p.n_layer);
+        const rt::GenerationResult r = rt::run_generation(executor, req, draft.get(), static_cast<int>(draft_max));
+        if (!r.ok) throw jfh::Error(jfh::Status::InvalidArgument, r.error_code + ": " + r.error_message);
+        for (size_t i = 0; i < r.sampled_tokens.size(); ++i) out_tokens[i] = static_cast<int32_t>(r.sampled_tokens[i]);
+        *out_count = static_cast<uint32_t>(r.sampled_tokens.size());
+        if (stats) {
+            stats->completion_tokens = static_cast<uint32_t>(r.completion_tokens);
+            stats->target_decode_passes = static_cast<uint32_t>(r.target_decode_passes);
+            stats->speculative_draft_tokens = static_cast<uint32_t>(r.speculative_draft_tokens);
+            stats->speculative_accepted_tokens = static_cast<uint32_t>(r.speculative_accepted_tokens);
+            stats->time_to_first_token_ms = r.time_to_first_token_ms;
+            stats->decode_ms = r.decode_ms;
+        }
+    });
+}
+
+}  // extern "C"

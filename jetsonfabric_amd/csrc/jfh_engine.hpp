@@ -1,0 +1,176 @@
+// HIP Qwen2 stage engine: device-resident weights, sessions owning F16 KV
+// caches, and batched forward steps (prefill chunks, decode, draft verify).
+//
+// Replaces the reference's Qwen2Architecture/Qwen2Session/ForwardGraph
+// (runtime/engines/native/src/qwen2_architecture.cpp:120-1212) and
+// TensorStore (tensor_store.cpp:57-196) for one GPU holding every layer.
+#pragma once
+
+#include "jfh_kernels.hpp"
+#include "jfh_model.hpp"
+
+#include <hip/hip_runtime_api.h>
+
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace jfh {
+
+struct EngineOptions {
+    int device = 0;
+    bool use_graphs = true;
+};
+
+class Engine;
+
+// KV-cache owner; position bookkeeping follows Qwen2Session
+// (qwen2_architecture.cpp:800-823, 1040-1054).
+class Session {
+public:
+    ~Session();
+    Session(const Session&) = delete;
+    Session& operator=(const Session&) = delete;
+
+    uint32_t capacity() const { return capacity_; }
+    uint32_t position() const { return position_; }
+    uint32_t prefill_position() const { return prefill_position_; }
+    void rollback(uint32_t n);
+    uint64_t kv_bytes() const { return kv_bytes_; }
+
+private:
+    friend class Engine;
+    Session(Engine* engine, uint32_t capacity);
+
+    Engine* engine_;
+    uint32_t capacity_;
+    uint32_t position_ = 0;
+    uint32_t prefill_position_ = 0;
+    uint16_t* k_ = nullptr;
+    uint16_t* v_ = nullptr;
+    uint64_t kv_bytes_ = 0;
+};
+
+// One sequence's share of a batched step.
+struct SeqStep {
+    Session* session = nullptr;
+    const int32_t* tokens = nullptr;
+    uint32_t n = 0;
+    // 0: no logits, 1: last row, 2: every row (draft verify)
+    int logits = 1;
+};
+
+// Per-kernel device time of one step, measured with HIP events around every
+// launch of an un-graphed step (averaged over iterations).
+struct KernelStat {
+    std::string label;
+    double launches = 0.0;   // launches per step
+    double total_ms = 0.0;   // device ms per step
+    double bytes = 0.0;      // algorithmic HBM bytes per step
+};
+
+class Engine {
+public:
+    Engine(const HostModel& model, const EngineOptions& options);
+    ~Engine();
+    Engine(const Engine&) = delete;
+    Engine& operator=(const Engine&) = delete;
+
+    const ModelParams& params() const { return params_; }
+    uint64_t weight_bytes() const { return weight_bytes_; }
+    hipStream_t stream() const { return stream_; }
+    const std::string& device_name() const { return device_name_; }
+
+    std::unique_ptr<Session> create_session(uint32_t capacity);
+
+    // Runs token rows for several sessions in one pass. Positions advance by
+    // each sequence's row count. out_tokens receives one greedy id per logits
+    // row (sequence order); accepted (optional) one accepted-draft count per
+    // sequence; logits (optional) n_logits_rows x vocab floats.
+    void forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int32_t* accepted, float* logits);
+
+    // Prefill of arbitrary length: runs the prompt in chunks and returns the
+    // greedy token of the last row (and its logits if requested).
+    int32_t prefill(Session& s, const int32_t* tokens, uint32_t n, float* logits);
+
+    // Parity entry points: dequantize rows of a device tensor; multiply a
+    // device matrix with host activations through the same kernels.
+    void dequantize(const std::string& name, uint32_t row0, uint32_t n_rows, float* out_host);
+    void matmul(const std::string& name, const float* x_host, uint32_t n_tok, float* y_host);
+
+    // Runs the step `iterations` times without graphs, timing every kernel
+    // launch; sessions are restored to their starting positions.
+    std::vector<KernelStat> profile(const std::vector<SeqStep>& steps, uint32_t iterations);
+
+    uint32_t max_prefill_chunk() const { return prefill_chunk_; }
+
+private:
+    friend class Session;
+    struct DeviceTensor {
+        gpu::DMat mat;
+        void* main = nullptr;
+        void* aux = nullptr;
+        void* bias_alloc = nullptr;
+        uint64_t bytes = 0;
+    };
+    struct Layer {
+        const DeviceTensor *q, *k, *v, *o, *gate, *up, *down;
+        const float *attn_norm, *ffn_norm, *bq, *bk, *bv;
+    };
+
+    const DeviceTensor& upload(const TensorView& t);
+    const float* upload_f32(const TensorView& t);
+    void ensure_capacity(uint32_t capacity);
+    void record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_out, bool store_logits);
+    template <typename F>
+    void timed(const std::string& label, double bytes, F&& fn);
+
+    struct ProfEvent {
+        std::string label;
+        double bytes = 0.0;
+        hipEvent_t begin = nullptr;
+        hipEvent_t end = nullptr;
+    };
+    std::vector<ProfEvent>* prof_ = nullptr;
+    void* device_alloc(size_t bytes);
+
+    ModelParams params_;
+    EngineOptions options_;
+    std::string device_name_;
+    hipStream_t stream_ = nullptr;
+    std::map<std::string, DeviceTensor> tensors_;
+    std::vector<void*> allocations_;
+    std::vector<Layer> layers_;
+    const DeviceTensor* embd_ = nullptr;
+    const DeviceTensor* output_ = nullptr;
+    const float* output_norm_ = nullptr;
+    uint64_t weight_bytes_ = 0;
+    bool quantized_act_ = true;
+    uint32_t prefill_chunk_ = 8;
+
+    // workspace
+    int32_t kmax_ = 0;
+    float* h_ = nullptr;
+    gpu::Act act_{};
+    float* qkv_ = nullptr;
+    float* q_ = nullptr;
+    float* ffn_ = nullptr;
+    float* logits_ = nullptr;
+    unsigned long long* best_ = nullptr;
+    gpu::StepDev* step_dev_ = nullptr;
+    gpu::StepOut* out_dev_ = nullptr;
+    gpu::StepDev* step_host_ = nullptr;  // pinned
+    gpu::StepOut* out_host_ = nullptr;   // pinned
+    float* partial_ = nullptr;
+    float* rope_ = nullptr;
+    uint32_t capacity_max_ = 0;
+    int32_t max_chunks_ = 0;
+
+    // captured step graphs keyed by (rows, seqs, outs, store_logits)
+    std::map<uint64_t, hipGraphExec_t> graphs_;
+    std::mutex mutex_;
+};
+
+}  // namespace jfh

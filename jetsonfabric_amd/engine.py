@@ -1,0 +1,427 @@
+"""Python face of the HIP Qwen2 stage engine.
+
+Mirrors the reference's native engine facade
+(runtime/engines/native/include/jetsonfabric/native_inference.hpp:98-160):
+``NativeEngine`` (load, ``logits``, ``forced_decode_logits``, ``generate``,
+``create_session``) and ``NativeSession`` (``prefill_greedy``,
+``decode_greedy``, ``rollback``), plus the draft verification and batched
+steps the speculative decoder needs. Every call goes through libjfh.so.
+"""
+from __future__ import annotations
+
+import ctypes
+import time
+from dataclasses import dataclass, field
+from typing import Iterable, Sequence
+
+import numpy as np
+
+from . import _capi
+from ._capi import F16, F32, Q2_K, Q4_K, Q6_K, Q8_0, check, library
+
+__all__ = [
+    "F32", "F16", "Q8_0", "Q2_K", "Q4_K", "Q6_K",
+    "ModelConfig", "Model", "NativeEngine", "NativeSession", "GenerationResult", "prompt_lookup_propose",
+    "type_layout", "sha256",
+]
+
+
+@dataclass
+class ModelConfig:
+    """Qwen2 hyper-parameters (qwen2_metadata.hpp:10-18)."""
+
+    n_layer: int
+    n_embd: int
+    n_ff: int
+    n_head: int
+    n_head_kv: int
+    n_vocab: int
+    n_ctx: int = 32768
+    rope_base: float = 1.0e6
+    rms_eps: float = 1.0e-6
+
+    @property
+    def head_dim(self) -> int:
+        return self.n_embd // self.n_head
+
+    def to_c(self) -> _capi.ModelParams:
+        return _capi.ModelParams(self.n_layer, self.n_embd, self.n_ff, self.n_head, self.n_head_kv, self.n_ctx,
+                                 self.n_vocab, self.head_dim, self.rope_base, self.rms_eps)
+
+    @staticmethod
+    def from_c(p: _capi.ModelParams) -> "ModelConfig":
+        return ModelConfig(p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_head_kv, p.n_vocab, p.n_ctx, p.rope_base,
+                           p.rms_eps)
+
+
+def type_layout(type_id: int) -> tuple[int, int]:
+    e, b = ctypes.c_uint32(), ctypes.c_uint32()
+    check(library().jfh_tensor_type_layout(type_id, ctypes.byref(e), ctypes.byref(b)))
+    return e.value, b.value
+
+
+def sha256(data: bytes) -> bytes:
+    out = (ctypes.c_uint8 * 32)()
+    buf = ctypes.create_string_buffer(bytes(data), len(data))
+    check(library().jfh_sha256(buf, len(data), out))
+    return bytes(out)
+
+
+class Package:
+    """A JFM v2 package opened for a layer range (jf_model_open, engine.h:106-150)."""
+
+    def __init__(self, path: str, layer_start: int = 0, layer_end: int = 0xFFFFFFFF, verify_hashes: bool = True):
+        h = ctypes.c_void_p()
+        check(library().jfh_package_open(path.encode(), layer_start, layer_end, int(verify_hashes), ctypes.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if self._h:
+            library().jfh_package_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def stats(self) -> dict:
+        s = _capi.PackageStats()
+        check(library().jfh_package_get_stats(self._h, ctypes.byref(s)))
+        return {f: getattr(s, f) for f, _ in _capi.PackageStats._fields_ if f != "pad"}
+
+    def tensors(self) -> dict:
+        """name -> (type, shape, bytes), sorted by name."""
+        lib = library()
+        out = {}
+        for i in range(lib.jfh_package_tensor_count(self._h)):
+            v = _capi.TensorView()
+            check(lib.jfh_package_tensor_at(self._h, i, ctypes.byref(v)))
+            out[v.name.decode()] = (int(v.type), tuple(int(v.shape[d]) for d in range(v.rank)),
+                                    ctypes.string_at(v.data, v.size))
+        return out
+
+    def gguf_metadata(self) -> bytes:
+        data, size = ctypes.c_void_p(), ctypes.c_size_t()
+        check(library().jfh_package_gguf_metadata(self._h, ctypes.byref(data), ctypes.byref(size)))
+        return ctypes.string_at(data, size.value)
+
+    def source_sha256(self) -> bytes:
+        out = (ctypes.c_uint8 * 32)()
+        check(library().jfh_package_source_sha256(self._h, out))
+        return bytes(out)
+
+
+class Model:
+    """Host-resident model: a JFM v2 package, synthetic weights, or tensors added one by one."""
+
+    def __init__(self, handle: int):
+        self._h = ctypes.c_void_p(handle)
+
+    @classmethod
+    def open(cls, package: str, layer_start: int = 0, layer_end: int = 0xFFFFFFFF, verify_hashes: bool = True) -> "Model":
+        h = ctypes.c_void_p()
+        check(library().jfh_model_open(package.encode(), layer_start, layer_end, int(verify_hashes), ctypes.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def synthesize(cls, config: ModelConfig, type_linear: int = Q4_K, type_embd: int = Q4_K, type_output: int = Q6_K,
+                   tied_output: bool = False, output_bias: bool = False, seed: int = 1234, stddev: float = 0.02,
+                   threads: int = 0) -> "Model":
+        spec = _capi.SynthSpec(config.to_c(), type_linear, type_embd, type_output, int(tied_output), int(output_bias),
+                               0, seed, stddev, threads)
+        h = ctypes.c_void_p()
+        check(library().jfh_model_synthesize(ctypes.byref(spec), ctypes.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def build(cls, config: ModelConfig, tensors: Iterable[tuple[str, int, Sequence[int], bytes]]) -> "Model":
+        """tensors: (name, type, GGML shape ne0.., raw bytes)."""
+        h = ctypes.c_void_p()
+        lib = library()
+        params = config.to_c()
+        check(lib.jfh_model_create(ctypes.byref(params), ctypes.byref(h)))
+        model = cls(h.value)
+        for name, type_id, shape, data in tensors:
+            dims = (ctypes.c_uint64 * 4)(*list(shape) + [1] * (4 - len(shape)))
+            buf = ctypes.create_string_buffer(bytes(data), len(data))
+            check(lib.jfh_model_add_tensor(model._h, name.encode(), type_id, len(shape), dims, buf, len(data)))
+        check(lib.jfh_model_finalize(model._h))
+        return model
+
+    def close(self) -> None:
+        if self._h:
+            library().jfh_model_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    @property
+    def config(self) -> ModelConfig:
+        p = _capi.ModelParams()
+        check(library().jfh_model_get_params(self._h, ctypes.byref(p)))
+        return ModelConfig.from_c(p)
+
+    def stats(self) -> dict:
+        s = _capi.ModelStats()
+        check(library().jfh_model_get_stats(self._h, ctypes.byref(s)))
+        return {f: getattr(s, f) for f, _ in _capi.ModelStats._fields_}
+
+    def source_sha256(self) -> str:
+        buf = (ctypes.c_char * 65)()
+        check(library().jfh_model_source_sha256(self._h, buf))
+        return buf.value.decode()
+
+    def tensor_names(self) -> list[str]:
+        lib = library()
+        out = []
+        for i in range(lib.jfh_model_tensor_count(self._h)):
+            v = _capi.TensorView()
+            check(lib.jfh_model_tensor_at(self._h, i, ctypes.byref(v)))
+            out.append(v.name.decode())
+        return out
+
+    def tensor(self, name: str) -> dict:
+        """View of a tensor: type, shape (ne0, ne1, ...), data pointer and a bytes copy accessor."""
+        v = _capi.TensorView()
+        check(library().jfh_model_find_tensor(self._h, name.encode(), ctypes.byref(v)))
+        shape = tuple(int(v.shape[d]) for d in range(v.rank))
+        return {"name": name, "type": int(v.type), "shape": shape, "layer": int(v.layer), "data": int(v.data),
+                "size": int(v.size)}
+
+    def tensor_bytes(self, name: str) -> bytes:
+        t = self.tensor(name)
+        return ctypes.string_at(t["data"], t["size"])
+
+    def write_package(self, directory: str) -> None:
+        check(library().jfh_model_write_package(self._h, directory.encode()))
+
+
+@dataclass
+class GenerationResult:
+    """Result of a generation run (native_inference.hpp:88-96 plus speculation counters)."""
+
+    sampled_tokens: list[int]
+    time_to_first_token_ms: float = 0.0
+    decode_ms: float = 0.0
+    target_decode_passes: int = 0
+    speculative_draft_tokens: int = 0
+    speculative_accepted_tokens: int = 0
+    extra: dict = field(default_factory=dict)
+
+
+def _i32(values: Sequence[int]):
+    arr = (ctypes.c_int32 * max(1, len(values)))(*values)
+    return arr
+
+
+class NativeSession:
+    """One sequence: F16 KV cache on the device plus its position (native_inference.hpp:98-124)."""
+
+    def __init__(self, engine: "NativeEngine", handle: int):
+        self._engine = engine
+        self._h = ctypes.c_void_p(handle)
+
+    def close(self) -> None:
+        if self._h:
+            library().jfh_session_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    def capacity(self) -> int:
+        return int(library().jfh_session_capacity(self._h))
+
+    def position(self) -> int:
+        return int(library().jfh_session_position(self._h))
+
+    def prefill_greedy(self, tokens: Sequence[int], logits: bool = False):
+        out = ctypes.c_int32()
+        buf = np.zeros(self._engine.vocab, dtype=np.float32) if logits else None
+        ptr = buf.ctypes.data_as(ctypes.POINTER(ctypes.c_float)) if logits else None
+        check(library().jfh_session_prefill(self._h, _i32(tokens), len(tokens), ctypes.byref(out), ptr))
+        return (out.value, buf) if logits else out.value
+
+    def decode_greedy(self, token: int, logits: bool = False):
+        out = ctypes.c_int32()
+        buf = np.zeros(self._engine.vocab, dtype=np.float32) if logits else None
+        ptr = buf.ctypes.data_as(ctypes.POINTER(ctypes.c_float)) if logits else None
+        check(library().jfh_session_decode(self._h, token, ctypes.byref(out), ptr))
+        return (out.value, buf) if logits else out.value
+
+    def verify(self, tokens: Sequence[int], logits: bool = False):
+        """Decodes [previous, draft...] in one pass: greedy id after every row + accepted draft prefix."""
+        n = len(tokens)
+        out = (ctypes.c_int32 * n)()
+        acc = ctypes.c_uint32()
+        buf = np.zeros((n, self._engine.vocab), dtype=np.float32) if logits else None
+        ptr = buf.ctypes.data_as(ctypes.POINTER(ctypes.c_float)) if logits else None
+        check(library().jfh_session_verify(self._h, _i32(tokens), n, out, ctypes.byref(acc), ptr))
+        ids = [int(x) for x in out]
+        return (ids, int(acc.value), buf) if logits else (ids, int(acc.value))
+
+    def rollback(self, token_count: int) -> None:
+        check(library().jfh_session_rollback(self._h, token_count))
+
+    def time_steps(self, tokens: Sequence[int], iterations: int, warmup: int = 2, all_logits: bool | None = None) -> float:
+        """Mean device ms per step of `tokens` at the current position (rolled back after each step)."""
+        ms = ctypes.c_double()
+        if all_logits is None:
+            all_logits = len(tokens) > 1
+        check(library().jfh_session_time_steps(self._h, _i32(tokens), len(tokens), int(all_logits), warmup,
+                                               iterations, ctypes.byref(ms)))
+        return ms.value
+
+    def profile_step(self, tokens: Sequence[int], iterations: int = 3, all_logits: bool | None = None) -> list[dict]:
+        """Per-kernel device time and algorithmic bytes of one step (HIP events per launch)."""
+        if all_logits is None:
+            all_logits = len(tokens) > 1
+        cap = 64
+        out = (_capi.KernelStat * cap)()
+        count = ctypes.c_uint32()
+        check(library().jfh_session_profile_step(self._h, _i32(tokens), len(tokens), int(all_logits), iterations, out,
+                                                 cap, ctypes.byref(count)))
+        return [{"kernel": out[i].label.decode(), "launches": out[i].launches, "ms": out[i].total_ms,
+                 "bytes": out[i].bytes} for i in range(count.value)]
+
+
+class NativeEngine:
+    """Device-resident Qwen2 weights and the step kernels (native_inference.hpp:126-160)."""
+
+    def __init__(self, model: Model, device: int = 0, use_graphs: bool = True):
+        opts = _capi.EngineOptions(device, int(use_graphs))
+        h = ctypes.c_void_p()
+        start = time.perf_counter()
+        check(library().jfh_engine_create(model.handle, ctypes.byref(opts), ctypes.byref(h)))
+        self.load_time_ms = (time.perf_counter() - start) * 1e3
+        self._h = h
+        self._config = model.config
+        self.vocab = self._config.n_vocab
+        info = _capi.EngineInfo()
+        check(library().jfh_engine_get_info(self._h, ctypes.byref(info)))
+        self.weight_bytes = int(info.weight_bytes)
+        self.prefill_chunk = int(info.prefill_chunk)
+        self.device_name = info.device_name.decode()
+
+    def close(self) -> None:
+        if self._h:
+            library().jfh_engine_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    def model_info(self) -> ModelConfig:
+        return self._config
+
+    def create_session(self, capacity: int) -> NativeSession:
+        h = ctypes.c_void_p()
+        check(library().jfh_session_create(self._h, capacity, ctypes.byref(h)))
+        return NativeSession(self, h.value)
+
+    def step_batch(self, sessions: Sequence[NativeSession], token_rows: Sequence[Sequence[int]]):
+        """One pass over several sessions; returns (ids per session, accepted per session)."""
+        count = len(sessions)
+        handles = (ctypes.c_void_p * count)(*[s.handle.value for s in sessions])
+        flat = [t for row in token_rows for t in row]
+        lengths = (ctypes.c_uint32 * count)(*[len(r) for r in token_rows])
+        out = (ctypes.c_int32 * len(flat))()
+        acc = (ctypes.c_uint32 * count)()
+        check(library().jfh_engine_step_batch(self._h, handles, count, _i32(flat), lengths, out, acc))
+        ids, o = [], 0
+        for row in token_rows:
+            ids.append([int(x) for x in out[o:o + len(row)]])
+            o += len(row)
+        return ids, [int(a) for a in acc]
+
+    def logits(self, tokens: Sequence[int]) -> np.ndarray:
+        """Last-row logits of a fresh prefill (NativeEngine::logits, native_inference.cpp:396-411)."""
+        s = self.create_session(len(tokens))
+        try:
+            _, out = s.prefill_greedy(tokens, logits=True)
+            return out
+        finally:
+            s.close()
+
+    def forced_decode_logits(self, prompt: Sequence[int], forced: Sequence[int]) -> list[np.ndarray]:
+        """Prefill logits, then one decode per forced token (native_inference.cpp:413-441)."""
+        s = self.create_session(len(prompt) + len(forced))
+        try:
+            trace = [s.prefill_greedy(prompt, logits=True)[1]]
+            for t in forced:
+                trace.append(s.decode_greedy(t, logits=True)[1])
+            return trace
+        finally:
+            s.close()
+
+    def dequantize_rows(self, tensor: str, row0: int, n_rows: int, cols: int) -> np.ndarray:
+        out = np.zeros((n_rows, cols), dtype=np.float32)
+        check(library().jfh_engine_dequantize(self._h, tensor.encode(), row0, n_rows,
+                                              out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+        return out
+
+    def matmul(self, tensor: str, x: np.ndarray, rows: int) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim == 1:
+            x = x[None, :]
+        y = np.zeros((x.shape[0], rows), dtype=np.float32)
+        check(library().jfh_engine_matmul(self._h, tensor.encode(), x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                          x.shape[0], y.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+        return y
+
+    def generate(self, prompt: Sequence[int], max_tokens: int, draft_max: int = 0, max_ngram: int = 4,
+                 min_ngram: int = 2) -> GenerationResult:
+        """GenerationRunner loop over the HIP stage executor (generation_runner.cpp:398-566)."""
+        out = (ctypes.c_int32 * max_tokens)()
+        count = ctypes.c_uint32()
+        stats = _capi.GenerationStats()
+        check(library().jfh_generate(self._h, _i32(prompt), len(prompt), max_tokens, draft_max, max_ngram, min_ngram,
+                                     out, ctypes.byref(count), ctypes.byref(stats)))
+        return GenerationResult(
+            sampled_tokens=[int(x) for x in out[:count.value]],
+            time_to_first_token_ms=stats.time_to_first_token_ms,
+            decode_ms=stats.decode_ms,
+            target_decode_passes=int(stats.target_decode_passes),
+            speculative_draft_tokens=int(stats.speculative_draft_tokens),
+            speculative_accepted_tokens=int(stats.speculative_accepted_tokens),
+        )
+
+
+def prompt_lookup_propose(history: Sequence[int], max_tokens: int, max_ngram: int = 4, min_ngram: int = 2) -> list[int]:
+    """PromptLookupDraft::propose through the C ABI (prompt_lookup_draft.cpp:15-44)."""
+    hist = (ctypes.c_uint32 * max(1, len(history)))(*history)
+    out = (ctypes.c_uint32 * max(1, max_tokens))()
+    n = ctypes.c_uint32()
+    check(library().jfh_prompt_lookup_propose(hist, len(history), max_ngram, min_ngram, max_tokens, out,
+                                              ctypes.byref(n)))
+    return [int(x) for x in out[:n.value]]

@@ -1,0 +1,361 @@
+/*
+ * jfo_forward.c -- CPU restatement of the native Qwen2 stage forward.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker); see jfo.h.
+ *
+ * Follows runtime/engines/native/src/qwen2_architecture.cpp op for op:
+ *   embedding get_rows (564-568) -> per layer [rms_norm*gain (373-376),
+ *   q/k/v linear + bias (394-396), NEOX rope on q and k (401-402, 499-506),
+ *   K/V rows written to the F16 cache at the step's positions (405-424),
+ *   causal attention softmax(q.k * hd^-1/2 + mask) v over the cache
+ *   (438-464, mask 697-708), output linear (469), residual add (573),
+ *   rms_norm*gain, up/gate linear, silu(gate)*up, down linear (508-520),
+ *   residual add (576)] -> rows selected for output (584) -> output norm ->
+ *   head linear (+ bias if present, 378-384) -> argmax (594).
+ * Float rounding points kept from the reference: K/V are stored as binary16;
+ * rms_norm scale is 1/sqrtf(mean + eps) applied as (x*scale)*gain; the
+ * attention scale is 1/sqrtf(head_dim) in float; silu(x) = x/(1+expf(-x)).
+ * Accumulations are in double, which is more precise than the reference.
+ */
+#include "jfo.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+struct jfo_session {
+    const jfo_model * m;
+    int32_t capacity;
+    int32_t mode;
+    int32_t threads;
+    int32_t pos;
+    int32_t prefill_pos;
+    int32_t head_dim;
+    uint16_t * k; /* [layer][kv_head][capacity][head_dim] */
+    uint16_t * v;
+    float * rope; /* [capacity][head_dim]: cos, sin per pair */
+};
+
+void jfo_rope_table(float base, int32_t head_dim, int32_t pos_begin, int32_t pos_count, float * out) {
+    /* ggml rope cache: theta starts at the position and is multiplied by
+     * theta_scale = base^(-2/n_dims) once per rotated pair. */
+    const float theta_scale = powf(base, -2.0f / (float) head_dim);
+    for (int32_t p = 0; p < pos_count; ++p) {
+        float theta = (float) (pos_begin + p);
+        float * row = out + (size_t) p * head_dim;
+        for (int32_t i = 0; i < head_dim / 2; ++i) {
+            row[2 * i] = cosf(theta);
+            row[2 * i + 1] = sinf(theta);
+            theta *= theta_scale;
+        }
+    }
+}
+
+int jfo_matmul(int type, const void * w, int64_t n, int64_t rows,
+               const float * x, int64_t tokens, float * y, int mode, int threads) {
+    uint32_t be = 0, bb = 0;
+    if (!jfo_type_block(type, &be, &bb) || n % be != 0) return -1;
+    const size_t row_bytes = (size_t) (n / be) * bb;
+    const int quantized = mode == JFO_MODE_Q8 && type != JFO_F32 && type != JFO_F16;
+    int8_t * q = NULL;
+    float * d = NULL;
+    int16_t * s16 = NULL;
+    if (quantized) {
+        if (n % 256 != 0) return -1;
+        q = malloc((size_t) (tokens * n));
+        d = malloc(sizeof(float) * (size_t) (tokens * n / 256));
+        s16 = malloc(sizeof(int16_t) * (size_t) (tokens * n / 16));
+        if (!q || !d || !s16) {
+            free(q); free(d); free(s16);
+            return -1;
+        }
+        for (int64_t t = 0; t < tokens; ++t) {
+            jfo_quantize_act(x + t * n, n, q + t * n, d + t * n / 256, s16 + t * n / 16);
+        }
+    }
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+#endif
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint8_t * row = (const uint8_t *) w + (size_t) r * row_bytes;
+        for (int64_t t = 0; t < tokens; ++t) {
+            const double v = quantized
+                ? jfo_vec_dot_q8(type, row, q + t * n, d + t * n / 256, s16 + t * n / 16, n)
+                : jfo_vec_dot_f32(type, row, x + t * n, n);
+            y[t * rows + r] = (float) v;
+        }
+    }
+    (void) threads;
+    free(q);
+    free(d);
+    free(s16);
+    return 0;
+}
+
+static void rms_norm(const float * x, const jfo_tensor * gain, int64_t n, float eps, float * out) {
+    double sum = 0.0;
+    for (int64_t i = 0; i < n; ++i) sum += (double) x[i] * (double) x[i];
+    const float mean = (float) (sum / (double) n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    if (gain->type == JFO_F32) {
+        const float * gv = (const float *) gain->data;
+        for (int64_t i = 0; i < n; ++i) out[i] = (x[i] * scale) * gv[i];
+        return;
+    }
+    float * gv = malloc(sizeof(float) * (size_t) n);
+    jfo_dequantize_row(gain->type, gain->data, gv, n);
+    for (int64_t i = 0; i < n; ++i) out[i] = (x[i] * scale) * gv[i];
+    free(gv);
+}
+
+static void add_bias(float * y, const jfo_tensor * b, int64_t tokens, int64_t n) {
+    if (b->data == NULL) return;
+    float * tmp = malloc(sizeof(float) * (size_t) n);
+    jfo_dequantize_row(b->type, b->data, tmp, n);
+    for (int64_t t = 0; t < tokens; ++t) {
+        for (int64_t i = 0; i < n; ++i) y[t * n + i] += tmp[i];
+    }
+    free(tmp);
+}
+
+static int linear(const jfo_session * s, const jfo_tensor * w, const float * x, int64_t tokens, float * y) {
+    return jfo_matmul(w->type, w->data, w->ne0, w->ne1, x, tokens, y, s->mode, s->threads);
+}
+
+static void rope_rows(const jfo_session * s, float * x, int64_t tokens, int32_t heads, int32_t pos0) {
+    const int32_t hd = s->head_dim, half = hd / 2;
+    for (int64_t t = 0; t < tokens; ++t) {
+        const float * cs = s->rope + (size_t) (pos0 + t) * hd;
+        for (int32_t h = 0; h < heads; ++h) {
+            float * v = x + (t * heads + h) * hd;
+            for (int32_t i = 0; i < half; ++i) {
+                const float c = cs[2 * i], sn = cs[2 * i + 1];
+                const float x0 = v[i], x1 = v[i + half];
+                v[i] = x0 * c - x1 * sn;
+                v[i + half] = x0 * sn + x1 * c;
+            }
+        }
+    }
+}
+
+jfo_session * jfo_session_create(const jfo_model * model, int32_t capacity, int32_t mode, int32_t threads) {
+    if (model == NULL || capacity <= 0 || capacity > model->n_ctx || model->n_head <= 0 ||
+        model->n_head_kv <= 0 || model->n_embd % model->n_head != 0 ||
+        model->n_head % model->n_head_kv != 0) {
+        return NULL;
+    }
+    jfo_session * s = calloc(1, sizeof(*s));
+    if (!s) return NULL;
+    s->m = model;
+    s->capacity = capacity;
+    s->mode = mode;
+    s->threads = threads;
+    s->head_dim = model->n_embd / model->n_head;
+    const size_t per_layer = (size_t) model->n_head_kv * capacity * s->head_dim;
+    s->k = calloc(per_layer * model->n_layer, sizeof(uint16_t));
+    s->v = calloc(per_layer * model->n_layer, sizeof(uint16_t));
+    s->rope = malloc(sizeof(float) * (size_t) capacity * s->head_dim);
+    if (!s->k || !s->v || !s->rope) {
+        jfo_session_destroy(s);
+        return NULL;
+    }
+    jfo_rope_table(model->rope_base, s->head_dim, 0, capacity, s->rope);
+    return s;
+}
+
+void jfo_session_destroy(jfo_session * s) {
+    if (!s) return;
+    free(s->k);
+    free(s->v);
+    free(s->rope);
+    free(s);
+}
+
+int32_t jfo_session_position(const jfo_session * s) { return s->pos; }
+
+int32_t jfo_session_rollback(jfo_session * s, int32_t n) {
+    /* qwen2_architecture.cpp:818-823: KV rows are left in place and overwritten later. */
+    if (n <= 0 || n > s->pos - s->prefill_pos) return -1;
+    s->pos -= n;
+    return 0;
+}
+
+static uint16_t * cache_row(const jfo_session * s, uint16_t * base, int32_t layer, int32_t kvh, int32_t p) {
+    const jfo_model * m = s->m;
+    return base + (((size_t) layer * m->n_head_kv + kvh) * s->capacity + p) * s->head_dim;
+}
+
+static void attention(const jfo_session * s, int32_t layer, const float * q, int64_t tokens,
+                      int32_t pos0, float * out) {
+    const jfo_model * m = s->m;
+    const int32_t hd = s->head_dim, group = m->n_head / m->n_head_kv;
+    const float scale = 1.0f / sqrtf((float) hd);
+#ifdef _OPENMP
+#pragma omp parallel for collapse(2) num_threads(s->threads > 0 ? s->threads : 1) schedule(static)
+#endif
+    for (int64_t t = 0; t < tokens; ++t) {
+        for (int32_t h = 0; h < m->n_head; ++h) {
+            const int32_t kvh = h / group;
+            const int32_t keys = pos0 + (int32_t) t + 1; /* causal: keys <= query position */
+            const float * qv = q + (t * m->n_head + h) * hd;
+            double * score = malloc(sizeof(double) * (size_t) keys);
+            double mx = -INFINITY;
+            for (int32_t j = 0; j < keys; ++j) {
+                const uint16_t * kr = cache_row(s, s->k, layer, kvh, j);
+                double dot = 0.0;
+                for (int32_t d = 0; d < hd; ++d) dot += (double) qv[d] * jfo_f16_to_f32(kr[d]);
+                score[j] = dot * scale;
+                if (score[j] > mx) mx = score[j];
+            }
+            double denom = 0.0;
+            for (int32_t j = 0; j < keys; ++j) {
+                score[j] = exp(score[j] - mx);
+                denom += score[j];
+            }
+            float * o = out + (t * m->n_head + h) * hd;
+            for (int32_t d = 0; d < hd; ++d) {
+                double acc = 0.0;
+                for (int32_t j = 0; j < keys; ++j) {
+                    acc += score[j] * jfo_f16_to_f32(cache_row(s, s->v, layer, kvh, j)[d]);
+                }
+                o[d] = (float) (acc / denom);
+            }
+            free(score);
+        }
+    }
+}
+
+int32_t jfo_session_forward(jfo_session * s, const int32_t * tokens, int32_t n,
+                            int32_t logits_rows, float * logits, int32_t * argmax_out) {
+    const jfo_model * m = s->m;
+    if (n <= 0 || (logits_rows != 0 && logits_rows != 1 && logits_rows != n)) return -1;
+    if ((int64_t) s->pos + n > s->capacity) return -2;
+    for (int32_t t = 0; t < n; ++t) {
+        if (tokens[t] < 0 || tokens[t] >= m->n_vocab) return -3;
+    }
+    const int64_t H = m->n_embd, F = m->n_ff, hd = s->head_dim;
+    const int64_t kv = (int64_t) m->n_head_kv * hd;
+    const int32_t pos0 = s->pos;
+    float * h = malloc(sizeof(float) * (size_t) (n * H));
+    float * xn = malloc(sizeof(float) * (size_t) (n * H));
+    float * q = malloc(sizeof(float) * (size_t) (n * H));
+    float * k = malloc(sizeof(float) * (size_t) (n * kv));
+    float * v = malloc(sizeof(float) * (size_t) (n * kv));
+    float * att = malloc(sizeof(float) * (size_t) (n * H));
+    float * o = malloc(sizeof(float) * (size_t) (n * H));
+    float * g = malloc(sizeof(float) * (size_t) (n * F));
+    float * u = malloc(sizeof(float) * (size_t) (n * F));
+    if (!h || !xn || !q || !k || !v || !att || !o || !g || !u) {
+        free(h); free(xn); free(q); free(k); free(v); free(att); free(o); free(g); free(u);
+        return -1;
+    }
+    /* embedding rows */
+    {
+        uint32_t be = 0, bb = 0;
+        jfo_type_block(m->tok_embd.type, &be, &bb);
+        const size_t row_bytes = (size_t) (H / be) * bb;
+        for (int32_t t = 0; t < n; ++t) {
+            jfo_dequantize_row(m->tok_embd.type,
+                               (const uint8_t *) m->tok_embd.data + (size_t) tokens[t] * row_bytes,
+                               h + t * H, H);
+        }
+    }
+    for (int32_t l = 0; l < m->n_layer; ++l) {
+        const jfo_layer * L = &m->layers[l];
+        for (int32_t t = 0; t < n; ++t) rms_norm(h + t * H, &L->attn_norm, H, m->rms_eps, xn + t * H);
+        linear(s, &L->wq, xn, n, q);
+        add_bias(q, &L->bq, n, H);
+        linear(s, &L->wk, xn, n, k);
+        add_bias(k, &L->bk, n, kv);
+        linear(s, &L->wv, xn, n, v);
+        add_bias(v, &L->bv, n, kv);
+        rope_rows(s, q, n, m->n_head, pos0);
+        rope_rows(s, k, n, m->n_head_kv, pos0);
+        for (int32_t t = 0; t < n; ++t) {
+            for (int32_t kh = 0; kh < m->n_head_kv; ++kh) {
+                uint16_t * kr = cache_row(s, s->k, l, kh, pos0 + t);
+                uint16_t * vr = cache_row(s, s->v, l, kh, pos0 + t);
+                for (int64_t d = 0; d < hd; ++d) {
+                    kr[d] = jfo_f32_to_f16(k[t * kv + kh * hd + d]);
+                    vr[d] = jfo_f32_to_f16(v[t * kv + kh * hd + d]);
+                }
+            }
+        }
+        attention(s, l, q, n, pos0, att);
+        linear(s, &L->wo, att, n, o);
+        for (int64_t i = 0; i < n * H; ++i) h[i] += o[i];
+        for (int32_t t = 0; t < n; ++t) rms_norm(h + t * H, &L->ffn_norm, H, m->rms_eps, xn + t * H);
+        linear(s, &L->w_up, xn, n, u);
+        linear(s, &L->w_gate, xn, n, g);
+        for (int64_t i = 0; i < n * F; ++i) g[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+        linear(s, &L->w_down, g, n, o);
+        for (int64_t i = 0; i < n * H; ++i) h[i] += o[i];
+    }
+    if (logits_rows > 0) {
+        const int32_t first = n - logits_rows;
+        const int64_t V = m->n_vocab;
+        float * lg = logits ? logits : malloc(sizeof(float) * (size_t) (logits_rows * V));
+        for (int32_t r = 0; r < logits_rows; ++r) {
+            rms_norm(h + (first + r) * H, &m->output_norm, H, m->rms_eps, xn + r * H);
+        }
+        linear(s, &m->output, xn, logits_rows, lg);
+        add_bias(lg, &m->output_bias, logits_rows, V);
+        if (argmax_out) {
+            for (int32_t r = 0; r < logits_rows; ++r) argmax_out[r] = jfo_argmax(lg + r * V, V);
+        }
+        if (!logits) free(lg);
+    }
+    if (s->pos == 0) s->prefill_pos = n;
+    s->pos += n;
+    free(h); free(xn); free(q); free(k); free(v); free(att); free(o); free(g); free(u);
+    return 0;
+}
+
+int32_t jfo_session_fill_kv(jfo_session * s, int32_t n, uint64_t seed) {
+    if (n <= 0 || n > s->capacity) return -1;
+    const jfo_model * m = s->m;
+    uint64_t state = seed ? seed : 0x9E3779B97F4A7C15ull;
+    for (int32_t l = 0; l < m->n_layer; ++l) {
+        for (int32_t kh = 0; kh < m->n_head_kv; ++kh) {
+            for (int32_t p = 0; p < n; ++p) {
+                uint16_t * kr = cache_row(s, s->k, l, kh, p);
+                uint16_t * vr = cache_row(s, s->v, l, kh, p);
+                for (int32_t d = 0; d < s->head_dim; ++d) {
+                    state ^= state << 13; state ^= state >> 7; state ^= state << 17;
+                    kr[d] = jfo_f32_to_f16((float) ((int32_t) (state & 0xFFFF) - 32768) / 32768.0f);
+                    vr[d] = jfo_f32_to_f16((float) ((int32_t) ((state >> 16) & 0xFFFF) - 32768) / 32768.0f);
+                }
+            }
+        }
+    }
+    s->pos = n;
+    s->prefill_pos = n;
+    return 0;
+}
+
+int32_t jfo_session_read_kv(const jfo_session * s, int32_t layer, int32_t n, uint16_t * k, uint16_t * v) {
+    const jfo_model * m = s->m;
+    if (layer < 0 || layer >= m->n_layer || n < 0 || n > s->capacity) return -1;
+    for (int32_t kh = 0; kh < m->n_head_kv; ++kh) {
+        memcpy(k + (size_t) kh * n * s->head_dim, cache_row(s, s->k, layer, kh, 0),
+               sizeof(uint16_t) * (size_t) n * s->head_dim);
+        memcpy(v + (size_t) kh * n * s->head_dim, cache_row(s, s->v, layer, kh, 0),
+               sizeof(uint16_t) * (size_t) n * s->head_dim);
+    }
+    return 0;
+}
+
+int32_t jfo_session_write_kv(jfo_session * s, int32_t layer, int32_t n, const uint16_t * k, const uint16_t * v) {
+    const jfo_model * m = s->m;
+    if (layer < 0 || layer >= m->n_layer || n < 0 || n > s->capacity) return -1;
+    for (int32_t kh = 0; kh < m->n_head_kv; ++kh) {
+        memcpy(cache_row(s, s->k, layer, kh, 0), k + (size_t) kh * n * s->head_dim,
+               sizeof(uint16_t) * (size_t) n * s->head_dim);
+        memcpy(cache_row(s, s->v, layer, kh, 0), v + (size_t) kh * n * s->head_dim,
+               sizeof(uint16_t) * (size_t) n * s->head_dim);
+    }
+    return 0;
+}
