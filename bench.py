@@ -1,0 +1,213 @@
+#!/usr/bin/env python3
+"""Decode / draft-verify throughput of the HIP Qwen2 stage engine on one MI355X.
+
+Workload (default): Qwen2.5-7B-shape model, Q4_K linear and embedding weights,
+Q6_K output head, synthetic seeded N(0, 0.02) weights; a seeded uniform
+1024-token prompt is prefilled, then K greedy decode steps at batch 1 are
+timed (one step = one full forward of one token through all 28 layers, the
+head and the on-GPU argmax). Draft verification (prompt-lookup k = 4) is timed
+with forced acceptance 0..k so the number does not depend on what random
+weights accept.
+
+Prints one JSON line. `roofline` is computed from per-launch HIP-event
+durations of the dominant kernel measured in this run; `cpu_baseline` times
+the CPU oracle (C, OpenMP) on the host cores over a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+import jetsonfabric_amd as jf  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--workload", default="qwen2.5-7b-q4k", choices=sorted(jf.CONFIGS))
+    ap.add_argument("--context", type=int, default=None, help="prompt tokens before the timed steps")
+    ap.add_argument("--draft", type=int, default=4, help="draft length k of the verify timing")
+    ap.add_argument("--verify-reps", type=int, default=20)
+    ap.add_argument("--profile-iters", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-threads", type=int, default=None)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--seed", type=int, default=1234)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (the engine holds every layer "
+              "on one device and runs no collectives)", file=sys.stderr)
+        return 2
+
+    wl = jf.config_by_name(args.workload)
+    cfg = wl.model
+    context = args.context if args.context is not None else wl.prompt_tokens
+    k = args.draft
+
+    t0 = time.perf_counter()
+    model = jf.Model.synthesize(cfg, type_linear=wl.type_linear, type_embd=wl.type_embd, type_output=wl.type_output,
+                                tied_output=wl.tied_output, seed=args.seed, threads=min(16, os.cpu_count() or 8))
+    log(f"synthesized {wl.description} in {time.perf_counter() - t0:.1f}s")
+    t0 = time.perf_counter()
+    engine = jf.NativeEngine(model)
+    log(f"engine on {engine.device_name}: {engine.weight_bytes / 1e9:.3f} GB of weights uploaded in "
+        f"{time.perf_counter() - t0:.1f}s")
+
+    rng = np.random.default_rng(args.seed)
+    prompt = [int(t) for t in rng.integers(0, cfg.n_vocab, context)]
+    capacity = context + args.warmup + args.steps + k + 8
+    session = engine.create_session(capacity)
+    t0 = time.perf_counter()
+    tok = session.prefill_greedy(prompt)
+    prefill_ms = (time.perf_counter() - t0) * 1e3
+    log(f"prefill of {context} tokens: {prefill_ms:.1f} ms")
+
+    for _ in range(args.warmup):
+        tok = session.decode_greedy(tok)
+    start_pos = session.position()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        tok = session.decode_greedy(tok)
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    tok_s = args.steps / elapsed
+    log(f"decode: {ms_per_step * 1e3:.1f} us/step = {tok_s:.1f} tok/s at positions {start_pos}..{session.position()}")
+
+    # Forced-acceptance verify: [prev] + first `a` tokens of the true continuation + wrong ids.
+    cont = [tok]
+    # true greedy continuation from the timed session's current state, then rewind
+    for _ in range(k + 1):
+        cont.append(session.decode_greedy(cont[-1]))
+    for _ in range(k + 1):
+        session.rollback(1)
+    verify_us = {}
+    for a in range(k + 1):
+        draft = cont[1:1 + a] + [(cont[1 + i] + 1 + i) % cfg.n_vocab for i in range(a, k)]
+        rows = [cont[0]] + draft
+        times = []
+        for _ in range(args.verify_reps):
+            t1 = time.perf_counter()
+            ids, accepted = session.verify(rows)
+            rollback = k - accepted
+            if rollback:
+                session.rollback(rollback)
+            times.append(time.perf_counter() - t1)
+            session.rollback(accepted + 1)  # restore the position for the next repetition
+        if accepted != a:
+            log(f"warning: forced acceptance {a} measured {accepted}")
+        verify_us[str(a)] = round(1e6 * float(np.median(times)), 1)
+    verify_mean = float(np.mean(list(verify_us.values())))
+    verify_dev_ms = session.time_steps([cont[0]] + cont[1:1 + k], iterations=args.verify_reps, warmup=2)
+    log(f"verify k={k}: {verify_us} us (wall, median) ; device {verify_dev_ms * 1e3:.1f} us/step")
+
+    # Per-kernel profile of one decode step (HIP events around every launch, graphs off).
+    prof = session.profile_step([tok], iterations=args.profile_iters)
+    step_bytes = sum(p["bytes"] for p in prof)
+    dominant = prof[0]
+    per_launch_ms = dominant["ms"] / dominant["launches"]
+    per_launch_bytes = dominant["bytes"] / dominant["launches"]
+    achieved = per_launch_bytes / (per_launch_ms * 1e-3) / 1e9
+    log("profile (ms/step): " + ", ".join(f"{p['kernel']} {p['ms']:.3f} ({p['launches']:.0f}x)" for p in prof[:8]))
+    log(f"dominant {dominant['kernel']}: {per_launch_bytes / 1e6:.2f} MB/launch, {per_launch_ms * 1e3:.1f} us/launch "
+        f"-> {achieved:.0f} GB/s")
+    vprof = session.profile_step([cont[0]] + cont[1:1 + k], iterations=args.profile_iters)
+    verify_bytes = sum(p["bytes"] for p in vprof)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(model, cfg, context, args)
+
+    line = {
+        "metric": "decode tok/s + spec-verify us/step, Qwen2-7B Q4_K, 1 MI355X; % HBM peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: seeded N(0,0.02) weights quantized per tensor type, seeded uniform prompt",
+        "config": {
+            "workload": f"{wl.name} greedy decode, batch 1, {context}-token context",
+            "weights": f"linear {jf.TYPE_NAMES[wl.type_linear]}, embedding {jf.TYPE_NAMES[wl.type_embd]}, "
+                       f"head {jf.TYPE_NAMES[wl.type_output]}",
+            "compute": "quant blocks x int8 activations (256-value blocks), int32 dot, f32 accumulate; f16 KV",
+            "verify_draft_k": k,
+        },
+        "verify_us_per_step": round(verify_mean, 1),
+        "verify_us_by_accepted": verify_us,
+        "verify_device_us_per_step": round(verify_dev_ms * 1e3, 1),
+        "decode_hbm_fraction": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "verify_hbm_fraction": round(verify_bytes / (verify_mean * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "decode_step_bytes": round(step_bytes),
+        "prefill_ms": round(prefill_ms, 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dominant["kernel"],
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "launch_us": round(per_launch_ms * 1e3, 2),
+            "launch_bytes": round(per_launch_bytes),
+        },
+        "cpu_baseline": cpu,
+        "kernels": [{"kernel": p["kernel"], "launches": p["launches"], "us_per_step": round(p["ms"] * 1e3, 1),
+                     "bytes_per_step": round(p["bytes"])} for p in prof],
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline(model, cfg, context, args):
+    """The oracle's multithreaded C forward timed on the host cores over a bounded sample."""
+    import oracle as jo
+
+    threads = args.cpu_threads or min(16, os.cpu_count() or 8)
+    om = jo.OracleModel.from_model(model)
+    sess = om.session(context + 64, jo.MODE_Q8, threads)
+    sess.fill_kv(context, seed=args.seed)
+    tok = 1
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        ids, _ = sess.forward([tok], 1)
+        tok = ids[0]
+        steps += 1
+        if time.perf_counter() - t0 >= args.cpu_seconds or steps >= 64:
+            break
+    elapsed = time.perf_counter() - t0
+    log(f"cpu baseline: {steps} decode steps in {elapsed:.1f}s on {threads} threads")
+    return {
+        "value": round(steps / elapsed, 4),
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{steps} greedy decode steps of the same model at position {context} "
+                  f"(KV filled with seeded values), CPU oracle, {threads} threads",
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

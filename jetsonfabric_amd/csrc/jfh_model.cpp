@@ -24,12 +24,16 @@ uint64_t splitmix(uint64_t x) {
     return x ^ (x >> 31);
 }
 
-// Standard normal for element i of a stream (Box-Muller on one 64-bit draw).
-float normal_at(uint64_t key, uint64_t i) {
-    const uint64_t r = splitmix(key ^ splitmix(i));
-    const double u1 = (double((r >> 11) & ((1ull << 26) - 1)) + 0.5) / double(1ull << 26);
-    const double u2 = double(r >> 38) / double(1ull << 26);
-    return float(std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2));
+// Two standard normals for elements 2p and 2p+1 of a stream: Box-Muller on
+// one 64-bit draw of a counter-based generator.
+void normal_pair(uint64_t key, uint64_t p, float* a, float* b) {
+    const uint64_t r = splitmix(key + p * 0xD1B54A32D192ED03ull);
+    const float u1 = (static_cast<float>(r & 0xFFFFFFu) + 0.5F) * (1.0F / 16777216.0F);
+    const float u2 = static_cast<float>((r >> 32) & 0xFFFFFFu) * (1.0F / 16777216.0F);
+    const float rad = std::sqrt(-2.0F * std::log(u1));
+    const float ang = 6.28318530718F * u2;
+    *a = rad * std::cos(ang);
+    *b = rad * std::sin(ang);
 }
 
 float roundf_half_away(float x) { return std::round(x); }
@@ -468,10 +472,18 @@ std::unique_ptr<HostModel> HostModel::synthesize(const SynthSpec& spec) {
         std::vector<uint8_t> bytes(rb * rows);
         const uint64_t key = spec.seed ^ fnv1a(name);
         parallel_rows(int64_t(rows), spec.threads, [&](int64_t a, int64_t b) {
-            std::vector<float> row(cols);
+            std::vector<float> row(cols + 1);
             for (int64_t r = a; r < b; ++r) {
-                for (uint64_t c = 0; c < cols; ++c) {
-                    row[c] = kind == 1 ? 1.0F : spec.stddev * normal_at(key, uint64_t(r) * cols + c);
+                if (kind == 1) {
+                    std::fill(row.begin(), row.end(), 1.0F);
+                } else {
+                    const uint64_t base = uint64_t(r) * cols;  // cols is even for every tensor here
+                    for (uint64_t c = 0; c < cols; c += 2) {
+                        float x0, x1;
+                        normal_pair(key, (base + c) / 2, &x0, &x1);
+                        row[c] = spec.stddev * x0;
+                        row[c + 1] = spec.stddev * x1;
+                    }
                 }
                 quantize_row(type, row.data(), bytes.data() + size_t(r) * rb, int64_t(cols));
             }
