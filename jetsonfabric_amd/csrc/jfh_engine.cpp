@@ -168,7 +168,8 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
         fail(Status::InvalidArgument, "the HIP engine holds every model layer on one device");
     }
     const ModelParams& p = params_;
-    if (p.head_dim % 2 != 0 || p.head_dim > 256) fail(Status::InvalidArgument, "unsupported head dimension");
+    if (p.head_dim % 2 != 0 || p.head_dim > 128) fail(Status::InvalidArgument, "unsupported head dimension");
+    if (p.n_embd % 4 != 0) fail(Status::InvalidArgument, "hidden size must be a multiple of 4");
     const uint32_t G = p.n_head / p.n_head_kv;
     prefill_chunk_ = std::max<uint32_t>(1, std::min<uint32_t>(8, 64 / G));
 
@@ -225,6 +226,10 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
     ffn_ = static_cast<float*>(device_alloc(R * F * sizeof(float)));
     logits_ = static_cast<float*>(device_alloc(R * static_cast<size_t>(p.n_vocab) * sizeof(float)));
     best_ = static_cast<unsigned long long*>(device_alloc(R * sizeof(unsigned long long)));
+    // attention split counters: zero here, and every kernel that uses them leaves them zero
+    const size_t n_counters = static_cast<size_t>(gpu::kMaxSeq) * p.n_head_kv;
+    counters_ = static_cast<int32_t*>(device_alloc(n_counters * sizeof(int32_t)));
+    hip_check(hipMemset(counters_, 0, n_counters * sizeof(int32_t)), "clear attention counters");
     step_dev_ = static_cast<gpu::StepDev*>(device_alloc(sizeof(gpu::StepDev)));
     out_dev_ = static_cast<gpu::StepOut*>(device_alloc(sizeof(gpu::StepOut)));
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&step_host_), sizeof(gpu::StepDev), hipHostMallocDefault),
@@ -256,9 +261,8 @@ void Engine::ensure_capacity(uint32_t capacity) {
     rope_ = nullptr;
     hip_check(hipMalloc(&rope_, table.size() * sizeof(float)), "allocate rope table");
     hip_check(hipMemcpy(rope_, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice), "upload rope table");
-    max_chunks_ = static_cast<int32_t>((cap + gpu::kAttnChunk - 1) / gpu::kAttnChunk);
-    const size_t partial_floats =
-        static_cast<size_t>(gpu::kMaxRows) * p.n_head * max_chunks_ * (p.head_dim + 2);
+    splits_ = gpu::attention_splits(static_cast<int32_t>(cap));
+    const size_t partial_floats = static_cast<size_t>(gpu::kMaxRows) * p.n_head * splits_ * (p.head_dim + 2);
     if (partial_) (void) hipFree(partial_);
     partial_ = nullptr;
     hip_check(hipMalloc(&partial_, partial_floats * sizeof(float)), "allocate attention partials");
@@ -352,7 +356,7 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         qkv.x = act_;
         qkv.y = qkv_;
         qkv.y_stride = H + 2 * kv;
-        timed(gemv_label(qkv), gemv_bytes(qkv), [&] { gpu::launch_gemv(qkv, s); });
+        timed(gemv_label(qkv) + ":qkv", gemv_bytes(qkv), [&] { gpu::launch_gemv(qkv, s); });
         timed("k_rope_kv", n * (H + 2 * kv) * 4.0 + n * H * 4.0 + n * 2 * kv * 2.0, [&] {
             gpu::launch_rope_kv(qkv_, n_rows, static_cast<int32_t>(p.n_head), static_cast<int32_t>(p.n_head_kv),
                                 static_cast<int32_t>(p.head_dim), rope_, step_dev_, static_cast<int32_t>(l), q_, s);
@@ -360,7 +364,7 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         timed("k_attention", n * H * 8.0, [&] {
             gpu::launch_attention(q_, step_dev_, n_rows, max_len, n_seq, static_cast<int32_t>(l),
                                   static_cast<int32_t>(p.n_head), static_cast<int32_t>(p.n_head_kv),
-                                  static_cast<int32_t>(p.head_dim), max_chunks_, partial_, act_, s);
+                                  static_cast<int32_t>(p.head_dim), splits_, partial_, counters_, act_, s);
         });
         gpu::GemvArgs o;
         o.mat[0] = L.o->mat;
@@ -369,7 +373,7 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         o.x = act_;
         o.y = h_;
         o.y_stride = H;
-        timed(gemv_label(o), gemv_bytes(o), [&] { gpu::launch_gemv(o, s); });
+        timed(gemv_label(o) + ":attn_output", gemv_bytes(o), [&] { gpu::launch_gemv(o, s); });
         timed("k_norm_quant", norm_bytes, [&] {
             gpu::launch_norm_quant(h_, H, L.ffn_norm, p.rms_eps, H, step_dev_, 0, n_rows, quantized_act_, act_, s);
         });
@@ -382,7 +386,7 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         gu.x = act_;
         gu.y = ffn_;
         gu.y_stride = F;
-        timed(gemv_label(gu), gemv_bytes(gu), [&] { gpu::launch_gemv(gu, s); });
+        timed(gemv_label(gu) + ":ffn_gate_up", gemv_bytes(gu), [&] { gpu::launch_gemv(gu, s); });
         timed("k_quant", n * F * (4.0 + 4.0 + 1.0), [&] {
             gpu::launch_quant(ffn_, F, F, n_rows, quantized_act_, act_, s);
         });
@@ -393,7 +397,7 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         dn.x = act_;
         dn.y = h_;
         dn.y_stride = H;
-        timed(gemv_label(dn), gemv_bytes(dn), [&] { gpu::launch_gemv(dn, s); });
+        timed(gemv_label(dn) + ":ffn_down", gemv_bytes(dn), [&] { gpu::launch_gemv(dn, s); });
     }
     if (n_out > 0) {
         timed("k_norm_quant", static_cast<double>(n_out) * H * 9.0 + 4.0 * H, [&] {
@@ -408,7 +412,7 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         head.y_stride = static_cast<int32_t>(p.n_vocab);
         head.best = best_;
         head.store_logits = store_logits ? 1 : 0;
-        timed(gemv_label(head), gemv_bytes(head), [&] { gpu::launch_gemv(head, s); });
+        timed(gemv_label(head) + ":output", gemv_bytes(head), [&] { gpu::launch_gemv(head, s); });
         timed("k_finish", 1024.0, [&] { gpu::launch_finish(best_, step_dev_, n_out, out_dev_, s); });
     }
 }

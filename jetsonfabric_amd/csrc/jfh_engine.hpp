@@ -166,7 +166,8 @@ private:
     float* partial_ = nullptr;
     float* rope_ = nullptr;
     uint32_t capacity_max_ = 0;
-    int32_t max_chunks_ = 0;
+    int32_t splits_ = 0;
+    int32_t* counters_ = nullptr;
 
     // captured step graphs keyed by (rows, seqs, outs, store_logits)
     std::map<uint64_t, hipGraphExec_t> graphs_;

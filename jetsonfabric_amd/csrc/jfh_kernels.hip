@@ -173,64 +173,57 @@ __device__ __forceinline__ void quant_block_wave(const float v[4], int lane, int
 
 // RMSNorm * gain of each selected row (qwen2_architecture.cpp:373-376), then
 // the int8 quantization consumed by the next matmul.
-__global__ __launch_bounds__(kThreads) void k_norm_quant(const float* h, int32_t hs, const float* gain, float eps,
-                                                         int32_t H, const StepDev* step, int32_t select_out,
-                                                         int32_t quant, Act x) {
-    extern __shared__ __align__(16) uint8_t lds_raw[];
-    float* xl = reinterpret_cast<float*>(lds_raw);
-    __shared__ float partial[kThreads / kWave];
-    const int r = blockIdx.x;
+// One wave per (256-value block, row): every wave reduces the whole row's sum
+// of squares itself (the row is a few KB, served from L2), then scales and
+// quantizes only its own block, so a row is spread over H/256 work-groups.
+__global__ __launch_bounds__(kWave) void k_norm_quant(const float* h, int32_t hs, const float* gain, float eps,
+                                                      int32_t H, const StepDev* step, int32_t select_out,
+                                                      int32_t quant, Act x) {
+    const int r = blockIdx.y, b = blockIdx.x, lane = threadIdx.x;
     const int src = select_out ? step->out_row[r] : r;
     const float* hr = h + static_cast<size_t>(src) * hs;
     float ss = 0.0F;
-    for (int i = threadIdx.x; i < H; i += kThreads) {
-        const float v = hr[i];
-        xl[i] = v;
-        ss += v * v;
+    for (int i = 4 * lane; i < H; i += 4 * kWave) {
+        const float4 v = *reinterpret_cast<const float4*>(hr + i);
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
     }
     ss = wave_sum(ss);
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    if (lane == 0) partial[wave] = ss;
-    __syncthreads();
-    float total = 0.0F;
-#pragma unroll
-    for (int w = 0; w < kThreads / kWave; ++w) total += partial[w];
-    const float mean = total / static_cast<float>(H);
+    const float mean = ss / static_cast<float>(H);
     const float scale = 1.0F / sqrtf(mean + eps);
+    float v[4] = {0.0F, 0.0F, 0.0F, 0.0F};
     float* xf = x.f + static_cast<size_t>(r) * x.stride;
-    for (int i = threadIdx.x; i < H; i += kThreads) {
-        const float v = (xl[i] * scale) * gain[i];
-        xl[i] = v;
-        xf[i] = v;
+    const int e0 = b * kActBlock + 4 * lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (e0 + i < H) {
+            v[i] = (hr[e0 + i] * scale) * gain[e0 + i];
+            xf[e0 + i] = v[i];
+        }
     }
     if (!quant) return;
-    __syncthreads();
-    for (int b = wave; b < H / kActBlock; b += kThreads / kWave) {
-        float v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = xl[b * kActBlock + 4 * lane + i];
-        quant_block_wave(v, lane, x.q + static_cast<size_t>(r) * x.stride + b * kActBlock,
-                         x.d + static_cast<size_t>(r) * (x.stride / kActBlock) + b,
-                         x.s + static_cast<size_t>(r) * (x.stride / 16) + b * 16);
-    }
+    quant_block_wave(v, lane, x.q + static_cast<size_t>(r) * x.stride + b * kActBlock,
+                     x.d + static_cast<size_t>(r) * (x.stride / kActBlock) + b,
+                     x.s + static_cast<size_t>(r) * (x.stride / 16) + b * 16);
 }
 
-// Quantizes float rows (SwiGLU output) and keeps the float copy.
-__global__ __launch_bounds__(kThreads) void k_quant(const float* src, int32_t ss, int32_t K, int32_t quant, Act x) {
-    const int r = blockIdx.x;
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+// Quantizes float rows (SwiGLU and attention outputs), one wave per
+// (256-value block, row), keeping the float copy when the source differs.
+__global__ __launch_bounds__(kWave) void k_quant(const float* src, int32_t ss, int32_t K, int32_t quant, Act x) {
+    const int r = blockIdx.y, b = blockIdx.x, lane = threadIdx.x;
     const float* row = src + static_cast<size_t>(r) * ss;
-    for (int b = wave; quant && b < K / kActBlock; b += kThreads / kWave) {
-        float v[4];
+    const int e0 = b * kActBlock + 4 * lane;
+    float v[4] = {0.0F, 0.0F, 0.0F, 0.0F};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = row[b * kActBlock + 4 * lane + i];
-        quant_block_wave(v, lane, x.q + static_cast<size_t>(r) * x.stride + b * kActBlock,
-                         x.d + static_cast<size_t>(r) * (x.stride / kActBlock) + b,
-                         x.s + static_cast<size_t>(r) * (x.stride / 16) + b * 16);
+    for (int i = 0; i < 4; ++i) {
+        if (e0 + i < K) {
+            v[i] = row[e0 + i];
+            if (x.f != src) x.f[static_cast<size_t>(r) * x.stride + e0 + i] = v[i];
+        }
     }
-    if (x.f != src) {
-        for (int i = threadIdx.x; i < K; i += kThreads) x.f[static_cast<size_t>(r) * x.stride + i] = row[i];
-    }
+    if (!quant) return;
+    quant_block_wave(v, lane, x.q + static_cast<size_t>(r) * x.stride + b * kActBlock,
+                     x.d + static_cast<size_t>(r) * (x.stride / kActBlock) + b,
+                     x.s + static_cast<size_t>(r) * (x.stride / 16) + b * 16);
 }
 #pragma clang fp contract(on)
 
@@ -655,133 +648,178 @@ __global__ __launch_bounds__(kThreads) void k_rope_kv(const float* qkv, int32_t 
 #pragma clang fp contract(on)
 
 // ------------------------------------------------------------------ attention
-// Split-K causal GQA attention (qwen2_architecture.cpp:438-464, mask 697-708):
-// one work-group per (key chunk, kv head, sequence) scores every query row of
-// the heads sharing that kv head, keeping (max, sum, unnormalized output).
-__global__ __launch_bounds__(kThreads) void k_attn_partial(const float* q, const StepDev* step, int32_t layer,
-                                                           int32_t n_head, int32_t n_head_kv, int32_t hd,
-                                                           int32_t max_chunks, float* partial) {
-    extern __shared__ __align__(16) uint8_t lds_raw[];
-    const int s_idx = blockIdx.z;
-    if (s_idx >= step->n_seq) return;
-    const SeqDev sd = step->seqs[s_idx];
-    const int n_keys = sd.pos0 + sd.len;
-    const int c = blockIdx.x;
-    const int j0 = c * kAttnChunk;
-    if (j0 >= n_keys) return;
+// Split-K causal GQA flash attention (qwen2_architecture.cpp:438-464, mask
+// 697-708) over the f16 cache. Work-group = (key split, kv head, sequence);
+// its 4 waves own disjoint slices of the query rows (G heads x T rows) that
+// share the kv head. Inside a wave each lane owns one key of a 64-key tile:
+// the lane loads its K row once and scores it against the wave's queries
+// (query values are wave-uniform, read through the scalar cache), the online
+// softmax keeps (max, sum, output) in registers, and for P.V the lanes switch
+// to owning two head dims each. The last work-group of a (sequence, kv head)
+// to finish merges the splits' partials (atomic counter, reset afterwards).
+constexpr int kAttnWaves = 4;
+
+template <int QPW>
+__global__ __launch_bounds__(kAttnWaves * kWave) void k_attention(
+    const float* __restrict__ q, const StepDev* __restrict__ step, int32_t layer, int32_t n_head, int32_t n_head_kv,
+    int32_t hd, int32_t splits_max, float* __restrict__ partial, int32_t* __restrict__ counters,
+    float* __restrict__ out, int32_t out_stride) {
+    __shared__ float P[kAttnWaves][QPW][kWave];
+    __shared__ int32_t last;
+    const int seq = blockIdx.z;
+    if (seq >= step->n_seq) return;
+    const int32_t pos0 = step->seqs[seq].pos0, len = step->seqs[seq].len, row0 = step->seqs[seq].row0;
+    const int32_t capacity = step->seqs[seq].capacity;
+    const int n_keys = pos0 + len;
+    int L = (n_keys + splits_max - 1) / splits_max;
+    L = (L + kWave - 1) / kWave * kWave;
+    const int n_splits = (n_keys + L - 1) / L;
+    const int split = blockIdx.x;
+    if (split >= n_splits) return;
+    const int k0 = split * L, k1 = min(n_keys, k0 + L);
     const int kvh = blockIdx.y;
-    const int G = n_head / n_head_kv;
-    const int NQ = G * sd.len;
-    const int H = n_head * hd;
-    const int ks = hd + 1;  // padded K row stride (floats)
-    float* Kc = reinterpret_cast<float*>(lds_raw);                // [CK][hd+1]
-    float* Vc = Kc + kAttnChunk * ks;                             // [CK][hd]
-    float* Qs = Vc + kAttnChunk * hd;                             // [NQ][hd]
-    float* P = Qs + NQ * hd;                                      // [NQ][CK]
-    const size_t head_base = (static_cast<size_t>(layer) * n_head_kv + kvh) * sd.capacity;
-    for (int idx = threadIdx.x; idx < kAttnChunk * hd; idx += kThreads) {
-        const int j = idx / hd, dd = idx % hd;
-        const int key = j0 + j;
-        float kv_k = 0.0F, kv_v = 0.0F;
-        if (key < n_keys) {
-            kv_k = h2f(sd.k[(head_base + key) * hd + dd]);
-            kv_v = h2f(sd.v[(head_base + key) * hd + dd]);
-        }
-        Kc[j * ks + dd] = kv_k;
-        Vc[j * hd + dd] = kv_v;
-    }
-    for (int idx = threadIdx.x; idx < NQ * hd; idx += kThreads) {
-        const int qi = idx / hd, dd = idx % hd;
-        const int t = qi / G, head = kvh * G + qi % G;
-        Qs[idx] = q[static_cast<size_t>(sd.row0 + t) * H + head * hd + dd];
-    }
-    __syncthreads();
+    const int G = n_head / n_head_kv, NQ = G * len, H = n_head * hd;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int q_begin = wave * QPW;
+    const int nq = max(0, min(QPW, NQ - q_begin));
     const float scale = 1.0F / sqrtf(static_cast<float>(hd));
-    {
-        // thread = (key j, dim slice sl of 8)
-        const int sl = threadIdx.x & 7, j = threadIdx.x >> 3;  // 32 keys x 8 slices per pass
-        const int dps = (hd + 7) / 8;
-        const int d0 = sl * dps, d1 = min(hd, d0 + dps);
-        for (int jj = j; jj < kAttnChunk; jj += kThreads / 8) {
-            const int key = j0 + jj;
-            for (int qi = 0; qi < NQ; ++qi) {
-                float dot = 0.0F;
-                for (int dd = d0; dd < d1; ++dd) dot += Qs[qi * hd + dd] * Kc[jj * ks + dd];
-                dot += __shfl_xor(dot, 1);
-                dot += __shfl_xor(dot, 2);
-                dot += __shfl_xor(dot, 4);
-                if (sl == 0) {
-                    const int t = qi / G;
-                    P[qi * kAttnChunk + jj] = (key <= sd.pos0 + t) ? dot * scale : -INFINITY;
+    const size_t head_base = (static_cast<size_t>(layer) * n_head_kv + kvh) * capacity;
+    const uint16_t* kc = step->seqs[seq].k + head_base * hd;
+    const uint16_t* vc = step->seqs[seq].v + head_base * hd;
+
+    const float* qrow[QPW];
+    int limit[QPW];  // last visible key of each query row (causal)
+#pragma unroll
+    for (int i = 0; i < QPW; ++i) {
+        const int qi = min(q_begin + i, NQ - 1);
+        const int t = qi / G, head = kvh * G + qi % G;
+        qrow[i] = q + static_cast<size_t>(row0 + t) * H + head * hd;
+        limit[i] = pos0 + t;
+    }
+    float m[QPW], l[QPW], o0[QPW], o1[QPW];
+#pragma unroll
+    for (int i = 0; i < QPW; ++i) {
+        m[i] = -INFINITY;
+        l[i] = 0.0F;
+        o0[i] = 0.0F;
+        o1[i] = 0.0F;
+    }
+    const bool vec8 = (hd & 7) == 0;
+    for (int t0 = k0; t0 < k1; t0 += kWave) {
+        const int key = t0 + lane;
+        const uint16_t* krow = kc + static_cast<size_t>(min(key, capacity - 1)) * hd;
+        float sc[QPW];
+#pragma unroll
+        for (int i = 0; i < QPW; ++i) sc[i] = 0.0F;
+        if (vec8) {
+            for (int d = 0; d < hd; d += 8) {
+                const uint4 kv = *reinterpret_cast<const uint4*>(krow + d);
+                const float kf[8] = {h2f(kv.x), h2f(kv.x >> 16), h2f(kv.y), h2f(kv.y >> 16),
+                                     h2f(kv.z), h2f(kv.z >> 16), h2f(kv.w), h2f(kv.w >> 16)};
+#pragma unroll
+                for (int i = 0; i < QPW; ++i) {
+                    if (i < nq) {
+                        const float* qd = qrow[i] + d;
+                        float acc = sc[i];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc += kf[e] * qd[e];
+                        sc[i] = acc;
+                    }
+                }
+            }
+        } else {
+            for (int d = 0; d < hd; ++d) {
+                const float kf = h2f(krow[d]);
+#pragma unroll
+                for (int i = 0; i < QPW; ++i) {
+                    if (i < nq) sc[i] += kf * qrow[i][d];
                 }
             }
         }
-    }
-    __syncthreads();
-    // softmax statistics of the chunk, one wave lane per query row
-    for (int qi = threadIdx.x; qi < NQ; qi += kThreads) {
-        float mx = -INFINITY;
-        for (int jj = 0; jj < kAttnChunk; ++jj) mx = fmaxf(mx, P[qi * kAttnChunk + jj]);
-        float l = 0.0F;
-        for (int jj = 0; jj < kAttnChunk; ++jj) {
-            const float p = mx == -INFINITY ? 0.0F : expf(P[qi * kAttnChunk + jj] - mx);
-            P[qi * kAttnChunk + jj] = p;
-            l += p;
-        }
-        const int t = qi / G, head = kvh * G + qi % G;
-        float* dst = partial + ((static_cast<size_t>(sd.row0 + t) * n_head + head) * max_chunks + c) * (hd + 2);
-        dst[0] = mx;
-        dst[1] = l;
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < NQ * hd; idx += kThreads) {
-        const int qi = idx / hd, dd = idx % hd;
-        float o = 0.0F;
-        for (int jj = 0; jj < kAttnChunk; ++jj) o += P[qi * kAttnChunk + jj] * Vc[jj * hd + dd];
-        const int t = qi / G, head = kvh * G + qi % G;
-        partial[((static_cast<size_t>(sd.row0 + t) * n_head + head) * max_chunks + c) * (hd + 2) + 2 + dd] = o;
-    }
-}
-
-// Merges the chunk partials of one row into the attention output and
-// quantizes it for the output projection.
-__global__ __launch_bounds__(kThreads) void k_attn_combine(const float* partial, const StepDev* step, int32_t n_head,
-                                                           int32_t hd, int32_t max_chunks, int32_t quant, Act x) {
-    extern __shared__ __align__(16) uint8_t lds_raw[];
-    float* row_out = reinterpret_cast<float*>(lds_raw);
-    const int r = blockIdx.x;
-    if (r >= step->n_rows) return;
-    const SeqDev& sd = step->seqs[step->seq[r]];
-    const int n_chunks = (sd.pos0 + sd.len + kAttnChunk - 1) / kAttnChunk;
-    const int H = n_head * hd;
-    for (int idx = threadIdx.x; idx < H; idx += kThreads) {
-        const int head = idx / hd, dd = idx % hd;
-        const float* base = partial + (static_cast<size_t>(r) * n_head + head) * max_chunks * (hd + 2);
-        float M = -INFINITY;
-        for (int c = 0; c < n_chunks; ++c) M = fmaxf(M, base[c * (hd + 2)]);
-        float L = 0.0F, O = 0.0F;
-        for (int c = 0; c < n_chunks; ++c) {
-            const float m = base[c * (hd + 2)];
-            if (m == -INFINITY) continue;
-            const float w = expf(m - M);
-            L += base[c * (hd + 2) + 1] * w;
-            O += base[c * (hd + 2) + 2 + dd] * w;
-        }
-        const float v = O / L;
-        row_out[idx] = v;
-        x.f[static_cast<size_t>(r) * x.stride + idx] = v;
-    }
-    if (!quant) return;
-    __syncthreads();
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    for (int b = wave; b < H / kActBlock; b += kThreads / kWave) {
-        float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = row_out[b * kActBlock + 4 * lane + i];
-        quant_block_wave(v, lane, x.q + static_cast<size_t>(r) * x.stride + b * kActBlock,
-                         x.d + static_cast<size_t>(r) * (x.stride / kActBlock) + b,
-                         x.s + static_cast<size_t>(r) * (x.stride / 16) + b * 16);
+        for (int i = 0; i < QPW; ++i) {
+            if (i < nq) {
+                const bool vis = key < k1 && key <= limit[i];
+                const float s = vis ? sc[i] * scale : -INFINITY;
+                const float m_new = fmaxf(m[i], wave_max(s));
+                float p = 0.0F, alpha = 1.0F;
+                if (m_new != -INFINITY) {
+                    alpha = m[i] == -INFINITY ? 0.0F : expf(m[i] - m_new);
+                    p = vis ? expf(s - m_new) : 0.0F;
+                }
+                l[i] = l[i] * alpha + p;
+                o0[i] *= alpha;
+                o1[i] *= alpha;
+                m[i] = m_new;
+                P[wave][i][lane] = p;
+            }
+        }
+        __syncthreads();
+        const int nk = min(kWave, k1 - t0);
+        if (2 * lane < hd) {
+            for (int j = 0; j < nk; ++j) {
+                const uint32_t vv = *reinterpret_cast<const uint32_t*>(vc + static_cast<size_t>(t0 + j) * hd + 2 * lane);
+                const float v0 = h2f(vv), v1 = h2f(vv >> 16);
+#pragma unroll
+                for (int i = 0; i < QPW; ++i) {
+                    if (i < nq) {
+                        const float pj = P[wave][i][j];
+                        o0[i] += pj * v0;
+                        o1[i] += pj * v1;
+                    }
+                }
+            }
+        }
+        __syncthreads();
     }
+    // split partial: (max, sum, unnormalized output) per query row
+#pragma unroll
+    for (int i = 0; i < QPW; ++i) {
+        if (i < nq) {
+            const float lsum = wave_sum(l[i]);
+            const int qi = q_begin + i;
+            const int t = qi / G, head = kvh * G + qi % G;
+            float* dst = partial + ((static_cast<size_t>(row0 + t) * n_head + head) * splits_max + split) * (hd + 2);
+            if (lane == 0) {
+                dst[0] = m[i];
+                dst[1] = lsum;
+            }
+            if (2 * lane < hd) {
+                dst[2 + 2 * lane] = o0[i];
+                dst[3 + 2 * lane] = o1[i];
+            }
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) last = atomicAdd(counters + seq * n_head_kv + kvh, 1) == n_splits - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    // merge the splits: lanes over splits for the statistics, lanes over dims for the output
+    for (int qi = wave; qi < NQ; qi += kAttnWaves) {
+        const int t = qi / G, head = kvh * G + qi % G;
+        const float* base = partial + (static_cast<size_t>(row0 + t) * n_head + head) * splits_max * (hd + 2);
+        const float ms = lane < n_splits ? base[lane * (hd + 2)] : -INFINITY;
+        const float ls = lane < n_splits ? base[lane * (hd + 2) + 1] : 0.0F;
+        const float M = wave_max(ms);
+        const float w = ms == -INFINITY ? 0.0F : expf(ms - M);
+        const float total = wave_sum(ls * w);
+        float a0 = 0.0F, a1 = 0.0F;
+        for (int sp = 0; sp < n_splits; ++sp) {
+            const float ws = __shfl(w, sp);
+            if (2 * lane < hd) {
+                a0 += ws * base[sp * (hd + 2) + 2 + 2 * lane];
+                a1 += ws * base[sp * (hd + 2) + 3 + 2 * lane];
+            }
+        }
+        if (2 * lane < hd) {
+            float* o = out + static_cast<size_t>(row0 + t) * out_stride + head * hd;
+            o[2 * lane] = a0 / total;
+            o[2 * lane + 1] = a1 / total;
+        }
+    }
+    if (threadIdx.x == 0) counters[seq * n_head_kv + kvh] = 0;
 }
 
 // ------------------------------------------------------------------ argmax + acceptance
@@ -893,14 +931,16 @@ void launch_embed(const DMat& table, const StepDev* step, float* h, int32_t n_ro
 void launch_norm_quant(const float* h, int32_t h_stride, const float* gain, float eps, int32_t H,
                        const StepDev* step, int32_t select_out, int32_t n_rows, bool quantize, Act x,
                        hipStream_t stream) {
-    hipLaunchKernelGGL(k_norm_quant, dim3(n_rows), dim3(kThreads), static_cast<size_t>(H) * 4, stream, h, h_stride,
-                       gain, eps, H, step, select_out, quantize ? 1 : 0, x);
+    if (H % 4 != 0) throw std::invalid_argument("hidden size must be a multiple of 4");
+    hipLaunchKernelGGL(k_norm_quant, dim3((H + kActBlock - 1) / kActBlock, n_rows), dim3(kWave), 0, stream, h,
+                       h_stride, gain, eps, H, step, select_out, quantize ? 1 : 0, x);
     check(hipGetLastError(), "norm launch");
 }
 
 void launch_quant(const float* src, int32_t src_stride, int32_t K, int32_t n_rows, bool quantize, Act x,
                   hipStream_t stream) {
-    hipLaunchKernelGGL(k_quant, dim3(n_rows), dim3(kThreads), 0, stream, src, src_stride, K, quantize ? 1 : 0, x);
+    hipLaunchKernelGGL(k_quant, dim3((K + kActBlock - 1) / kActBlock, n_rows), dim3(kWave), 0, stream, src, src_stride,
+                       K, quantize ? 1 : 0, x);
     check(hipGetLastError(), "quant launch");
 }
 
@@ -911,23 +951,31 @@ void launch_rope_kv(const float* qkv, int32_t n_rows, int32_t n_head, int32_t n_
     check(hipGetLastError(), "rope launch");
 }
 
+int32_t attention_splits(int32_t capacity) {
+    const int32_t s = (capacity + kWave - 1) / kWave;
+    return s < 1 ? 1 : (s > kWave ? kWave : s);
+}
+
 void launch_attention(const float* q, const StepDev* step, int32_t n_rows, int32_t max_len, int32_t n_seq,
-                      int32_t layer, int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t max_chunks,
-                      float* partial, Act out, hipStream_t stream) {
+                      int32_t layer, int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t splits,
+                      float* partial, int32_t* counters, Act out, hipStream_t stream) {
     const int G = n_head / n_head_kv;
-    const int nq_max = G * max_len;
-    const size_t lds = (static_cast<size_t>(kAttnChunk) * (head_dim + 1) + static_cast<size_t>(kAttnChunk) * head_dim +
-                        static_cast<size_t>(nq_max) * head_dim + static_cast<size_t>(nq_max) * kAttnChunk) *
-                       sizeof(float);
-    if (lds > 160 * 1024) throw std::invalid_argument("attention work-group exceeds LDS: too many query rows");
-    hipLaunchKernelGGL(k_attn_partial, dim3(max_chunks, n_head_kv, n_seq), dim3(kThreads), lds, stream, q, step,
-                       layer, n_head, n_head_kv, head_dim, max_chunks, partial);
+    const int nq = G * max_len;
+    if (head_dim > 2 * kWave || head_dim % 2 != 0) throw std::invalid_argument("attention supports even head dims <= 128");
+    if (nq > kAttnWaves * 16) throw std::invalid_argument("attention work-group exceeds its query rows");
+    const int qpw = (nq + kAttnWaves - 1) / kAttnWaves;
+    dim3 grid(splits, n_head_kv, n_seq), block(kAttnWaves * kWave);
+#define JFH_ATTN(QPW)                                                                                          \
+    hipLaunchKernelGGL(k_attention<QPW>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, \
+                       splits, partial, counters, out.f, out.stride)
+    if (qpw <= 2) JFH_ATTN(2);
+    else if (qpw <= 4) JFH_ATTN(4);
+    else if (qpw <= 8) JFH_ATTN(8);
+    else JFH_ATTN(16);
+#undef JFH_ATTN
     check(hipGetLastError(), "attention launch");
     const int H = n_head * head_dim;
-    const bool quant = H % kActBlock == 0;
-    hipLaunchKernelGGL(k_attn_combine, dim3(n_rows), dim3(kThreads), static_cast<size_t>(H) * 4, stream, partial,
-                       step, n_head, head_dim, max_chunks, quant ? 1 : 0, out);
-    check(hipGetLastError(), "attention combine launch");
+    launch_quant(out.f, out.stride, H, n_rows, H % kActBlock == 0, out, stream);
 }
 
 void launch_finish(const unsigned long long* best, const StepDev* step, int32_t n_out, StepOut* out,

@@ -11,7 +11,6 @@ namespace jfh::gpu {
 constexpr int kMaxRows = 64;   // token rows of one step (sum over sequences)
 constexpr int kMaxSeq = 16;    // sequences of one batched step
 constexpr int kActBlock = 256; // activation quantization block (values)
-constexpr int kAttnChunk = 64; // keys per attention work-group
 
 // A weight matrix in device memory. Quantized types are stored as a 16-byte
 // aligned main plane [rows][blocks][main_block_bytes] plus an aux plane
@@ -97,9 +96,13 @@ void launch_quant(const float* src, int32_t src_stride, int32_t K, int32_t n_row
 void launch_gemv(const GemvArgs& a, hipStream_t stream);
 void launch_rope_kv(const float* qkv, int32_t n_rows, int32_t n_head, int32_t n_head_kv, int32_t head_dim,
                     const float* rope, const StepDev* step, int32_t layer, float* qout, hipStream_t stream);
+// Split-K flash attention writing out.f rows, then the int8 quantization of
+// those rows. `splits` is fixed per capacity (attention_splits); `counters`
+// holds kMaxSeq * n_head_kv zero-initialized ints that the kernel resets.
 void launch_attention(const float* q, const StepDev* step, int32_t n_rows, int32_t max_len, int32_t n_seq,
-                      int32_t layer, int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t max_chunks,
-                      float* partial, Act out, hipStream_t stream);
+                      int32_t layer, int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t splits,
+                      float* partial, int32_t* counters, Act out, hipStream_t stream);
+int32_t attention_splits(int32_t capacity);
 void launch_finish(const unsigned long long* best, const StepDev* step, int32_t n_out, StepOut* out,
                    hipStream_t stream);
 void launch_dequant_rows(const DMat& m, int32_t row0, int32_t n_rows, float* out, hipStream_t stream);

@@ -10,6 +10,7 @@ steps the speculative decoder needs. Every call goes through libjfh.so.
 from __future__ import annotations
 
 import ctypes
+import os
 import time
 from dataclasses import dataclass, field
 from typing import Iterable, Sequence
@@ -311,7 +312,10 @@ class NativeSession:
 class NativeEngine:
     """Device-resident Qwen2 weights and the step kernels (native_inference.hpp:126-160)."""
 
-    def __init__(self, model: Model, device: int = 0, use_graphs: bool = True):
+    def __init__(self, model: Model, device: int = 0, use_graphs: bool | None = None):
+        if use_graphs is None:
+            # JFH_USE_GRAPHS=0 launches every kernel directly instead of replaying captured step graphs
+            use_graphs = os.environ.get("JFH_USE_GRAPHS", "1") != "0"
         opts = _capi.EngineOptions(device, int(use_graphs))
         h = ctypes.c_void_p()
         start = time.perf_counter()
