@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstddef>
 #include <cstring>
 
 namespace jfh {
@@ -80,76 +81,140 @@ const float* Engine::upload_f32(const TensorView& t) {
     return static_cast<const float*>(p);
 }
 
-const Engine::DeviceTensor& Engine::upload(const TensorView& t) {
-    auto found = tensors_.find(t.name);
-    if (found != tensors_.end()) return found->second;
-    DeviceTensor d;
-    const uint64_t cols = t.shape[0];
-    const uint64_t rows = t.size / row_bytes(t.type, cols);
-    d.mat.type = t.type;
-    d.mat.rows = static_cast<uint32_t>(rows);
-    d.mat.cols = static_cast<uint32_t>(cols);
-    d.bytes = t.size;
-    std::vector<uint8_t> main, aux;
-    const uint8_t* src = t.data;
-    switch (t.type) {
+namespace {
+
+// Device row layout per type: main plane bytes and aux plane bytes of one row.
+void device_row_bytes(uint32_t type, uint64_t cols, uint32_t& main, uint32_t& aux) {
+    switch (type) {
     case kF32:
     case kF16:
     case kQ4_K:
-        d.mat.main_row_bytes = static_cast<uint32_t>(row_bytes(t.type, cols));
-        break;
-    case kQ6_K: {
-        const uint64_t nb = cols / 256;
-        d.mat.main_row_bytes = static_cast<uint32_t>(nb * 208);
-        d.mat.aux_row_bytes = static_cast<uint32_t>(nb * 2);
-        main.resize(rows * nb * 208);
-        aux.resize(rows * nb * 2);
-        for (uint64_t b = 0; b < rows * nb; ++b) {
-            std::memcpy(&main[b * 208], src + b * 210, 208);
-            std::memcpy(&aux[b * 2], src + b * 210 + 208, 2);
-        }
-        break;
-    }
-    case kQ8_0: {
-        const uint64_t nb = cols / 32;
-        d.mat.main_row_bytes = static_cast<uint32_t>(nb * 32);
-        d.mat.aux_row_bytes = static_cast<uint32_t>(nb * 2);
-        main.resize(rows * nb * 32);
-        aux.resize(rows * nb * 2);
-        for (uint64_t b = 0; b < rows * nb; ++b) {
-            std::memcpy(&aux[b * 2], src + b * 34, 2);
-            std::memcpy(&main[b * 32], src + b * 34 + 2, 32);
-        }
-        break;
-    }
-    case kQ2_K: {
-        const uint64_t nb = cols / 256;
-        d.mat.main_row_bytes = static_cast<uint32_t>(nb * 80);
-        d.mat.aux_row_bytes = static_cast<uint32_t>(nb * 4);
-        main.resize(rows * nb * 80);
-        aux.resize(rows * nb * 4);
-        for (uint64_t b = 0; b < rows * nb; ++b) {
-            std::memcpy(&main[b * 80], src + b * 84, 80);
-            std::memcpy(&aux[b * 4], src + b * 84 + 80, 4);
-        }
-        break;
-    }
+        main = static_cast<uint32_t>(row_bytes(type, cols));
+        aux = 0;
+        return;
+    case kQ6_K:
+        main = static_cast<uint32_t>(cols / 256 * 208);
+        aux = static_cast<uint32_t>(cols / 256 * 2);
+        return;
+    case kQ8_0:
+        main = static_cast<uint32_t>(cols / 32 * 32);
+        aux = static_cast<uint32_t>(cols / 32 * 2);
+        return;
+    case kQ2_K:
+        main = static_cast<uint32_t>(cols / 256 * 80);
+        aux = static_cast<uint32_t>(cols / 256 * 4);
+        return;
     default:
-        fail(Status::FormatError, std::string("unsupported tensor type ") + type_name(t.type) + " for " + t.name);
+        fail(Status::FormatError, std::string("unsupported tensor type ") + type_name(type) + " for a device matrix");
     }
-    const size_t main_bytes = static_cast<size_t>(rows) * d.mat.main_row_bytes;
-    d.main = device_alloc(main_bytes);
-    hip_check(hipMemcpy(d.main, main.empty() ? static_cast<const void*>(src) : main.data(), main_bytes,
-                        hipMemcpyHostToDevice),
-              "upload tensor");
-    d.mat.main = static_cast<const uint8_t*>(d.main);
+}
+
+// One GGML-encoded row split into the device planes: Q4_K/F32/F16 verbatim;
+// Q6_K ql|qh|scales (208) + d; Q8_0 qs (32) + d; Q2_K scales|qs (80) + d,dmin.
+void repack_row(uint32_t type, const uint8_t* src, uint64_t cols, uint8_t* main, uint8_t* aux) {
+    switch (type) {
+    case kQ6_K:
+        for (uint64_t b = 0; b < cols / 256; ++b) {
+            std::memcpy(main + b * 208, src + b * 210, 208);
+            std::memcpy(aux + b * 2, src + b * 210 + 208, 2);
+        }
+        return;
+    case kQ8_0:
+        for (uint64_t b = 0; b < cols / 32; ++b) {
+            std::memcpy(aux + b * 2, src + b * 34, 2);
+            std::memcpy(main + b * 32, src + b * 34 + 2, 32);
+        }
+        return;
+    case kQ2_K:
+        for (uint64_t b = 0; b < cols / 256; ++b) {
+            std::memcpy(main + b * 80, src + b * 84, 80);
+            std::memcpy(aux + b * 4, src + b * 84 + 80, 4);
+        }
+        return;
+    default:
+        std::memcpy(main, src, row_bytes(type, cols));
+        return;
+    }
+}
+
+}  // namespace
+
+uint32_t Engine::device_row(const TensorRef& r, uint32_t row) {
+    switch (r.kind) {
+    case 1: {
+        // q/k heads: physical row 2i holds head row i, 2i + 1 holds head row i + head_dim/2
+        const uint32_t hd = r.head_dim, head = row / hd, i = row % hd;
+        const uint32_t within = i < hd / 2 ? 2 * i : 2 * (i - hd / 2) + 1;
+        return r.offset + head * hd + within;
+    }
+    case 2:
+        return (row / gpu::kGluGroup) * 2 * gpu::kGluGroup + row % gpu::kGluGroup;
+    case 3:
+        return (row / gpu::kGluGroup) * 2 * gpu::kGluGroup + gpu::kGluGroup + row % gpu::kGluGroup;
+    default:
+        return r.offset + row;
+    }
+}
+
+const Engine::DeviceTensor& Engine::upload_rows(const std::string& key, uint32_t type, uint64_t cols,
+                                                const std::vector<RowSource>& rows, const float* bias) {
+    DeviceTensor d;
+    uint32_t main_rb = 0, aux_rb = 0;
+    device_row_bytes(type, cols, main_rb, aux_rb);
+    d.mat.type = type;
+    d.mat.rows = static_cast<uint32_t>(rows.size());
+    d.mat.cols = static_cast<uint32_t>(cols);
+    d.mat.main_row_bytes = main_rb;
+    d.mat.aux_row_bytes = aux_rb;
+    const uint64_t src_rb = row_bytes(type, cols);
+    std::vector<uint8_t> main(rows.size() * main_rb), aux(rows.size() * aux_rb);
+    for (size_t r = 0; r < rows.size(); ++r) {
+        const RowSource& rs = rows[r];
+        repack_row(type, rs.tensor->data + static_cast<uint64_t>(rs.row) * src_rb, cols, main.data() + r * main_rb,
+                   aux.empty() ? nullptr : aux.data() + r * aux_rb);
+        d.bytes += src_rb;
+    }
+    void* mp = device_alloc(main.size());
+    hip_check(hipMemcpy(mp, main.data(), main.size(), hipMemcpyHostToDevice), "upload matrix");
+    d.mat.main = static_cast<const uint8_t*>(mp);
     if (!aux.empty()) {
-        d.aux = device_alloc(aux.size());
-        hip_check(hipMemcpy(d.aux, aux.data(), aux.size(), hipMemcpyHostToDevice), "upload tensor");
-        d.mat.aux = static_cast<const uint8_t*>(d.aux);
+        void* ap = device_alloc(aux.size());
+        hip_check(hipMemcpy(ap, aux.data(), aux.size(), hipMemcpyHostToDevice), "upload matrix");
+        d.mat.aux = static_cast<const uint8_t*>(ap);
     }
+    if (bias) {
+        void* bp = device_alloc(rows.size() * sizeof(float));
+        hip_check(hipMemcpy(bp, bias, rows.size() * sizeof(float), hipMemcpyHostToDevice), "upload bias");
+        d.mat.bias = static_cast<const float*>(bp);
+    }
+    return matrices_.emplace(key, d).first->second;
+}
+
+void Engine::add_ref(const TensorView& t, const DeviceTensor& dev, uint32_t offset, uint32_t kind) {
+    TensorRef r;
+    r.dev = &dev;
+    r.rows = static_cast<uint32_t>(t.size / row_bytes(t.type, t.shape[0]));
+    r.offset = offset;
+    r.kind = kind;
+    r.head_dim = params_.head_dim;
+    refs_[t.name] = r;
     weight_bytes_ += t.size;
-    return tensors_.emplace(t.name, d).first->second;
+}
+
+const Engine::DeviceTensor& Engine::upload_single(const TensorView& t) {
+    const uint64_t cols = t.shape[0];
+    const uint32_t rows = static_cast<uint32_t>(t.size / row_bytes(t.type, cols));
+    std::vector<RowSource> order(rows);
+    for (uint32_t r = 0; r < rows; ++r) order[r] = {&t, r};
+    const DeviceTensor& d = upload_rows(t.name, t.type, cols, order, nullptr);
+    add_ref(t, d, 0, 0);
+    return d;
+}
+
+const Engine::TensorRef& Engine::find_ref(const std::string& name) const {
+    auto it = refs_.find(name);
+    if (it == refs_.end()) fail(Status::NotFound, "tensor is not resident as a matrix: " + name);
+    return it->second;
 }
 
 Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(model.params()), options_(options) {
@@ -173,33 +238,76 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
     const uint32_t G = p.n_head / p.n_head_kv;
     prefill_chunk_ = std::max<uint32_t>(1, std::min<uint32_t>(8, 64 / G));
 
-    embd_ = &upload(model.require("token_embd.weight"));
-    output_ = &upload(model.require("output.weight"));
+    if (p.head_dim % 4 != 0) fail(Status::InvalidArgument, "head dimension must be a multiple of 4");
+    if (p.n_ff % gpu::kGluGroup != 0) fail(Status::InvalidArgument, "feed-forward length must be a multiple of 8");
+    embd_ = &upload_single(model.require("token_embd.weight"));
     output_norm_ = upload_f32(model.require("output_norm.weight"));
-    if (const TensorView* b = model.find("output.bias")) {
-        DeviceTensor& out = tensors_.at("output.weight");
-        out.mat.bias = upload_f32(*b);
-        output_ = &out;
+    {
+        const TensorView& out = model.require("output.weight");
+        std::vector<float> bias;
+        if (const TensorView* b = model.find("output.bias")) {
+            if (b->type != kF32) fail(Status::FormatError, "tensor must be F32: " + b->name);
+            bias.assign(reinterpret_cast<const float*>(b->data), reinterpret_cast<const float*>(b->data) + b->size / 4);
+            weight_bytes_ += b->size;
+        }
+        const uint32_t rows = static_cast<uint32_t>(out.size / row_bytes(out.type, out.shape[0]));
+        if (!bias.empty() && bias.size() != rows) fail(Status::FormatError, "output.bias does not match output.weight");
+        std::vector<RowSource> order(rows);
+        for (uint32_t r = 0; r < rows; ++r) order[r] = {&out, r};
+        output_ = &upload_rows(out.name, out.type, out.shape[0], order, bias.empty() ? nullptr : bias.data());
+        add_ref(out, *output_, 0, 0);
     }
+    const uint32_t Hq = p.n_head * p.head_dim, KV = p.n_head_kv * p.head_dim;
     for (uint32_t l = 0; l < p.n_layer; ++l) {
         const std::string pre = "blk." + std::to_string(l) + ".";
         Layer L{};
         L.attn_norm = upload_f32(model.require(pre + "attn_norm.weight"));
         L.ffn_norm = upload_f32(model.require(pre + "ffn_norm.weight"));
-        L.bq = upload_f32(model.require(pre + "attn_q.bias"));
-        L.bk = upload_f32(model.require(pre + "attn_k.bias"));
-        L.bv = upload_f32(model.require(pre + "attn_v.bias"));
-        L.q = &upload(model.require(pre + "attn_q.weight"));
-        L.k = &upload(model.require(pre + "attn_k.weight"));
-        L.v = &upload(model.require(pre + "attn_v.weight"));
-        L.o = &upload(model.require(pre + "attn_output.weight"));
-        L.gate = &upload(model.require(pre + "ffn_gate.weight"));
-        L.up = &upload(model.require(pre + "ffn_up.weight"));
-        L.down = &upload(model.require(pre + "ffn_down.weight"));
-        if (L.q->mat.type != L.k->mat.type || L.q->mat.type != L.v->mat.type || L.gate->mat.type != L.up->mat.type) {
+        const TensorView& wq = model.require(pre + "attn_q.weight");
+        const TensorView& wk = model.require(pre + "attn_k.weight");
+        const TensorView& wv = model.require(pre + "attn_v.weight");
+        const TensorView& gate = model.require(pre + "ffn_gate.weight");
+        const TensorView& up = model.require(pre + "ffn_up.weight");
+        if (wq.type != wk.type || wq.type != wv.type || gate.type != up.type) {
             fail(Status::FormatError, "q/k/v and gate/up of a layer must share one tensor type");
         }
-        for (const DeviceTensor* t : {L.q, L.o, L.gate, L.down}) {
+        // fused q|k|v rows (q and k in RoPE pair order) with their biases
+        std::vector<RowSource> order(Hq + 2 * KV);
+        std::vector<float> bias(Hq + 2 * KV);
+        const TensorView* parts[3] = {&wq, &wk, &wv};
+        const char* bias_names[3] = {"attn_q.bias", "attn_k.bias", "attn_v.bias"};
+        const uint32_t offsets[3] = {0, Hq, Hq + KV}, counts[3] = {Hq, KV, KV}, kinds[3] = {1, 1, 0};
+        for (int i = 0; i < 3; ++i) {
+            const TensorView& b = model.require(pre + bias_names[i]);
+            if (b.type != kF32 || b.size != counts[i] * 4) fail(Status::FormatError, "bias shape mismatch: " + b.name);
+            TensorRef ref;
+            ref.offset = offsets[i];
+            ref.kind = kinds[i];
+            ref.head_dim = p.head_dim;
+            for (uint32_t r = 0; r < counts[i]; ++r) {
+                const uint32_t dr = device_row(ref, r);
+                order[dr] = {parts[i], r};
+                bias[dr] = reinterpret_cast<const float*>(b.data)[r];
+            }
+            weight_bytes_ += b.size;
+        }
+        L.qkv = &upload_rows(pre + "attn_qkv", wq.type, wq.shape[0], order, bias.data());
+        for (int i = 0; i < 3; ++i) add_ref(*parts[i], *L.qkv, offsets[i], kinds[i]);
+        // gate/up interleaved in groups of kGluGroup rows
+        std::vector<RowSource> glu(2 * p.n_ff);
+        for (uint32_t r = 0; r < p.n_ff; ++r) {
+            TensorRef g, u;
+            g.kind = 2;
+            u.kind = 3;
+            glu[device_row(g, r)] = {&gate, r};
+            glu[device_row(u, r)] = {&up, r};
+        }
+        L.gate_up = &upload_rows(pre + "ffn_gate_up", gate.type, gate.shape[0], glu, nullptr);
+        add_ref(gate, *L.gate_up, 0, 2);
+        add_ref(up, *L.gate_up, 0, 3);
+        L.o = &upload_single(model.require(pre + "attn_output.weight"));
+        L.down = &upload_single(model.require(pre + "ffn_down.weight"));
+        for (const DeviceTensor* t : {L.qkv, L.o, L.gate_up, L.down}) {
             if (quantized(t->mat.type) && t->mat.cols % gpu::kActBlock != 0) {
                 fail(Status::FormatError, "quantized matrices need row lengths that are multiples of 256");
             }
@@ -209,25 +317,17 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
     if (quantized(output_->mat.type) && output_->mat.cols % gpu::kActBlock != 0) {
         fail(Status::FormatError, "quantized matrices need row lengths that are multiples of 256");
     }
-    quantized_act_ = p.n_embd % gpu::kActBlock == 0 && p.n_ff % gpu::kActBlock == 0;
 
     const int32_t H = static_cast<int32_t>(p.n_embd), F = static_cast<int32_t>(p.n_ff);
-    const int32_t kv = static_cast<int32_t>(p.n_head_kv * p.head_dim);
-    kmax_ = (std::max(H, F) + 255) / 256 * 256;
     const size_t R = gpu::kMaxRows;
     h_ = static_cast<float*>(device_alloc(R * H * sizeof(float)));
-    act_.q = static_cast<int8_t*>(device_alloc(R * kmax_));
-    act_.d = static_cast<float*>(device_alloc(R * (kmax_ / 256) * sizeof(float)));
-    act_.s = static_cast<int16_t*>(device_alloc(R * (kmax_ / 16) * sizeof(int16_t)));
-    act_.f = static_cast<float*>(device_alloc(R * kmax_ * sizeof(float)));
-    act_.stride = kmax_;
-    qkv_ = static_cast<float*>(device_alloc(R * (H + 2 * kv) * sizeof(float)));
-    q_ = static_cast<float*>(device_alloc(R * H * sizeof(float)));
+    q_ = static_cast<float*>(device_alloc(R * Hq * sizeof(float)));
+    attn_ = static_cast<float*>(device_alloc(R * Hq * sizeof(float)));
     ffn_ = static_cast<float*>(device_alloc(R * F * sizeof(float)));
     logits_ = static_cast<float*>(device_alloc(R * static_cast<size_t>(p.n_vocab) * sizeof(float)));
     best_ = static_cast<unsigned long long*>(device_alloc(R * sizeof(unsigned long long)));
     // attention split counters: zero here, and every kernel that uses them leaves them zero
-    const size_t n_counters = static_cast<size_t>(gpu::kMaxSeq) * p.n_head_kv;
+    const size_t n_counters = static_cast<size_t>(gpu::kMaxSeq) * p.n_head_kv * gpu::kMaxAttnQGroups;
     counters_ = static_cast<int32_t*>(device_alloc(n_counters * sizeof(int32_t)));
     hip_check(hipMemset(counters_, 0, n_counters * sizeof(int32_t)), "clear attention counters");
     step_dev_ = static_cast<gpu::StepDev*>(device_alloc(sizeof(gpu::StepDev)));
@@ -262,7 +362,8 @@ void Engine::ensure_capacity(uint32_t capacity) {
     hip_check(hipMalloc(&rope_, table.size() * sizeof(float)), "allocate rope table");
     hip_check(hipMemcpy(rope_, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice), "upload rope table");
     splits_ = gpu::attention_splits(static_cast<int32_t>(cap));
-    const size_t partial_floats = static_cast<size_t>(gpu::kMaxRows) * p.n_head * splits_ * (p.head_dim + 2);
+    const size_t partial_floats = gpu::attention_partial_floats(gpu::kMaxRows, static_cast<int32_t>(p.n_head),
+                                                                static_cast<int32_t>(p.head_dim), splits_);
     if (partial_) (void) hipFree(partial_);
     partial_ = nullptr;
     hip_check(hipMalloc(&partial_, partial_floats * sizeof(float)), "allocate attention partials");
@@ -285,28 +386,32 @@ namespace {
 uint64_t mat_bytes(const gpu::DMat& m) { return static_cast<uint64_t>(m.rows) * row_bytes(m.type, m.cols); }
 
 std::string gemv_label(const gpu::GemvArgs& a) {
-    const uint32_t t = a.mat[0].type;
+    const uint32_t t = a.mat.type;
     const bool fl = t == kF32 || t == kF16;
     const int nt = a.n_tok > 8 ? 8 : a.n_tok;
     return std::string(fl ? "k_gemv_f<" : "k_gemv_q<") + (fl ? "" : std::to_string(t) + ",") + std::to_string(nt) + ">";
 }
 
-// Algorithmic HBM bytes of one matmul launch: encoded weights, the activation
-// rows (int8 + scales + sums), bias, and the output rows (read too for residual adds).
+// Algorithmic HBM bytes of one matmul launch: encoded weights and bias, the
+// float activation rows (and norm gain), and what the epilogue writes (and
+// reads back for residual adds).
 double gemv_bytes(const gpu::GemvArgs& a) {
-    double w = 0.0, rows = 0.0;
-    for (int i = 0; i < a.n_mat; ++i) {
-        w += static_cast<double>(mat_bytes(a.mat[i]));
-        rows += a.mat[i].rows;
-        if (a.mat[i].bias) w += 4.0 * a.mat[i].rows;
+    const double rows = a.mat.rows, K = a.mat.cols, n = a.n_tok;
+    double w = static_cast<double>(mat_bytes(a.mat)) + (a.mat.bias ? 4.0 * rows : 0.0);
+    double in = n * K * 4.0 + (a.x.gain ? K * 4.0 : 0.0);
+    double out = n * rows * 4.0;
+    switch (a.mode) {
+    case gpu::kAdd: out *= 2.0; break;
+    case gpu::kSwiGLU: out = n * rows / 2 * 4.0; break;
+    case gpu::kLogits: out = a.store_logits ? out : 0.0; break;
+    case gpu::kQKV: {
+        const double hq = static_cast<double>(a.qkv.n_head) * a.qkv.head_dim;
+        out = n * hq * 4.0 + n * (rows - hq) * 2.0;
+        break;
     }
-    const double K = a.mat[0].cols;
-    const double act = a.n_tok * (K + K / 256 * 4 + K / 16 * 2);
-    double out = a.n_tok * rows * 4.0;
-    if (a.mode == gpu::kSwiGLU) out = a.n_tok * a.mat[0].rows * 4.0;
-    if (a.mode == gpu::kAdd) out *= 2.0;
-    if (a.mode == gpu::kLogits && !a.store_logits) out = 0.0;
-    return w + act + out;
+    default: break;
+    }
+    return w + in + out;
 }
 
 }  // namespace
@@ -331,83 +436,65 @@ void Engine::timed(const std::string& label, double bytes, F&& fn) {
 void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_out, bool store_logits) {
     const ModelParams& p = params_;
     const int32_t H = static_cast<int32_t>(p.n_embd), F = static_cast<int32_t>(p.n_ff);
-    const int32_t kv = static_cast<int32_t>(p.n_head_kv * p.head_dim);
+    const int32_t Hq = static_cast<int32_t>(p.n_head * p.head_dim);
     const double n = n_rows;
-    const double norm_bytes = n * H * (4.0 + 4.0 + 1.0) + 4.0 * H;
     hipStream_t s = stream_;
-    timed("k_embed", n * H * (4.0 + static_cast<double>(row_bytes(embd_->mat.type, H))), [&] {
+    timed("k_embed", n * H * 4.0 + n * static_cast<double>(row_bytes(embd_->mat.type, H)), [&] {
         gpu::launch_embed(embd_->mat, step_dev_, h_, n_rows, H, best_, gpu::kMaxRows, s);
     });
     for (uint32_t l = 0; l < p.n_layer; ++l) {
         const Layer& L = layers_[l];
-        timed("k_norm_quant", norm_bytes, [&] {
-            gpu::launch_norm_quant(h_, H, L.attn_norm, p.rms_eps, H, step_dev_, 0, n_rows, quantized_act_, act_, s);
-        });
         gpu::GemvArgs qkv;
-        qkv.n_mat = 3;
-        qkv.mat[0] = L.q->mat;
-        qkv.mat[0].bias = L.bq;
-        qkv.mat[1] = L.k->mat;
-        qkv.mat[1].bias = L.bk;
-        qkv.mat[2] = L.v->mat;
-        qkv.mat[2].bias = L.bv;
-        qkv.mode = gpu::kStore;
+        qkv.mat = L.qkv->mat;
+        qkv.mode = gpu::kQKV;
         qkv.n_tok = n_rows;
-        qkv.x = act_;
-        qkv.y = qkv_;
-        qkv.y_stride = H + 2 * kv;
+        qkv.x = {h_, H, nullptr, L.attn_norm, p.rms_eps};
+        qkv.qkv.step = step_dev_;
+        qkv.qkv.rope = rope_;
+        qkv.qkv.q = q_;
+        qkv.qkv.layer = static_cast<int32_t>(l);
+        qkv.qkv.n_head = static_cast<int32_t>(p.n_head);
+        qkv.qkv.n_head_kv = static_cast<int32_t>(p.n_head_kv);
+        qkv.qkv.head_dim = static_cast<int32_t>(p.head_dim);
         timed(gemv_label(qkv) + ":qkv", gemv_bytes(qkv), [&] { gpu::launch_gemv(qkv, s); });
-        timed("k_rope_kv", n * (H + 2 * kv) * 4.0 + n * H * 4.0 + n * 2 * kv * 2.0, [&] {
-            gpu::launch_rope_kv(qkv_, n_rows, static_cast<int32_t>(p.n_head), static_cast<int32_t>(p.n_head_kv),
-                                static_cast<int32_t>(p.head_dim), rope_, step_dev_, static_cast<int32_t>(l), q_, s);
-        });
-        timed("k_attention", n * H * 8.0, [&] {
-            gpu::launch_attention(q_, step_dev_, n_rows, max_len, n_seq, static_cast<int32_t>(l),
-                                  static_cast<int32_t>(p.n_head), static_cast<int32_t>(p.n_head_kv),
-                                  static_cast<int32_t>(p.head_dim), splits_, partial_, counters_, act_, s);
+        timed("k_attention", attn_kv_bytes_ + n * Hq * 8.0, [&] {
+            gpu::launch_attention(q_, step_dev_, max_len, n_seq, static_cast<int32_t>(l), static_cast<int32_t>(p.n_head),
+                                  static_cast<int32_t>(p.n_head_kv), static_cast<int32_t>(p.head_dim), splits_, partial_,
+                                  counters_, attn_, s);
         });
         gpu::GemvArgs o;
-        o.mat[0] = L.o->mat;
+        o.mat = L.o->mat;
         o.mode = gpu::kAdd;
         o.n_tok = n_rows;
-        o.x = act_;
+        o.x = {attn_, Hq, nullptr, nullptr, 0.0F};
         o.y = h_;
         o.y_stride = H;
         timed(gemv_label(o) + ":attn_output", gemv_bytes(o), [&] { gpu::launch_gemv(o, s); });
-        timed("k_norm_quant", norm_bytes, [&] {
-            gpu::launch_norm_quant(h_, H, L.ffn_norm, p.rms_eps, H, step_dev_, 0, n_rows, quantized_act_, act_, s);
-        });
         gpu::GemvArgs gu;
-        gu.n_mat = 2;
-        gu.mat[0] = L.gate->mat;
-        gu.mat[1] = L.up->mat;
+        gu.mat = L.gate_up->mat;
         gu.mode = gpu::kSwiGLU;
         gu.n_tok = n_rows;
-        gu.x = act_;
+        gu.x = {h_, H, nullptr, L.ffn_norm, p.rms_eps};
         gu.y = ffn_;
         gu.y_stride = F;
         timed(gemv_label(gu) + ":ffn_gate_up", gemv_bytes(gu), [&] { gpu::launch_gemv(gu, s); });
-        timed("k_quant", n * F * (4.0 + 4.0 + 1.0), [&] {
-            gpu::launch_quant(ffn_, F, F, n_rows, quantized_act_, act_, s);
-        });
         gpu::GemvArgs dn;
-        dn.mat[0] = L.down->mat;
+        dn.mat = L.down->mat;
         dn.mode = gpu::kAdd;
         dn.n_tok = n_rows;
-        dn.x = act_;
+        dn.x = {ffn_, F, nullptr, nullptr, 0.0F};
         dn.y = h_;
         dn.y_stride = H;
         timed(gemv_label(dn) + ":ffn_down", gemv_bytes(dn), [&] { gpu::launch_gemv(dn, s); });
     }
     if (n_out > 0) {
-        timed("k_norm_quant", static_cast<double>(n_out) * H * 9.0 + 4.0 * H, [&] {
-            gpu::launch_norm_quant(h_, H, output_norm_, p.rms_eps, H, step_dev_, 1, n_out, quantized_act_, act_, s);
-        });
         gpu::GemvArgs head;
-        head.mat[0] = output_->mat;
+        head.mat = output_->mat;
         head.mode = gpu::kLogits;
         head.n_tok = n_out;
-        head.x = act_;
+        const int32_t* out_rows =
+            reinterpret_cast<const int32_t*>(reinterpret_cast<const char*>(step_dev_) + offsetof(gpu::StepDev, out_row));
+        head.x = {h_, H, out_rows, output_norm_, p.rms_eps};
         head.y = logits_;
         head.y_stride = static_cast<int32_t>(p.n_vocab);
         head.best = best_;
@@ -523,6 +610,10 @@ void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int
         max_len = std::max(max_len, static_cast<int32_t>(st.n));
     }
     sd.n_rows = rows;
+    attn_kv_bytes_ = 0.0;
+    for (size_t si = 0; si < steps.size(); ++si) {
+        attn_kv_bytes_ += 2.0 * p.n_head_kv * p.head_dim * 2.0 * (sd.seqs[si].pos0 + sd.seqs[si].len);
+    }
     sd.n_seq = static_cast<int32_t>(steps.size());
     sd.n_out = outs;
     const bool store = logits != nullptr && outs > 0;
@@ -597,15 +688,19 @@ int32_t Engine::prefill(Session& s, const int32_t* tokens, uint32_t n, float* lo
 
 void Engine::dequantize(const std::string& name, uint32_t row0, uint32_t n_rows, float* out_host) {
     std::lock_guard lock(mutex_);
-    auto it = tensors_.find(name);
-    if (it == tensors_.end()) fail(Status::NotFound, "tensor is not resident as a matrix: " + name);
-    const gpu::DMat& m = it->second.mat;
-    if (n_rows == 0 || static_cast<uint64_t>(row0) + n_rows > m.rows) fail(Status::InvalidArgument, "row range is outside the tensor");
+    const TensorRef& ref = find_ref(name);
+    const gpu::DMat& m = ref.dev->mat;
+    if (n_rows == 0 || static_cast<uint64_t>(row0) + n_rows > ref.rows) {
+        fail(Status::InvalidArgument, "row range is outside the tensor");
+    }
     float* dev = nullptr;
     const size_t bytes = static_cast<size_t>(n_rows) * m.cols * sizeof(float);
     hip_check(hipMalloc(&dev, bytes), "allocate dequant output");
     try {
-        gpu::launch_dequant_rows(m, static_cast<int32_t>(row0), static_cast<int32_t>(n_rows), dev, stream_);
+        for (uint32_t i = 0; i < n_rows; ++i) {
+            gpu::launch_dequant_rows(m, static_cast<int32_t>(device_row(ref, row0 + i)), 1,
+                                     dev + static_cast<size_t>(i) * m.cols, stream_);
+        }
         hip_check(hipMemcpyAsync(out_host, dev, bytes, hipMemcpyDeviceToHost, stream_), "download dequant");
         hip_check(hipStreamSynchronize(stream_), "dequant");
     } catch (...) {
@@ -617,37 +712,46 @@ void Engine::dequantize(const std::string& name, uint32_t row0, uint32_t n_rows,
 
 void Engine::matmul(const std::string& name, const float* x_host, uint32_t n_tok, float* y_host) {
     std::lock_guard lock(mutex_);
-    auto it = tensors_.find(name);
-    if (it == tensors_.end()) fail(Status::NotFound, "tensor is not resident as a matrix: " + name);
-    const gpu::DMat& m = it->second.mat;
-    if (n_tok == 0 || n_tok > static_cast<uint32_t>(gpu::kMaxRows) || m.cols > static_cast<uint32_t>(kmax_)) {
+    const TensorRef& ref = find_ref(name);
+    const gpu::DMat& m = ref.dev->mat;
+    if (n_tok == 0 || n_tok > static_cast<uint32_t>(gpu::kMaxRows)) {
         fail(Status::InvalidArgument, "matmul shape is outside the engine workspace");
     }
-    hip_check(hipMemcpy2DAsync(act_.f, static_cast<size_t>(kmax_) * sizeof(float), x_host, m.cols * sizeof(float),
-                               m.cols * sizeof(float), n_tok, hipMemcpyHostToDevice, stream_),
-              "upload activations");
-    const bool q = quantized(m.type);
-    gpu::launch_quant(act_.f, kmax_, static_cast<int32_t>(m.cols), static_cast<int32_t>(n_tok), q, act_, stream_);
-    float* y = nullptr;
-    const size_t bytes = static_cast<size_t>(n_tok) * m.rows * sizeof(float);
-    hip_check(hipMalloc(&y, bytes), "allocate matmul output");
-    gpu::GemvArgs a;
-    a.mat[0] = m;
-    a.mat[0].bias = nullptr;
-    a.mode = gpu::kStore;
-    a.n_tok = static_cast<int32_t>(n_tok);
-    a.x = act_;
-    a.y = y;
-    a.y_stride = static_cast<int32_t>(m.rows);
+    // the whole device matrix runs through the kernels; the tensor's rows are gathered afterwards
+    const size_t x_bytes = static_cast<size_t>(n_tok) * m.cols * sizeof(float);
+    const size_t y_bytes = static_cast<size_t>(n_tok) * m.rows * sizeof(float);
+    float *x = nullptr, *y = nullptr;
+    hip_check(hipMalloc(&x, x_bytes), "allocate matmul input");
+    if (hipMalloc(&y, y_bytes) != hipSuccess) {
+        (void) hipFree(x);
+        fail(Status::OutOfMemory, "allocate matmul output");
+    }
+    std::vector<float> full(static_cast<size_t>(n_tok) * m.rows);
     try {
+        hip_check(hipMemcpyAsync(x, x_host, x_bytes, hipMemcpyHostToDevice, stream_), "upload activations");
+        gpu::GemvArgs a;
+        a.mat = m;
+        a.mat.bias = nullptr;
+        a.mode = gpu::kStore;
+        a.n_tok = static_cast<int32_t>(n_tok);
+        a.x = {x, static_cast<int32_t>(m.cols), nullptr, nullptr, 0.0F};
+        a.y = y;
+        a.y_stride = static_cast<int32_t>(m.rows);
         gpu::launch_gemv(a, stream_);
-        hip_check(hipMemcpyAsync(y_host, y, bytes, hipMemcpyDeviceToHost, stream_), "download matmul");
+        hip_check(hipMemcpyAsync(full.data(), y, y_bytes, hipMemcpyDeviceToHost, stream_), "download matmul");
         hip_check(hipStreamSynchronize(stream_), "matmul");
     } catch (...) {
+        (void) hipFree(x);
         (void) hipFree(y);
         throw;
     }
+    (void) hipFree(x);
     (void) hipFree(y);
+    for (uint32_t t = 0; t < n_tok; ++t) {
+        for (uint32_t r = 0; r < ref.rows; ++r) {
+            y_host[static_cast<size_t>(t) * ref.rows + r] = full[static_cast<size_t>(t) * m.rows + device_row(ref, r)];
+        }
+    }
 }
 
 }  // namespace jfh

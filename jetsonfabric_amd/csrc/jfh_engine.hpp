@@ -110,17 +110,31 @@ private:
     friend class Session;
     struct DeviceTensor {
         gpu::DMat mat;
-        void* main = nullptr;
-        void* aux = nullptr;
-        void* bias_alloc = nullptr;
-        uint64_t bytes = 0;
+        uint64_t bytes = 0;  // encoded GGML bytes of the rows it holds
+    };
+    // Where a model tensor's rows live: rows of a (possibly fused) device matrix.
+    struct TensorRef {
+        const DeviceTensor* dev = nullptr;
+        uint32_t rows = 0;     // rows of the model tensor
+        uint32_t offset = 0;   // first device row
+        uint32_t kind = 0;     // 0 contiguous, 1 RoPE pair order per head, 2 GLU gate rows, 3 GLU up rows
+        uint32_t head_dim = 0;
+    };
+    struct RowSource {
+        const TensorView* tensor;
+        uint32_t row;
     };
     struct Layer {
-        const DeviceTensor *q, *k, *v, *o, *gate, *up, *down;
-        const float *attn_norm, *ffn_norm, *bq, *bk, *bv;
+        const DeviceTensor *qkv, *o, *gate_up, *down;
+        const float *attn_norm, *ffn_norm;
     };
 
-    const DeviceTensor& upload(const TensorView& t);
+    static uint32_t device_row(const TensorRef& r, uint32_t row);
+    const DeviceTensor& upload_rows(const std::string& key, uint32_t type, uint64_t cols,
+                                    const std::vector<RowSource>& rows, const float* bias);
+    const DeviceTensor& upload_single(const TensorView& t);
+    void add_ref(const TensorView& t, const DeviceTensor& dev, uint32_t offset, uint32_t kind);
+    const TensorRef& find_ref(const std::string& name) const;
     const float* upload_f32(const TensorView& t);
     void ensure_capacity(uint32_t capacity);
     void record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_out, bool store_logits);
@@ -134,29 +148,28 @@ private:
         hipEvent_t end = nullptr;
     };
     std::vector<ProfEvent>* prof_ = nullptr;
+    double attn_kv_bytes_ = 0.0;  // K/V bytes one layer's attention reads in the step being recorded
     void* device_alloc(size_t bytes);
 
     ModelParams params_;
     EngineOptions options_;
     std::string device_name_;
     hipStream_t stream_ = nullptr;
-    std::map<std::string, DeviceTensor> tensors_;
+    std::map<std::string, DeviceTensor> matrices_;
+    std::map<std::string, TensorRef> refs_;
     std::vector<void*> allocations_;
     std::vector<Layer> layers_;
     const DeviceTensor* embd_ = nullptr;
     const DeviceTensor* output_ = nullptr;
     const float* output_norm_ = nullptr;
     uint64_t weight_bytes_ = 0;
-    bool quantized_act_ = true;
     uint32_t prefill_chunk_ = 8;
 
     // workspace
-    int32_t kmax_ = 0;
-    float* h_ = nullptr;
-    gpu::Act act_{};
-    float* qkv_ = nullptr;
-    float* q_ = nullptr;
-    float* ffn_ = nullptr;
+    float* h_ = nullptr;       // residual stream [row][n_embd]
+    float* q_ = nullptr;       // roped queries [row][n_embd]
+    float* attn_ = nullptr;    // attention output [row][n_embd]
+    float* ffn_ = nullptr;     // SwiGLU output [row][n_ff]
     float* logits_ = nullptr;
     unsigned long long* best_ = nullptr;
     gpu::StepDev* step_dev_ = nullptr;

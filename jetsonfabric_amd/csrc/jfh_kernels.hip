@@ -18,7 +18,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWave = 64;
-constexpr int kLdsActBytes = 32768;  // int8 activation bytes staged per K chunk
 
 __device__ __forceinline__ float h2f(uint32_t bits16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16 & 0xFFFFu)));
@@ -171,60 +170,6 @@ __device__ __forceinline__ void quant_block_wave(const float v[4], int lane, int
     if (lane == 0) *d = db;
 }
 
-// RMSNorm * gain of each selected row (qwen2_architecture.cpp:373-376), then
-// the int8 quantization consumed by the next matmul.
-// One wave per (256-value block, row): every wave reduces the whole row's sum
-// of squares itself (the row is a few KB, served from L2), then scales and
-// quantizes only its own block, so a row is spread over H/256 work-groups.
-__global__ __launch_bounds__(kWave) void k_norm_quant(const float* h, int32_t hs, const float* gain, float eps,
-                                                      int32_t H, const StepDev* step, int32_t select_out,
-                                                      int32_t quant, Act x) {
-    const int r = blockIdx.y, b = blockIdx.x, lane = threadIdx.x;
-    const int src = select_out ? step->out_row[r] : r;
-    const float* hr = h + static_cast<size_t>(src) * hs;
-    float ss = 0.0F;
-    for (int i = 4 * lane; i < H; i += 4 * kWave) {
-        const float4 v = *reinterpret_cast<const float4*>(hr + i);
-        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-    }
-    ss = wave_sum(ss);
-    const float mean = ss / static_cast<float>(H);
-    const float scale = 1.0F / sqrtf(mean + eps);
-    float v[4] = {0.0F, 0.0F, 0.0F, 0.0F};
-    float* xf = x.f + static_cast<size_t>(r) * x.stride;
-    const int e0 = b * kActBlock + 4 * lane;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (e0 + i < H) {
-            v[i] = (hr[e0 + i] * scale) * gain[e0 + i];
-            xf[e0 + i] = v[i];
-        }
-    }
-    if (!quant) return;
-    quant_block_wave(v, lane, x.q + static_cast<size_t>(r) * x.stride + b * kActBlock,
-                     x.d + static_cast<size_t>(r) * (x.stride / kActBlock) + b,
-                     x.s + static_cast<size_t>(r) * (x.stride / 16) + b * 16);
-}
-
-// Quantizes float rows (SwiGLU and attention outputs), one wave per
-// (256-value block, row), keeping the float copy when the source differs.
-__global__ __launch_bounds__(kWave) void k_quant(const float* src, int32_t ss, int32_t K, int32_t quant, Act x) {
-    const int r = blockIdx.y, b = blockIdx.x, lane = threadIdx.x;
-    const float* row = src + static_cast<size_t>(r) * ss;
-    const int e0 = b * kActBlock + 4 * lane;
-    float v[4] = {0.0F, 0.0F, 0.0F, 0.0F};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (e0 + i < K) {
-            v[i] = row[e0 + i];
-            if (x.f != src) x.f[static_cast<size_t>(r) * x.stride + e0 + i] = v[i];
-        }
-    }
-    if (!quant) return;
-    quant_block_wave(v, lane, x.q + static_cast<size_t>(r) * x.stride + b * kActBlock,
-                     x.d + static_cast<size_t>(r) * (x.stride / kActBlock) + b,
-                     x.s + static_cast<size_t>(r) * (x.stride / 16) + b * 16);
-}
 #pragma clang fp contract(on)
 
 // ------------------------------------------------------------------ quantized matmul
@@ -417,28 +362,46 @@ __device__ __forceinline__ void q80_compute(const Q80Regs& v, int part, const St
     }
 }
 
-template <uint32_t TYPE, int NT>
-__device__ __forceinline__ void block_dot(const RowRef& r, int gb, int part, const Staged& x, int lb, float* acc) {
-    if constexpr (TYPE == 11) {
-        q4k_compute<NT>(q4k_load(r, gb, part), part, x, lb, acc);
-    } else if constexpr (TYPE == 13) {
-        q6k_compute<NT>(q6k_load(r, gb, part), part, x, lb, acc);
-    } else if constexpr (TYPE == 9) {
-        q2k_compute<NT>(q2k_load(r, gb, part), part, x, lb, acc);
-    } else {
-        q80_compute<NT>(q80_load(r, gb, part), part, x, lb, acc);
+// Load/compute split per block type, so that a wave can issue the loads of
+// all of its rows (and two block iterations) before consuming any of them.
+template <uint32_t TYPE>
+struct QBlock;
+template <>
+struct QBlock<11> {
+    using Regs = Q4KRegs;
+    static __device__ __forceinline__ Regs load(const RowRef& r, int gb, int part) { return q4k_load(r, gb, part); }
+    template <int NT>
+    static __device__ __forceinline__ void dot(const Regs& v, int part, const Staged& x, int lb, float* acc) {
+        q4k_compute<NT>(v, part, x, lb, acc);
     }
-}
-
-// Which matrix and local row a concatenated row index belongs to.
-__device__ __forceinline__ int locate(const GemvArgs& a, int r, int& local) {
-    local = r;
-    for (int i = 0; i < a.n_mat; ++i) {
-        if (local < static_cast<int>(a.mat[i].rows)) return i;
-        local -= static_cast<int>(a.mat[i].rows);
+};
+template <>
+struct QBlock<13> {
+    using Regs = Q6KRegs;
+    static __device__ __forceinline__ Regs load(const RowRef& r, int gb, int part) { return q6k_load(r, gb, part); }
+    template <int NT>
+    static __device__ __forceinline__ void dot(const Regs& v, int part, const Staged& x, int lb, float* acc) {
+        q6k_compute<NT>(v, part, x, lb, acc);
     }
-    return -1;
-}
+};
+template <>
+struct QBlock<9> {
+    using Regs = Q2KRegs;
+    static __device__ __forceinline__ Regs load(const RowRef& r, int gb, int part) { return q2k_load(r, gb, part); }
+    template <int NT>
+    static __device__ __forceinline__ void dot(const Regs& v, int part, const Staged& x, int lb, float* acc) {
+        q2k_compute<NT>(v, part, x, lb, acc);
+    }
+};
+template <>
+struct QBlock<7> {
+    using Regs = Q80Regs;
+    static __device__ __forceinline__ Regs load(const RowRef& r, int gb, int part) { return q80_load(r, gb, part); }
+    template <int NT>
+    static __device__ __forceinline__ void dot(const Regs& v, int part, const Staged& x, int lb, float* acc) {
+        q80_compute<NT>(v, part, x, lb, acc);
+    }
+};
 
 __device__ __forceinline__ unsigned long long pack_best(float v, uint32_t idx) {
     uint32_t u = __float_as_uint(v);
@@ -446,256 +409,407 @@ __device__ __forceinline__ unsigned long long pack_best(float v, uint32_t idx) {
     return (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFu - idx);
 }
 
-// Shared epilogue: values of the wave's two weight rows for every token.
+// Sum over the 4 lanes of a quad (DPP quad permutations [1,0,3,2], [2,3,0,1]).
+__device__ __forceinline__ float quad_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+    return v;
+}
+
+__device__ __forceinline__ const float* x_row(const XIn& x, int t) {
+    return x.x + static_cast<size_t>(x.gather ? x.gather[t] : t) * x.stride;
+}
+
+// 1/sqrt(mean(x^2) + eps) of each token row (qwen2_architecture.cpp:373-376),
+// reduced by the whole work-group into rs[t].
 template <int NT>
-__device__ void gemv_epilogue(const GemvArgs& a, const int mi[2], const int lr[2], const int gr[2], float acc[2][NT],
-                              int wave, int lane) {
-    __shared__ float best_v[kThreads / kWave][NT];
-    __shared__ uint32_t best_i[kThreads / kWave][NT];
-    if (a.mode == kLogits) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            float bv = -INFINITY;
-            uint32_t bi = 0xFFFFFFFFu;
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                if (mi[k] < 0) continue;
-                float v = acc[k][t];
-                if (a.mat[mi[k]].bias) v += a.mat[mi[k]].bias[lr[k]];
-                if (a.store_logits && lane == 0 && t < a.n_tok) a.y[static_cast<size_t>(t) * a.y_stride + gr[k]] = v;
-                if (v > bv || (v == bv && static_cast<uint32_t>(gr[k]) < bi)) { bv = v; bi = static_cast<uint32_t>(gr[k]); }
-            }
-            if (lane == 0) { best_v[wave][t] = bv; best_i[wave][t] = bi; }
-        }
-        __syncthreads();
-        if (threadIdx.x < static_cast<unsigned>(a.n_tok) && threadIdx.x < NT) {
-            const int t = threadIdx.x;
-            float bv = -INFINITY;
-            uint32_t bi = 0xFFFFFFFFu;
-            for (int w = 0; w < kThreads / kWave; ++w) {
-                if (best_i[w][t] == 0xFFFFFFFFu) continue;
-                if (best_v[w][t] > bv || (best_v[w][t] == bv && best_i[w][t] < bi)) { bv = best_v[w][t]; bi = best_i[w][t]; }
-            }
-            if (bi != 0xFFFFFFFFu) atomicMax(a.best + t, pack_best(bv, bi));
-        }
-        return;
-    }
-    if (lane != 0) return;
-    if (a.mode == kSwiGLU) {
-        if (mi[0] < 0) return;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            if (t >= a.n_tok) break;
-            const float g = acc[0][t], u = acc[1][t];
-            a.y[static_cast<size_t>(t) * a.y_stride + lr[0]] = g / (1.0F + expf(-g)) * u;
-        }
-        return;
-    }
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        if (mi[k] < 0) continue;
-        const float b = a.mat[mi[k]].bias ? a.mat[mi[k]].bias[lr[k]] : 0.0F;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            if (t >= a.n_tok) break;
-            float* out = a.y + static_cast<size_t>(t) * a.y_stride + gr[k];
-            if (a.mode == kAdd) *out += acc[k][t];
-            else *out = acc[k][t] + b;
-        }
-    }
-}
-
-__device__ __forceinline__ void wave_rows(const GemvArgs& a, int wave_global, int mi[2], int lr[2], int gr[2]) {
-    if (a.mode == kSwiGLU) {
-        const int r = wave_global;
-        const bool ok = r < static_cast<int>(a.mat[0].rows);
-        mi[0] = ok ? 0 : -1;
-        mi[1] = ok ? 1 : -1;
-        lr[0] = lr[1] = r;
-        gr[0] = gr[1] = r;
-    } else {
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            gr[k] = 2 * wave_global + k;
-            mi[k] = locate(a, gr[k], lr[k]);
-        }
-    }
-}
-
-template <uint32_t TYPE, int NT>
-__global__ __launch_bounds__(kThreads) void k_gemv_q(GemvArgs a, int32_t chunk) {
-    extern __shared__ __align__(16) uint8_t lds_raw[];
-    int8_t* sq = reinterpret_cast<int8_t*>(lds_raw);
-    float* sd = reinterpret_cast<float*>(lds_raw + NT * chunk);
-    int16_t* ss = reinterpret_cast<int16_t*>(sd + NT * (chunk / 256));
+__device__ void row_rms(const XIn& x, int n_tok, int K, float* rs, float* red) {
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int part = lane & 3, slot = lane >> 2;
-    int mi[2], lr[2], gr[2];
-    wave_rows(a, blockIdx.x * (kThreads / kWave) + wave, mi, lr, gr);
-    RowRef rows[2];
+    for (int t = 0; t < n_tok; ++t) {
+        const float* xr = x_row(x, t);
+        float ss = 0.0F;
+        for (int i0 = 4 * threadIdx.x; i0 < K; i0 += 4 * 4 * kThreads) {
+            float4 v[4];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        rows[k].valid = mi[k] >= 0;
-        const DMat& m = a.mat[rows[k].valid ? mi[k] : 0];
-        rows[k].main = m.main + static_cast<size_t>(rows[k].valid ? lr[k] : 0) * m.main_row_bytes;
-        rows[k].aux = m.aux ? m.aux + static_cast<size_t>(rows[k].valid ? lr[k] : 0) * m.aux_row_bytes : nullptr;
-    }
-    float acc[2][NT];
+            for (int u = 0; u < 4; ++u) {
+                const int i = i0 + u * 4 * kThreads;
+                v[u] = i < K ? *reinterpret_cast<const float4*>(xr + i) : make_float4(0.0F, 0.0F, 0.0F, 0.0F);
+            }
 #pragma unroll
-    for (int k = 0; k < 2; ++k)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[k][t] = 0.0F;
-
-    const int K = static_cast<int>(a.mat[0].cols);
-    const Staged st{sq, sd, ss, chunk};
-    for (int c0 = 0; c0 < K; c0 += chunk) {
-        const int ce = min(chunk, K - c0);
-        __syncthreads();
-        for (int t = 0; t < NT; ++t) {
-            const int8_t* gq = a.x.q + static_cast<size_t>(t) * a.x.stride + c0;
-            for (int i = threadIdx.x * 16; i < ce; i += kThreads * 16) {
-                *reinterpret_cast<uint4*>(sq + t * chunk + i) = *reinterpret_cast<const uint4*>(gq + i);
-            }
-            for (int i = threadIdx.x; i < ce / 256; i += kThreads) {
-                sd[t * (chunk / 256) + i] = a.x.d[static_cast<size_t>(t) * (a.x.stride / 256) + c0 / 256 + i];
-            }
-            for (int i = threadIdx.x; i < ce / 16; i += kThreads) {
-                ss[t * (chunk / 16) + i] = a.x.s[static_cast<size_t>(t) * (a.x.stride / 16) + c0 / 16 + i];
-            }
+            for (int u = 0; u < 4; ++u) ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
         }
-        __syncthreads();
-        const int nb = ce / 256;
-        for (int lb = slot; lb < nb; lb += kWave / 4) {
-            const int gb = c0 / 256 + lb;
-            if (rows[0].valid) block_dot<TYPE, NT>(rows[0], gb, part, st, lb, acc[0]);
-            if (rows[1].valid) block_dot<TYPE, NT>(rows[1], gb, part, st, lb, acc[1]);
-        }
+        ss = wave_sum(ss);
+        if (lane == 0) red[t * (kThreads / kWave) + wave] = ss;
     }
-#pragma unroll
-    for (int k = 0; k < 2; ++k)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[k][t] = wave_sum(acc[k][t]);
-    gemv_epilogue<NT>(a, mi, lr, gr, acc, wave, lane);
+    __syncthreads();
+    if (threadIdx.x < static_cast<unsigned>(n_tok)) {
+        const int t = threadIdx.x;
+        float ss = 0.0F;
+        for (int w = 0; w < kThreads / kWave; ++w) ss += red[t * (kThreads / kWave) + w];
+        rs[t] = 1.0F / sqrtf(ss / static_cast<float>(K) + x.eps);
+    }
+    __syncthreads();
 }
 
-// Float weights (F32/F16): float activations, lanes stride over the row.
-template <int NT>
-__global__ __launch_bounds__(kThreads) void k_gemv_f(GemvArgs a) {
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    int mi[2], lr[2], gr[2];
-    wave_rows(a, blockIdx.x * (kThreads / kWave) + wave, mi, lr, gr);
-    float acc[2][NT];
-#pragma unroll
-    for (int k = 0; k < 2; ++k)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[k][t] = 0.0F;
-    const int K = static_cast<int>(a.mat[0].cols);
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        if (mi[k] < 0) continue;
-        const DMat& m = a.mat[mi[k]];
-        for (int c = lane; c < K; c += kWave) {
-            const float w = dequant_elem(m, static_cast<uint32_t>(lr[k]), static_cast<uint32_t>(c));
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                if (t < a.n_tok) acc[k][t] += w * a.x.f[static_cast<size_t>(t) * a.x.stride + c];
-            }
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < 2; ++k)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[k][t] = wave_sum(acc[k][t]);
-    gemv_epilogue<NT>(a, mi, lr, gr, acc, wave, lane);
-}
-
-// ------------------------------------------------------------------ RoPE + KV write
+// Quantizes values [c0, c0 + nb*256) of every token row into the LDS chunk
+// (int8, scale per 256 values, int16 sums per 16), one wave per 256-value
+// block, loads issued four blocks at a time.
 #pragma clang fp contract(off)
-// NEOX rotation of q and k heads (qwen2_architecture.cpp:499-506) with the
-// shared cos/sin table; k and v rows are stored as f16 at the row's position.
-__global__ __launch_bounds__(kThreads) void k_rope_kv(const float* qkv, int32_t n_head, int32_t n_head_kv,
-                                                      int32_t hd, const float* rope, const StepDev* step,
-                                                      int32_t layer, float* qout) {
-    const int r = blockIdx.x;
-    if (r >= step->n_rows) return;
-    const int H = n_head * hd, kv = n_head_kv * hd, half = hd / 2;
-    const int pos = step->pos[r];
-    const SeqDev& sd = step->seqs[step->seq[r]];
-    const float* src = qkv + static_cast<size_t>(r) * (H + 2 * kv);
-    const float* cs = rope + static_cast<size_t>(pos) * hd;
-    for (int idx = threadIdx.x; idx < (n_head + n_head_kv) * half; idx += kThreads) {
-        const int head = idx / half, i = idx % half;
-        const float c = cs[2 * i], s = cs[2 * i + 1];
-        if (head < n_head) {
-            const float x0 = src[head * hd + i], x1 = src[head * hd + i + half];
-            float* o = qout + static_cast<size_t>(r) * H + head * hd;
-            o[i] = x0 * c - x1 * s;
-            o[i + half] = x0 * s + x1 * c;
-        } else {
-            const int kh = head - n_head;
-            const float x0 = src[H + kh * hd + i], x1 = src[H + kh * hd + i + half];
-            uint16_t* kr = sd.k + ((static_cast<size_t>(layer) * n_head_kv + kh) * sd.capacity + pos) * hd;
-            kr[i] = f2h(x0 * c - x1 * s);
-            kr[i + half] = f2h(x0 * s + x1 * c);
+template <int NT>
+__device__ void stage_chunk(const XIn& x, int n_tok, int c0, int nb, const float* rs, int8_t* sq, float* sd,
+                            int16_t* ss, int chunk) {
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    constexpr int W = kThreads / kWave;
+    const int total = n_tok * nb;
+    for (int j0 = wave; j0 < total; j0 += 4 * W) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int j = j0 + u * W;
+            if (j < total) {
+                const int t = j / nb, b = j - t * nb;
+                const int c = c0 + b * 256 + 4 * lane;
+                v[u] = *reinterpret_cast<const float4*>(x_row(x, t) + c);
+                if (x.gain) {
+                    const float r = rs[t];
+                    const float4 g = *reinterpret_cast<const float4*>(x.gain + c);
+                    v[u].x = v[u].x * r * g.x;
+                    v[u].y = v[u].y * r * g.y;
+                    v[u].z = v[u].z * r * g.z;
+                    v[u].w = v[u].w * r * g.w;
+                }
+            }
         }
-    }
-    for (int idx = threadIdx.x; idx < kv; idx += kThreads) {
-        const int kh = idx / hd, dd = idx % hd;
-        uint16_t* vr = sd.v + ((static_cast<size_t>(layer) * n_head_kv + kh) * sd.capacity + pos) * hd;
-        vr[dd] = f2h(src[H + kv + idx]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int j = j0 + u * W;
+            if (j < total) {
+                const int t = j / nb, b = j - t * nb;
+                const float vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+                quant_block_wave(vv, lane, sq + t * chunk + b * 256, sd + t * (chunk / 256) + b,
+                                 ss + t * (chunk / 16) + b * 16);
+            }
+        }
     }
 }
 #pragma clang fp contract(on)
 
+// Launch geometry of one quantized matmul, fixed by the host.
+struct GemvGeom {
+    int32_t rows_per_wg;  // rows of one work-group (even; a multiple of 2*kGluGroup for SwiGLU)
+    int32_t chunk;        // K values staged per pass (multiple of 256)
+    uint64_t nbc_magic;   // ceil(2^32 / nbc), nbc = chunk / 256: f / nbc = (f * magic) >> 32
+};
+
+#pragma clang fp contract(off)
+__device__ __forceinline__ void qkv_store(const GemvArgs& a, int t, int gr, float va, float vb, bool pair) {
+    // gr: first fused row of a rotated pair (q or k) or a v row (pair == false)
+    const QkvOut& o = a.qkv;
+    const int hd = o.head_dim, half = hd / 2, Hq = o.n_head * hd, kv = o.n_head_kv * hd;
+    const StepDev* st = o.step;
+    const int pos = st->pos[o.row0 + t];
+    const SeqDev& sd = st->seqs[st->seq[o.row0 + t]];
+    if (pair) {
+        const int region = gr < Hq ? 0 : 1;
+        const int g = region == 0 ? gr : gr - Hq;
+        const int head = g / hd, i = (g % hd) / 2;
+        const float c = o.rope[static_cast<size_t>(pos) * hd + 2 * i];
+        const float s = o.rope[static_cast<size_t>(pos) * hd + 2 * i + 1];
+        const float r0 = va * c - vb * s;
+        const float r1 = va * s + vb * c;
+        if (region == 0) {
+            float* q = o.q + static_cast<size_t>(t) * Hq + head * hd;
+            q[i] = r0;
+            q[i + half] = r1;
+        } else {
+            const size_t row = ((static_cast<size_t>(o.layer) * o.n_head_kv + head) * sd.capacity + pos) * hd;
+            sd.k[row + i] = f2h(r0);
+            sd.k[row + i + half] = f2h(r1);
+        }
+    } else {
+        const int g = gr - Hq - kv;
+        const int head = g / hd, dcol = g % hd;
+        const size_t row = ((static_cast<size_t>(o.layer) * o.n_head_kv + head) * sd.capacity + pos) * hd;
+        sd.v[row + dcol] = f2h(va);
+    }
+}
+#pragma clang fp contract(on)
+
+// Row results of a work-group (sums in LDS) -> bias / residual / SwiGLU /
+// RoPE + cache / greedy argmax. `sum(j, t)` returns the dot of local row j.
+template <int NT, typename Sum>
+__device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, float* lv) {
+    const int n = nrows * a.n_tok;
+    switch (a.mode) {
+    case kStore:
+    case kAdd:
+        for (int idx = threadIdx.x; idx < n; idx += kThreads) {
+            const int t = idx / nrows, j = idx - t * nrows, gr = row0 + j;
+            float* out = a.y + static_cast<size_t>(t) * a.y_stride + gr;
+            if (a.mode == kAdd) *out += sum(j, t);
+            else *out = sum(j, t) + (a.mat.bias ? a.mat.bias[gr] : 0.0F);
+        }
+        break;
+    case kSwiGLU: {
+        const int half = nrows / 2;
+        for (int idx = threadIdx.x; idx < half * a.n_tok; idx += kThreads) {
+            const int t = idx / half, jj = idx - t * half;
+            const int j = (jj / kGluGroup) * 2 * kGluGroup + jj % kGluGroup;
+            const float g = sum(j, t), u = sum(j + kGluGroup, t);
+            const int o = (row0 / 2) + jj;
+            a.y[static_cast<size_t>(t) * a.y_stride + o] = g / (1.0F + expf(-g)) * u;
+        }
+        break;
+    }
+    case kQKV: {
+        const int Hq = a.qkv.n_head * a.qkv.head_dim, kv = a.qkv.n_head_kv * a.qkv.head_dim;
+        for (int idx = threadIdx.x; idx < n; idx += kThreads) {
+            const int t = idx / nrows, j = idx - t * nrows, gr = row0 + j;
+            const float* bias = a.mat.bias;
+            if (gr < Hq + kv) {
+                if (gr & 1) continue;
+                qkv_store(a, t, gr, sum(j, t) + (bias ? bias[gr] : 0.0F), sum(j + 1, t) + (bias ? bias[gr + 1] : 0.0F),
+                          true);
+            } else {
+                qkv_store(a, t, gr, sum(j, t) + (bias ? bias[gr] : 0.0F), 0.0F, false);
+            }
+        }
+        break;
+    }
+    case kLogits: {
+        for (int idx = threadIdx.x; idx < n; idx += kThreads) {
+            const int t = idx / nrows, j = idx - t * nrows, gr = row0 + j;
+            const float v = sum(j, t) + (a.mat.bias ? a.mat.bias[gr] : 0.0F);
+            if (a.store_logits) a.y[static_cast<size_t>(t) * a.y_stride + gr] = v;
+            lv[idx] = v;
+        }
+        __syncthreads();
+        // one wave per token: lanes scan rows, then a wave argmax (first maximum)
+        const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+        for (int t = wave; t < a.n_tok; t += kThreads / kWave) {
+            float bv = -INFINITY;
+            int bi = -1;
+            for (int j = lane; j < nrows; j += kWave) {
+                const float v = lv[t * nrows + j];
+                if (bi < 0 || v > bv) {
+                    bv = v;
+                    bi = j;
+                }
+            }
+            unsigned long long p = bi < 0 ? 0ull : pack_best(bv, static_cast<uint32_t>(row0 + bi));
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const unsigned long long q = __shfl_xor(p, o);
+                p = q > p ? q : p;
+            }
+            if (lane == 0 && p != 0ull) atomicMax(a.best + t, p);
+        }
+        break;
+    }
+    default:
+        break;
+    }
+}
+
+// Quantized matmul. Work-group w owns rows [w*RW, w*RW + RW) and streams
+// their blocks as one flat list (row-major, so contiguous in memory): quad q
+// of the 64 lane quads takes flat blocks q, q + 64, ..., two per iteration
+// with both loads issued first. Each block's dot (4 lanes, one per quarter)
+// is quad-reduced and added to its own LDS slot; rows are then summed over
+// their slots in a fixed order, so results do not depend on scheduling.
+// The activation is quantized into LDS by the work-group itself (after the
+// optional RMSNorm), chunk by chunk when it does not fit at once.
+template <uint32_t TYPE, int NT>
+__global__ __launch_bounds__(kThreads) void k_gemv_q(GemvArgs a, GemvGeom g) {
+    using B = QBlock<TYPE>;
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    const int K = static_cast<int>(a.mat.cols);
+    const int chunk = g.chunk, nbc = chunk / 256, RW = g.rows_per_wg;
+    const int n_tok = NT;  // token groups are launched with exactly NT rows
+    int8_t* sq = reinterpret_cast<int8_t*>(lds_raw);
+    float* sd = reinterpret_cast<float*>(lds_raw + NT * chunk);
+    int16_t* ss = reinterpret_cast<int16_t*>(sd + NT * nbc);
+    float* part = reinterpret_cast<float*>(ss + NT * (chunk / 16));
+    float* small = part + RW * nbc * NT;  // rs[NT], red[NT*4], logits values [RW*NT]
+    float* rs = small;
+    float* red = small + NT;
+    float* lv = red + NT * (kThreads / kWave);
+
+    const int row0 = blockIdx.x * RW;
+    const int nrows = min(RW, static_cast<int>(a.mat.rows) - row0);
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int part_id = lane & 3, quad = wave * (kWave / 4) + (lane >> 2);
+    const Staged st{sq, sd, ss, chunk};
+
+    if (a.x.gain) row_rms<NT>(a.x, n_tok, K, rs, red);
+    for (int i = threadIdx.x; i < RW * nbc * NT; i += kThreads) part[i] = 0.0F;
+
+    const size_t rb = a.mat.main_row_bytes, ab = a.mat.aux_row_bytes;
+    const uint8_t* main0 = a.mat.main + static_cast<size_t>(row0) * rb;
+    const uint8_t* aux0 = a.mat.aux ? a.mat.aux + static_cast<size_t>(row0) * ab : nullptr;
+    const int total = nrows * nbc;
+    for (int c0 = 0; c0 < K; c0 += chunk) {
+        const int nb = min(chunk, K - c0) / 256;
+        __syncthreads();
+        stage_chunk<NT>(a.x, n_tok, c0, nb, rs, sq, sd, ss, chunk);
+        __syncthreads();
+        for (int f0 = quad; f0 < total; f0 += 2 * kWave) {
+            const int f1 = f0 + kWave;
+            const int r0 = static_cast<int>((static_cast<uint64_t>(f0) * g.nbc_magic) >> 32);
+            const int r1 = static_cast<int>((static_cast<uint64_t>(f1) * g.nbc_magic) >> 32);
+            const int b0 = f0 - r0 * nbc, b1 = f1 - r1 * nbc;
+            const bool ok0 = b0 < nb, ok1 = f1 < total && b1 < nb;
+            typename B::Regs v0, v1;
+            if (ok0) v0 = B::load(RowRef{main0 + r0 * rb, aux0 ? aux0 + r0 * ab : nullptr, true}, c0 / 256 + b0, part_id);
+            if (ok1) v1 = B::load(RowRef{main0 + r1 * rb, aux0 ? aux0 + r1 * ab : nullptr, true}, c0 / 256 + b1, part_id);
+            float s0[NT], s1[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                s0[t] = 0.0F;
+                s1[t] = 0.0F;
+            }
+            if (ok0) B::template dot<NT>(v0, part_id, st, b0, s0);
+            if (ok1) B::template dot<NT>(v1, part_id, st, b1, s1);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                s0[t] = quad_sum(s0[t]);
+                s1[t] = quad_sum(s1[t]);
+            }
+            if (part_id == 0) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    if (ok0) part[f0 * NT + t] += s0[t];
+                    if (ok1) part[f1 * NT + t] += s1[t];
+                }
+            }
+        }
+    }
+    __syncthreads();
+    gemv_epilogue<NT>(a, row0, nrows,
+                      [&](int j, int t) {
+                          float acc = 0.0F;
+                          const float* p = part + j * nbc * NT + t;
+                          for (int b = 0; b < nbc; ++b) acc += p[b * NT];
+                          return acc;
+                      },
+                      lv);
+}
+
+// Float weights (F32/F16, small models): one wave per row, lanes over K,
+// float activations (RMS-normalized in the prologue when a gain is given).
+template <int NT>
+__global__ __launch_bounds__(kThreads) void k_gemv_f(GemvArgs a, int32_t rows_per_wg) {
+    __shared__ float rs[NT], red[NT * (kThreads / kWave)];
+    __shared__ float sums[kThreads / kWave * 2][NT];
+    extern __shared__ float lv_f[];
+    const int K = static_cast<int>(a.mat.cols);
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int n_tok = a.n_tok < NT ? a.n_tok : NT;
+    if (a.x.gain) row_rms<NT>(a.x, n_tok, K, rs, red);
+    const int RW = rows_per_wg, row0 = blockIdx.x * RW;
+    const int nrows = min(RW, static_cast<int>(a.mat.rows) - row0);
+    for (int j = wave; j < RW; j += kThreads / kWave) {
+        float acc[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = 0.0F;
+        if (j < nrows) {
+            for (int c = lane; c < K; c += kWave) {
+                const float w = dequant_elem(a.mat, static_cast<uint32_t>(row0 + j), static_cast<uint32_t>(c));
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    if (t < n_tok) {
+                        float xv = x_row(a.x, t)[c];
+                        if (a.x.gain) xv = xv * rs[t] * a.x.gain[c];
+                        acc[t] += w * xv;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = wave_sum(acc[t]);
+        if (lane == 0 && j < nrows) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) sums[j][t] = acc[t];
+        }
+    }
+    __syncthreads();
+    GemvArgs b = a;
+    b.n_tok = n_tok;
+    gemv_epilogue<NT>(b, row0, nrows, [&](int j, int t) { return sums[j][t]; }, lv_f);
+}
+
 // ------------------------------------------------------------------ attention
 // Split-K causal GQA flash attention (qwen2_architecture.cpp:438-464, mask
-// 697-708) over the f16 cache. Work-group = (key split, kv head, sequence);
-// its 4 waves own disjoint slices of the query rows (G heads x T rows) that
-// share the kv head. Inside a wave each lane owns one key of a 64-key tile:
-// the lane loads its K row once and scores it against the wave's queries
-// (query values are wave-uniform, read through the scalar cache), the online
-// softmax keeps (max, sum, output) in registers, and for P.V the lanes switch
-// to owning two head dims each. The last work-group of a (sequence, kv head)
-// to finish merges the splits' partials (atomic counter, reset afterwards).
-constexpr int kAttnWaves = 4;
+// 697-708) over the f16 caches. Work-group = (key split, kv head x query
+// group, sequence); a query group is up to kAttnQPW of the G*T query rows that
+// share the kv head, staged in LDS. Each wave takes 16-key tiles: for Q.K a
+// quad of lanes holds one key (a quarter of its dims each) and the score is
+// quad-reduced; for P.V the lanes own two head dims each. K and V of a tile
+// are loaded together. The four waves' online-softmax states are merged in
+// LDS; with several splits the last work-group to finish (atomic counter,
+// reset by it) merges the splits' partials.
+constexpr int kAttnQPW = 8;
+constexpr int kAttnTile = 16;
+constexpr int kAttnWgKeys = kAttnTile * (kThreads / kWave);
 
-template <int QPW>
-__global__ __launch_bounds__(kAttnWaves * kWave) void k_attention(
-    const float* __restrict__ q, const StepDev* __restrict__ step, int32_t layer, int32_t n_head, int32_t n_head_kv,
-    int32_t hd, int32_t splits_max, float* __restrict__ partial, int32_t* __restrict__ counters,
-    float* __restrict__ out, int32_t out_stride) {
-    __shared__ float P[kAttnWaves][QPW][kWave];
-    __shared__ int32_t last;
+template <int HD>
+__device__ __forceinline__ void attn_load_k(const uint16_t* krow, int hd, int qq, uint4* kr) {
+    if constexpr (HD > 0) {
+#pragma unroll
+        for (int c = 0; c < HD / 32; ++c) kr[c] = *reinterpret_cast<const uint4*>(krow + qq * (HD / 4) + 8 * c);
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(kThreads) void k_attention(const float* __restrict__ q, const StepDev* __restrict__ step,
+                                                        int32_t layer, int32_t n_head, int32_t n_head_kv,
+                                                        int32_t hd_arg, int32_t splits_max, int32_t qgroups,
+                                                        float* __restrict__ partial, int32_t* __restrict__ counters,
+                                                        float* __restrict__ out) {
+    constexpr int QPW = kAttnQPW, W = kThreads / kWave;
+    constexpr int QS = (HD > 0 ? HD : 128) + 16;  // LDS row stride of a query (quarters padded by 4)
+    __shared__ __align__(16) float Qs[QPW][QS];
+    __shared__ __align__(16) float P[W][QPW][kAttnTile];
+    __shared__ float Ms[W][QPW], Ls[W][QPW];
+    __shared__ __align__(16) float Os[W][QPW][128];
+    __shared__ int last;
+    const int hd = HD > 0 ? HD : hd_arg;
+    const int DQ = hd / 4;
     const int seq = blockIdx.z;
     if (seq >= step->n_seq) return;
     const int32_t pos0 = step->seqs[seq].pos0, len = step->seqs[seq].len, row0 = step->seqs[seq].row0;
     const int32_t capacity = step->seqs[seq].capacity;
+    const int G = n_head / n_head_kv, NQ = G * len, H = n_head * hd;
+    const int kvh = blockIdx.y / qgroups, qg = blockIdx.y % qgroups;
+    const int q_begin = qg * QPW;
+    if (q_begin >= NQ) return;
+    const int nq = min(QPW, NQ - q_begin);
     const int n_keys = pos0 + len;
     int L = (n_keys + splits_max - 1) / splits_max;
-    L = (L + kWave - 1) / kWave * kWave;
+    L = (L + kAttnWgKeys - 1) / kAttnWgKeys * kAttnWgKeys;
     const int n_splits = (n_keys + L - 1) / L;
     const int split = blockIdx.x;
     if (split >= n_splits) return;
     const int k0 = split * L, k1 = min(n_keys, k0 + L);
-    const int kvh = blockIdx.y;
-    const int G = n_head / n_head_kv, NQ = G * len, H = n_head * hd;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int q_begin = wave * QPW;
-    const int nq = max(0, min(QPW, NQ - q_begin));
+    const int kk = lane >> 2, qq = lane & 3;
     const float scale = 1.0F / sqrtf(static_cast<float>(hd));
     const size_t head_base = (static_cast<size_t>(layer) * n_head_kv + kvh) * capacity;
     const uint16_t* kc = step->seqs[seq].k + head_base * hd;
     const uint16_t* vc = step->seqs[seq].v + head_base * hd;
 
-    const float* qrow[QPW];
-    int limit[QPW];  // last visible key of each query row (causal)
-#pragma unroll
-    for (int i = 0; i < QPW; ++i) {
-        const int qi = min(q_begin + i, NQ - 1);
+    // queries -> LDS, quarter c of row i at Qs[i][c * (DQ + 4)]
+    for (int e = threadIdx.x; e < QPW * hd; e += kThreads) {
+        const int i = e / hd, d = e - i * hd;
+        const int qi = q_begin + min(i, nq - 1);
         const int t = qi / G, head = kvh * G + qi % G;
-        qrow[i] = q + static_cast<size_t>(row0 + t) * H + head * hd;
-        limit[i] = pos0 + t;
+        Qs[i][(d / DQ) * (DQ + 4) + d % DQ] = q[static_cast<size_t>(row0 + t) * H + head * hd + d];
     }
+    int limit[QPW];
+#pragma unroll
+    for (int i = 0; i < QPW; ++i) limit[i] = pos0 + (q_begin + min(i, nq - 1)) / G;
+    __syncthreads();
+
     float m[QPW], l[QPW], o0[QPW], o1[QPW];
 #pragma unroll
     for (int i = 0; i < QPW; ++i) {
@@ -704,122 +818,156 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void k_attention(
         o0[i] = 0.0F;
         o1[i] = 0.0F;
     }
-    const bool vec8 = (hd & 7) == 0;
-    for (int t0 = k0; t0 < k1; t0 += kWave) {
-        const int key = t0 + lane;
-        const uint16_t* krow = kc + static_cast<size_t>(min(key, capacity - 1)) * hd;
+    for (int t0 = k0 + wave * kAttnTile; t0 < k1; t0 += W * kAttnTile) {
+        const int key = t0 + kk;
+        const int keyc = min(key, capacity - 1);
+        // K quarter of this lane's key and V pairs of the tile's 16 keys, loaded together
+        uint4 kr[HD > 0 ? HD / 32 : 1];
+        attn_load_k<HD>(kc + static_cast<size_t>(keyc) * hd, hd, qq, kr);
+        uint32_t vv[kAttnTile];
+#pragma unroll
+        for (int u = 0; u < kAttnTile; ++u) {
+            const int kj = min(t0 + u, capacity - 1);
+            vv[u] = 2 * lane < hd ? *reinterpret_cast<const uint32_t*>(vc + static_cast<size_t>(kj) * hd + 2 * lane) : 0u;
+        }
         float sc[QPW];
 #pragma unroll
         for (int i = 0; i < QPW; ++i) sc[i] = 0.0F;
-        if (vec8) {
-            for (int d = 0; d < hd; d += 8) {
-                const uint4 kv = *reinterpret_cast<const uint4*>(krow + d);
-                const float kf[8] = {h2f(kv.x), h2f(kv.x >> 16), h2f(kv.y), h2f(kv.y >> 16),
-                                     h2f(kv.z), h2f(kv.z >> 16), h2f(kv.w), h2f(kv.w >> 16)};
+        if constexpr (HD > 0) {
+#pragma unroll
+            for (int c = 0; c < HD / 32; ++c) {
+                const float kf[8] = {h2f(kr[c].x), h2f(kr[c].x >> 16), h2f(kr[c].y), h2f(kr[c].y >> 16),
+                                     h2f(kr[c].z), h2f(kr[c].z >> 16), h2f(kr[c].w), h2f(kr[c].w >> 16)};
 #pragma unroll
                 for (int i = 0; i < QPW; ++i) {
-                    if (i < nq) {
-                        const float* qd = qrow[i] + d;
-                        float acc = sc[i];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) acc += kf[e] * qd[e];
-                        sc[i] = acc;
-                    }
+                    const float4 qa = *reinterpret_cast<const float4*>(&Qs[i][qq * (DQ + 4) + 8 * c]);
+                    const float4 qb = *reinterpret_cast<const float4*>(&Qs[i][qq * (DQ + 4) + 8 * c + 4]);
+                    sc[i] += kf[0] * qa.x + kf[1] * qa.y + kf[2] * qa.z + kf[3] * qa.w + kf[4] * qb.x + kf[5] * qb.y +
+                             kf[6] * qb.z + kf[7] * qb.w;
                 }
             }
         } else {
-            for (int d = 0; d < hd; ++d) {
-                const float kf = h2f(krow[d]);
+            const uint16_t* kq = kc + static_cast<size_t>(keyc) * hd + qq * DQ;
+            for (int d = 0; d < DQ; ++d) {
+                const float kf = h2f(kq[d]);
 #pragma unroll
-                for (int i = 0; i < QPW; ++i) {
-                    if (i < nq) sc[i] += kf * qrow[i][d];
-                }
+                for (int i = 0; i < QPW; ++i) sc[i] += kf * Qs[i][qq * (DQ + 4) + d];
             }
         }
 #pragma unroll
         for (int i = 0; i < QPW; ++i) {
-            if (i < nq) {
-                const bool vis = key < k1 && key <= limit[i];
-                const float s = vis ? sc[i] * scale : -INFINITY;
-                const float m_new = fmaxf(m[i], wave_max(s));
-                float p = 0.0F, alpha = 1.0F;
-                if (m_new != -INFINITY) {
-                    alpha = m[i] == -INFINITY ? 0.0F : expf(m[i] - m_new);
-                    p = vis ? expf(s - m_new) : 0.0F;
-                }
-                l[i] = l[i] * alpha + p;
-                o0[i] *= alpha;
-                o1[i] *= alpha;
-                m[i] = m_new;
-                P[wave][i][lane] = p;
+            const float full = quad_sum(sc[i]);
+            const bool vis = i < nq && key < k1 && key <= limit[i];
+            const float sv = vis ? full * scale : -INFINITY;
+            const float m_new = fmaxf(m[i], wave_max(sv));
+            float p = 0.0F, alpha = 1.0F;
+            if (m_new != -INFINITY) {
+                alpha = m[i] == -INFINITY ? 0.0F : expf(m[i] - m_new);
+                p = vis ? expf(sv - m_new) : 0.0F;
             }
+            l[i] = l[i] * alpha + (qq == 0 ? p : 0.0F);
+            o0[i] *= alpha;
+            o1[i] *= alpha;
+            m[i] = m_new;
+            if (qq == 0) P[wave][i][kk] = p;
         }
-        __syncthreads();
-        const int nk = min(kWave, k1 - t0);
-        if (2 * lane < hd) {
-            for (int j = 0; j < nk; ++j) {
-                const uint32_t vv = *reinterpret_cast<const uint32_t*>(vc + static_cast<size_t>(t0 + j) * hd + 2 * lane);
-                const float v0 = h2f(vv), v1 = h2f(vv >> 16);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-                for (int i = 0; i < QPW; ++i) {
-                    if (i < nq) {
-                        const float pj = P[wave][i][j];
-                        o0[i] += pj * v0;
-                        o1[i] += pj * v1;
-                    }
-                }
+        for (int u4 = 0; u4 < kAttnTile / 4; ++u4) {
+            float v0[4], v1[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                v0[u] = h2f(vv[4 * u4 + u]);
+                v1[u] = h2f(vv[4 * u4 + u] >> 16);
+            }
+#pragma unroll
+            for (int i = 0; i < QPW; ++i) {
+                const float4 pv = *reinterpret_cast<const float4*>(&P[wave][i][4 * u4]);
+                o0[i] += pv.x * v0[0] + pv.y * v0[1] + pv.z * v0[2] + pv.w * v0[3];
+                o1[i] += pv.x * v1[0] + pv.y * v1[1] + pv.z * v1[2] + pv.w * v1[3];
             }
         }
-        __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    // split partial: (max, sum, unnormalized output) per query row
+    // merge the four waves
 #pragma unroll
     for (int i = 0; i < QPW; ++i) {
-        if (i < nq) {
-            const float lsum = wave_sum(l[i]);
-            const int qi = q_begin + i;
-            const int t = qi / G, head = kvh * G + qi % G;
-            float* dst = partial + ((static_cast<size_t>(row0 + t) * n_head + head) * splits_max + split) * (hd + 2);
-            if (lane == 0) {
-                dst[0] = m[i];
-                dst[1] = lsum;
-            }
-            if (2 * lane < hd) {
-                dst[2 + 2 * lane] = o0[i];
-                dst[3 + 2 * lane] = o1[i];
-            }
+        const float ls = wave_sum(l[i]);
+        if (lane == 0) {
+            Ms[wave][i] = m[i];
+            Ls[wave][i] = ls;
+        }
+        if (2 * lane < hd) {
+            Os[wave][i][2 * lane] = o0[i];
+            Os[wave][i][2 * lane + 1] = o1[i];
         }
     }
+    __syncthreads();
+    const int half_hd = hd / 2;
+    for (int e = threadIdx.x; e < nq * half_hd; e += kThreads) {
+        const int i = e / half_hd, dp = e - i * half_hd;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, Ms[w][i]);
+        float Lsum = 0.0F, a0 = 0.0F, a1 = 0.0F;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                const float f = Ms[w][i] == -INFINITY ? 0.0F : expf(Ms[w][i] - M);
+                Lsum += f * Ls[w][i];
+                a0 += f * Os[w][i][2 * dp];
+                a1 += f * Os[w][i][2 * dp + 1];
+            }
+        }
+        const int qi = q_begin + i;
+        const int t = qi / G, head = kvh * G + qi % G;
+        if (n_splits == 1) {
+            float* o = out + static_cast<size_t>(row0 + t) * H + head * hd;
+            o[2 * dp] = a0 / Lsum;
+            o[2 * dp + 1] = a1 / Lsum;
+        } else {
+            float* dst = partial + ((static_cast<size_t>(row0 + t) * n_head + head) * splits_max + split) * (hd + 2);
+            if (dp == 0) {
+                dst[0] = M;
+                dst[1] = Lsum;
+            }
+            dst[2 + 2 * dp] = a0;
+            dst[3 + 2 * dp] = a1;
+        }
+    }
+    if (n_splits == 1) return;
     __threadfence();
     __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(counters + seq * n_head_kv + kvh, 1) == n_splits - 1;
+    int32_t* counter = counters + (static_cast<size_t>(seq) * n_head_kv + kvh) * qgroups + qg;
+    if (threadIdx.x == 0) last = atomicAdd(counter, 1) == n_splits - 1;
     __syncthreads();
     if (!last) return;
     __threadfence();
-    // merge the splits: lanes over splits for the statistics, lanes over dims for the output
-    for (int qi = wave; qi < NQ; qi += kAttnWaves) {
+    for (int e = threadIdx.x; e < nq * half_hd; e += kThreads) {
+        const int i = e / half_hd, dp = e - i * half_hd;
+        const int qi = q_begin + i;
         const int t = qi / G, head = kvh * G + qi % G;
         const float* base = partial + (static_cast<size_t>(row0 + t) * n_head + head) * splits_max * (hd + 2);
-        const float ms = lane < n_splits ? base[lane * (hd + 2)] : -INFINITY;
-        const float ls = lane < n_splits ? base[lane * (hd + 2) + 1] : 0.0F;
-        const float M = wave_max(ms);
-        const float w = ms == -INFINITY ? 0.0F : expf(ms - M);
-        const float total = wave_sum(ls * w);
-        float a0 = 0.0F, a1 = 0.0F;
+        float M = -INFINITY;
+        for (int sp = 0; sp < n_splits; ++sp) M = fmaxf(M, base[sp * (hd + 2)]);
+        float Lsum = 0.0F, a0 = 0.0F, a1 = 0.0F;
         for (int sp = 0; sp < n_splits; ++sp) {
-            const float ws = __shfl(w, sp);
-            if (2 * lane < hd) {
-                a0 += ws * base[sp * (hd + 2) + 2 + 2 * lane];
-                a1 += ws * base[sp * (hd + 2) + 3 + 2 * lane];
-            }
+            const float* src = base + sp * (hd + 2);
+            const float ms = src[0];
+            const float f = ms == -INFINITY ? 0.0F : expf(ms - M);
+            Lsum += f * src[1];
+            a0 += f * src[2 + 2 * dp];
+            a1 += f * src[3 + 2 * dp];
         }
-        if (2 * lane < hd) {
-            float* o = out + static_cast<size_t>(row0 + t) * out_stride + head * hd;
-            o[2 * lane] = a0 / total;
-            o[2 * lane + 1] = a1 / total;
-        }
+        float* o = out + static_cast<size_t>(row0 + t) * H + head * hd;
+        o[2 * dp] = a0 / Lsum;
+        o[2 * dp + 1] = a1 / Lsum;
     }
-    if (threadIdx.x == 0) counters[seq * n_head_kv + kvh] = 0;
+    if (threadIdx.x == 0) *counter = 0;
 }
 
 // ------------------------------------------------------------------ argmax + acceptance
@@ -851,71 +999,107 @@ void check(hipError_t e, const char* what) {
     if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// Host-side geometry: the activation chunk fits kGemvActBytes of LDS, the
+// per-block partial sums kGemvPartBytes, and the row count per work-group
+// aims at kGemvTargetWgs work-groups.
+constexpr int kGemvActBytes = 28672;
+constexpr int kGemvPartBytes = 16384;
+constexpr int kGemvTargetWgs = 512;
+constexpr int kGemvFloatRows = 2 * kGluGroup;
+
+GemvGeom gemv_geom(const GemvArgs& a, int nt, size_t& lds) {
+    const int K = static_cast<int>(a.mat.cols);
+    const double per_value = nt * (1.0 + 4.0 / 256.0 + 2.0 / 16.0);
+    int chunk = static_cast<int>(kGemvActBytes / per_value) / 256 * 256;
+    if (chunk < 256) chunk = 256;
+    const int k_round = (K + 255) / 256 * 256;
+    if (chunk > k_round) chunk = k_round;
+    const int nbc = chunk / 256;
+    const int rows = static_cast<int>(a.mat.rows);
+    int rw = (rows + kGemvTargetWgs - 1) / kGemvTargetWgs;
+    const int cap = kGemvPartBytes / (nbc * nt * 4);
+    if (rw > cap) rw = cap;
+    if (rw < 1) rw = 1;
+    const int align = a.mode == kSwiGLU ? 2 * kGluGroup : a.mode == kQKV ? 2 : 1;
+    rw = (rw + align - 1) / align * align;
+    GemvGeom g;
+    g.rows_per_wg = rw;
+    g.chunk = chunk;
+    g.nbc_magic = ((1ull << 32) + static_cast<uint64_t>(nbc) - 1) / static_cast<uint64_t>(nbc);
+    lds = static_cast<size_t>(nt) * chunk + static_cast<size_t>(nt) * nbc * 4 + static_cast<size_t>(nt) * chunk / 8 +
+          static_cast<size_t>(rw) * nbc * nt * 4 + static_cast<size_t>(nt + nt * (kThreads / kWave) + rw * nt) * 4;
+    return g;
+}
+
 template <uint32_t TYPE, int NT>
-void gemv_q(const GemvArgs& a, int blocks, hipStream_t stream) {
-    const int K = static_cast<int>(a.mat[0].cols);
-    const int chunk = gemv_chunk_values(NT, K);
-    const size_t lds = static_cast<size_t>(NT) * chunk + static_cast<size_t>(NT) * (chunk / 256) * 4 +
-                       static_cast<size_t>(NT) * (chunk / 16) * 2;
-    hipLaunchKernelGGL((k_gemv_q<TYPE, NT>), dim3(blocks), dim3(kThreads), lds, stream, a, chunk);
+void gemv_q(const GemvArgs& a, hipStream_t stream) {
+    size_t lds = 0;
+    const GemvGeom g = gemv_geom(a, NT, lds);
+    const int grid = (static_cast<int>(a.mat.rows) + g.rows_per_wg - 1) / g.rows_per_wg;
+    hipLaunchKernelGGL((k_gemv_q<TYPE, NT>), dim3(grid), dim3(kThreads), lds, stream, a, g);
     check(hipGetLastError(), "gemv launch");
 }
 
 template <uint32_t TYPE>
-void gemv_q_nt(const GemvArgs& a, int blocks, hipStream_t stream) {
+void gemv_q_nt(const GemvArgs& a, hipStream_t stream) {
     switch (a.n_tok) {
-    case 1: gemv_q<TYPE, 1>(a, blocks, stream); break;
-    case 2: gemv_q<TYPE, 2>(a, blocks, stream); break;
-    case 3: gemv_q<TYPE, 3>(a, blocks, stream); break;
-    case 4: gemv_q<TYPE, 4>(a, blocks, stream); break;
-    case 5: gemv_q<TYPE, 5>(a, blocks, stream); break;
-    case 6: gemv_q<TYPE, 6>(a, blocks, stream); break;
-    case 7: gemv_q<TYPE, 7>(a, blocks, stream); break;
-    case 8: gemv_q<TYPE, 8>(a, blocks, stream); break;
+    case 1: gemv_q<TYPE, 1>(a, stream); break;
+    case 2: gemv_q<TYPE, 2>(a, stream); break;
+    case 3: gemv_q<TYPE, 3>(a, stream); break;
+    case 4: gemv_q<TYPE, 4>(a, stream); break;
+    case 5: gemv_q<TYPE, 5>(a, stream); break;
+    case 6: gemv_q<TYPE, 6>(a, stream); break;
+    case 7: gemv_q<TYPE, 7>(a, stream); break;
+    case 8: gemv_q<TYPE, 8>(a, stream); break;
     default: throw std::invalid_argument("gemv token group must be 1..8");
     }
 }
 
-}  // namespace
-
-int32_t gemv_chunk_values(int32_t n_tok, int32_t K) {
-    int32_t chunk = (kLdsActBytes / n_tok) / 256 * 256;
-    if (chunk < 256) chunk = 256;
-    const int32_t k_round = (K + 255) / 256 * 256;
-    return chunk < k_round ? chunk : k_round;
+template <int NT>
+void gemv_f(const GemvArgs& a, hipStream_t stream) {
+    const int grid = (static_cast<int>(a.mat.rows) + kGemvFloatRows - 1) / kGemvFloatRows;
+    const size_t lds = static_cast<size_t>(kGemvFloatRows) * NT * sizeof(float);
+    hipLaunchKernelGGL((k_gemv_f<NT>), dim3(grid), dim3(kThreads), lds, stream, a, kGemvFloatRows);
+    check(hipGetLastError(), "gemv launch");
 }
 
+}  // namespace
+
 void launch_gemv(const GemvArgs& a_in, hipStream_t stream) {
+    const uint32_t type = a_in.mat.type;
+    const bool quantized = type == 7 || type == 9 || type == 11 || type == 13;
+    if (quantized && (a_in.mat.cols % kActBlock != 0 || a_in.x.stride % 4 != 0)) {
+        throw std::invalid_argument("quantized matmul needs rows of a multiple of 256 values");
+    }
+    if ((a_in.mode == kSwiGLU && a_in.mat.rows % (2 * kGluGroup) != 0) || (a_in.mode == kQKV && a_in.mat.rows % 2 != 0)) {
+        throw std::invalid_argument("matmul rows do not fit the fused row layout");
+    }
     // token groups of at most 8 rows
     for (int t0 = 0; t0 < a_in.n_tok; t0 += 8) {
         GemvArgs a = a_in;
         a.n_tok = a_in.n_tok - t0 < 8 ? a_in.n_tok - t0 : 8;
-        a.x.q += static_cast<size_t>(t0) * a.x.stride;
-        a.x.d += static_cast<size_t>(t0) * (a.x.stride / 256);
-        a.x.s += static_cast<size_t>(t0) * (a.x.stride / 16);
-        a.x.f += static_cast<size_t>(t0) * a.x.stride;
-        a.y += static_cast<size_t>(t0) * a.y_stride;
+        if (a.x.gather) a.x.gather += t0;
+        else a.x.x += static_cast<size_t>(t0) * a.x.stride;
+        if (a.y) a.y += static_cast<size_t>(t0) * a.y_stride;
         if (a.best) a.best += t0;
-        uint32_t total = 0;
-        for (int i = 0; i < a.n_mat; ++i) total += a.mat[i].rows;
-        const int waves = a.mode == kSwiGLU ? static_cast<int>(a.mat[0].rows) : static_cast<int>((total + 1) / 2);
-        const int blocks = (waves + kThreads / kWave - 1) / (kThreads / kWave);
-        const uint32_t type = a.mat[0].type;
-        if (type == 1 || type == 2) {
+        if (a.mode == kQKV) {
+            a.qkv.row0 += t0;
+            a.qkv.q += static_cast<size_t>(t0) * a.qkv.n_head * a.qkv.head_dim;
+        }
+        if (!quantized) {
             switch (a.n_tok) {
-            case 1: hipLaunchKernelGGL(k_gemv_f<1>, dim3(blocks), dim3(kThreads), 0, stream, a); break;
-            case 2: hipLaunchKernelGGL(k_gemv_f<2>, dim3(blocks), dim3(kThreads), 0, stream, a); break;
-            case 3: case 4: hipLaunchKernelGGL(k_gemv_f<4>, dim3(blocks), dim3(kThreads), 0, stream, a); break;
-            default: hipLaunchKernelGGL(k_gemv_f<8>, dim3(blocks), dim3(kThreads), 0, stream, a); break;
+            case 1: gemv_f<1>(a, stream); break;
+            case 2: gemv_f<2>(a, stream); break;
+            case 3: case 4: gemv_f<4>(a, stream); break;
+            default: gemv_f<8>(a, stream); break;
             }
-            check(hipGetLastError(), "gemv launch");
             continue;
         }
         switch (type) {
-        case 11: gemv_q_nt<11>(a, blocks, stream); break;
-        case 13: gemv_q_nt<13>(a, blocks, stream); break;
-        case 9: gemv_q_nt<9>(a, blocks, stream); break;
-        case 7: gemv_q_nt<7>(a, blocks, stream); break;
+        case 11: gemv_q_nt<11>(a, stream); break;
+        case 13: gemv_q_nt<13>(a, stream); break;
+        case 9: gemv_q_nt<9>(a, stream); break;
+        case 7: gemv_q_nt<7>(a, stream); break;
         default: throw std::invalid_argument("unsupported weight type for gemv");
         }
     }
@@ -928,54 +1112,36 @@ void launch_embed(const DMat& table, const StepDev* step, float* h, int32_t n_ro
     check(hipGetLastError(), "embed launch");
 }
 
-void launch_norm_quant(const float* h, int32_t h_stride, const float* gain, float eps, int32_t H,
-                       const StepDev* step, int32_t select_out, int32_t n_rows, bool quantize, Act x,
-                       hipStream_t stream) {
-    if (H % 4 != 0) throw std::invalid_argument("hidden size must be a multiple of 4");
-    hipLaunchKernelGGL(k_norm_quant, dim3((H + kActBlock - 1) / kActBlock, n_rows), dim3(kWave), 0, stream, h,
-                       h_stride, gain, eps, H, step, select_out, quantize ? 1 : 0, x);
-    check(hipGetLastError(), "norm launch");
-}
-
-void launch_quant(const float* src, int32_t src_stride, int32_t K, int32_t n_rows, bool quantize, Act x,
-                  hipStream_t stream) {
-    hipLaunchKernelGGL(k_quant, dim3((K + kActBlock - 1) / kActBlock, n_rows), dim3(kWave), 0, stream, src, src_stride,
-                       K, quantize ? 1 : 0, x);
-    check(hipGetLastError(), "quant launch");
-}
-
-void launch_rope_kv(const float* qkv, int32_t n_rows, int32_t n_head, int32_t n_head_kv, int32_t head_dim,
-                    const float* rope, const StepDev* step, int32_t layer, float* qout, hipStream_t stream) {
-    hipLaunchKernelGGL(k_rope_kv, dim3(n_rows), dim3(kThreads), 0, stream, qkv, n_head, n_head_kv, head_dim, rope,
-                       step, layer, qout);
-    check(hipGetLastError(), "rope launch");
-}
-
 int32_t attention_splits(int32_t capacity) {
-    const int32_t s = (capacity + kWave - 1) / kWave;
-    return s < 1 ? 1 : (s > kWave ? kWave : s);
+    const int32_t s = (capacity + kAttnWgKeys - 1) / kAttnWgKeys;
+    return s < 1 ? 1 : (s > 32 ? 32 : s);
 }
 
-void launch_attention(const float* q, const StepDev* step, int32_t n_rows, int32_t max_len, int32_t n_seq,
-                      int32_t layer, int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t splits,
-                      float* partial, int32_t* counters, Act out, hipStream_t stream) {
+size_t attention_partial_floats(int32_t rows, int32_t n_head, int32_t head_dim, int32_t splits) {
+    return static_cast<size_t>(rows) * n_head * splits * (head_dim + 2);
+}
+
+void launch_attention(const float* q, const StepDev* step, int32_t max_len, int32_t n_seq, int32_t layer,
+                      int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t splits, float* partial,
+                      int32_t* counters, float* out, hipStream_t stream) {
     const int G = n_head / n_head_kv;
-    const int nq = G * max_len;
-    if (head_dim > 2 * kWave || head_dim % 2 != 0) throw std::invalid_argument("attention supports even head dims <= 128");
-    if (nq > kAttnWaves * 16) throw std::invalid_argument("attention work-group exceeds its query rows");
-    const int qpw = (nq + kAttnWaves - 1) / kAttnWaves;
-    dim3 grid(splits, n_head_kv, n_seq), block(kAttnWaves * kWave);
-#define JFH_ATTN(QPW)                                                                                          \
-    hipLaunchKernelGGL(k_attention<QPW>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, \
-                       splits, partial, counters, out.f, out.stride)
-    if (qpw <= 2) JFH_ATTN(2);
-    else if (qpw <= 4) JFH_ATTN(4);
-    else if (qpw <= 8) JFH_ATTN(8);
-    else JFH_ATTN(16);
-#undef JFH_ATTN
+    const int qgroups = (G * max_len + kAttnQPW - 1) / kAttnQPW;
+    if (head_dim > 2 * kWave || head_dim % 4 != 0) {
+        throw std::invalid_argument("attention supports head dims that are multiples of 4 up to 128");
+    }
+    if (qgroups > kMaxAttnQGroups) throw std::invalid_argument("attention step has too many query rows per kv head");
+    dim3 grid(splits, n_head_kv * qgroups, n_seq), block(kThreads);
+    if (head_dim == 128) {
+        hipLaunchKernelGGL(k_attention<128>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
+                           qgroups, partial, counters, out);
+    } else if (head_dim == 64) {
+        hipLaunchKernelGGL(k_attention<64>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
+                           qgroups, partial, counters, out);
+    } else {
+        hipLaunchKernelGGL(k_attention<0>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
+                           qgroups, partial, counters, out);
+    }
     check(hipGetLastError(), "attention launch");
-    const int H = n_head * head_dim;
-    launch_quant(out.f, out.stride, H, n_rows, H % kActBlock == 0, out, stream);
 }
 
 void launch_finish(const unsigned long long* best, const StepDev* step, int32_t n_out, StepOut* out,
