@@ -501,6 +501,26 @@ std::vector<uint8_t> write_gguf_header(const std::vector<std::pair<std::string, 
 }
 
 // ---------------------------------------------------------------- writer
+std::pair<std::array<uint8_t, 32>, uint64_t> source_digest(const std::vector<uint8_t>& gguf_header,
+                                                           const std::vector<TensorBlob>& tensors) {
+    Sha256 src;
+    src.update(gguf_header.data(), gguf_header.size());
+    uint64_t size = gguf_header.size();
+    static const uint8_t zeros[32] = {};
+    uint64_t data_pos = 0;
+    for (const TensorBlob& t : tensors) {
+        while (data_pos % 32) {
+            src.update(zeros, 1);
+            ++data_pos;
+            ++size;
+        }
+        src.update(t.data, size_t(t.size));
+        data_pos += t.size;
+        size += t.size;
+    }
+    return {src.finish(), size};
+}
+
 void write_package(const std::string& dir, uint32_t layer_count, const std::vector<uint8_t>& gguf_header,
                    const std::vector<TensorBlob>& tensors) {
     namespace fs = std::filesystem;
@@ -629,19 +649,7 @@ void write_package(const std::string& dir, uint32_t layer_count, const std::vect
     if (groups.count("shared.jfs")) take("shared.jfs");
     if (!groups.empty()) fail(Status::InvalidArgument, "tensor belongs to a layer outside the model");
 
-    // Source GGUF = header + payloads at 32-byte aligned offsets, in the order of `tensors`.
-    Sha256 src;
-    src.update(gguf_header.data(), gguf_header.size());
-    uint64_t src_size = gguf_header.size();
-    static const uint8_t zeros[32] = {};
-    uint64_t data_pos = 0;
-    for (const TensorBlob& t : tensors) {
-        while (data_pos % 32) { src.update(zeros, 1); ++data_pos; ++src_size; }
-        src.update(t.data, size_t(t.size));
-        data_pos += t.size;
-        src_size += t.size;
-    }
-    const auto src_sha = src.finish();
+    const auto [src_sha, src_size] = source_digest(gguf_header, tensors);
 
     std::vector<uint8_t> man;
     man.insert(man.end(), {'J', 'F', 'M', 'O', 'D', 'E', 'L', '2'});

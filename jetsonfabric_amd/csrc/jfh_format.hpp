@@ -147,6 +147,12 @@ struct TensorBlob {
     uint64_t size = 0;
 };
 
+// SHA-256 and size of the source GGUF a package records in its manifest: the
+// GGUF header followed by the tensor payloads at 32-byte aligned offsets, in
+// the order given.
+std::pair<std::array<uint8_t, 32>, uint64_t> source_digest(const std::vector<uint8_t>& gguf_header,
+                                                           const std::vector<TensorBlob>& tensors);
+
 // Writes a JFM v2 package: manifest.jfm, metadata.gguf, input/output/shared and
 // one segment per layer, grouped by name (runtime/compiler/jf_model_compile.cpp:612-624).
 void write_package(const std::string& dir, uint32_t layer_count, const std::vector<uint8_t>& gguf_header,

@@ -397,8 +397,7 @@ void HostModel::finalize() {
         shape(pre + "ffn_down.weight", {F, H});
     }
     if (!package_) {
-        const auto g = gguf_header();
-        source_sha256_ = hex(sha256(g.data(), g.size()).data(), 32);
+        source_sha256_ = hex(source_digest(gguf_header(), blobs()).first.data(), 32);
     }
 }
 
@@ -440,8 +439,7 @@ std::vector<uint8_t> HostModel::gguf_header() const {
     return write_gguf_header(kv, infos);
 }
 
-void HostModel::write_package(const std::string& dir) const {
-    if (layer_start_ != 0 || layer_end_ != params_.n_layer) fail(Status::InvalidArgument, "only a full model can be written as a package");
+std::vector<TensorBlob> HostModel::blobs() const {
     std::vector<TensorBlob> blobs;
     for (const TensorView& t : tensors_) {
         TensorBlob b;
@@ -453,7 +451,12 @@ void HostModel::write_package(const std::string& dir) const {
         b.size = t.size;
         blobs.push_back(b);
     }
-    jfh::write_package(dir, params_.n_layer, gguf_header(), blobs);
+    return blobs;
+}
+
+void HostModel::write_package(const std::string& dir) const {
+    if (layer_start_ != 0 || layer_end_ != params_.n_layer) fail(Status::InvalidArgument, "only a full model can be written as a package");
+    jfh::write_package(dir, params_.n_layer, gguf_header(), blobs());
 }
 
 std::unique_ptr<HostModel> HostModel::synthesize(const SynthSpec& spec) {

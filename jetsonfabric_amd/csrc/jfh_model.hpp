@@ -66,6 +66,8 @@ public:
 
     // GGUF header bytes for the model's metadata (written or as loaded).
     std::vector<uint8_t> gguf_header() const;
+    // Tensors as package blobs, in model order.
+    std::vector<TensorBlob> blobs() const;
     void write_package(const std::string& dir) const;
 
 private:
