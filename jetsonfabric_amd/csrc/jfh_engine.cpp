@@ -83,61 +83,132 @@ const float* Engine::upload_f32(const TensorView& t) {
 
 namespace {
 
-// Device row layout per type: main plane bytes and aux plane bytes of one row.
-void device_row_bytes(uint32_t type, uint64_t cols, uint32_t& main, uint32_t& aux) {
+// Codes of one 256-value GGML block of a row, as unsigned 2/6-bit codes (Q2_K, Q6_K).
+void q6k_codes(const uint8_t* blk, uint8_t* code) {
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    for (int n = 0; n < 2; ++n) {
+        for (int l = 0; l < 32; ++l) {
+            const uint8_t h = qh[32 * n + l];
+            code[128 * n + l] = static_cast<uint8_t>((ql[64 * n + l] & 0xF) | ((h & 3) << 4));
+            code[128 * n + l + 32] = static_cast<uint8_t>((ql[64 * n + l + 32] & 0xF) | (((h >> 2) & 3) << 4));
+            code[128 * n + l + 64] = static_cast<uint8_t>((ql[64 * n + l] >> 4) | (((h >> 4) & 3) << 4));
+            code[128 * n + l + 96] = static_cast<uint8_t>((ql[64 * n + l + 32] >> 4) | (((h >> 6) & 3) << 4));
+        }
+    }
+}
+
+void q2k_codes(const uint8_t* blk, uint8_t* code) {
+    const uint8_t* qs = blk + 16;
+    for (int n = 0; n < 2; ++n) {
+        for (int r = 0; r < 4; ++r) {
+            for (int l = 0; l < 32; ++l) code[128 * n + 32 * r + l] = static_cast<uint8_t>((qs[32 * n + l] >> (2 * r)) & 3);
+        }
+    }
+}
+
+}  // namespace
+
+// One 16-row x 256-value tile (gfx950 layout, jfh_kernels.hpp) from the
+// rows' GGML blocks; absent rows (nullptr) are zero. Lane l = i + 16 g of a
+// wave owns row i's values 64 g .. 64 g + 63.
+void build_tile(uint32_t type, const uint8_t* const* blk, uint8_t* tile) {
+    std::memset(tile, 0, gpu::tile_bytes(type));
+    auto lane_chunk = [&](uint32_t base, uint32_t chunk, uint32_t lane) { return tile + base + (chunk * 64 + lane) * 16; };
     switch (type) {
-    case kF32:
-    case kF16:
     case kQ4_K:
-        main = static_cast<uint32_t>(row_bytes(type, cols));
-        aux = 0;
+        for (uint32_t i = 0; i < 16; ++i) {
+            if (!blk[i]) continue;
+            // header: d, dmin, then the eight 6-bit scale/min pairs regrouped
+            // per lane group g into 24-bit fields (sc 2g | sc 2g+1 | m 2g |
+            // m 2g+1) at bit 24 g of the 12 scale bytes
+            std::memcpy(tile + 16 * i, blk[i], 4);
+            const uint8_t* q = blk[i] + 4;
+            int sc[8], mn[8];
+            for (int j = 0; j < 8; ++j) {
+                if (j < 4) {
+                    sc[j] = q[j] & 63;
+                    mn[j] = q[j + 4] & 63;
+                } else {
+                    sc[j] = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+                    mn[j] = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+                }
+            }
+            uint8_t packed[12] = {};
+            for (uint32_t g = 0; g < 4; ++g) {
+                const uint32_t f = static_cast<uint32_t>(sc[2 * g]) | (static_cast<uint32_t>(sc[2 * g + 1]) << 6) |
+                                   (static_cast<uint32_t>(mn[2 * g]) << 12) | (static_cast<uint32_t>(mn[2 * g + 1]) << 18);
+                for (uint32_t b = 0; b < 3; ++b) packed[3 * g + b] = static_cast<uint8_t>(f >> (8 * b));
+            }
+            std::memcpy(tile + 16 * i + 4, packed, 12);
+            for (uint32_t g = 0; g < 4; ++g) {
+                for (uint32_t c = 0; c < 2; ++c) std::memcpy(lane_chunk(256, c, i + 16 * g), blk[i] + 16 + 32 * g + 16 * c, 16);
+            }
+        }
         return;
     case kQ6_K:
-        main = static_cast<uint32_t>(cols / 256 * 208);
-        aux = static_cast<uint32_t>(cols / 256 * 2);
+        for (uint32_t i = 0; i < 16; ++i) {
+            if (!blk[i]) continue;
+            std::memcpy(tile + 2 * i, blk[i] + 208, 2);
+            std::memcpy(tile + 32 + 16 * i, blk[i] + 192, 16);
+            uint8_t code[256];
+            q6k_codes(blk[i], code);
+            for (uint32_t g = 0; g < 4; ++g) {
+                const uint8_t* v = code + 64 * g;
+                uint32_t dw[12] = {};
+                for (uint32_t k = 0; k < 8; ++k) {
+                    for (uint32_t e = 0; e < 4; ++e) {
+                        dw[k] |= static_cast<uint32_t>((v[8 * k + e] & 0xF) | ((v[8 * k + 4 + e] & 0xF) << 4)) << (8 * e);
+                    }
+                }
+                for (uint32_t m = 0; m < 4; ++m) {
+                    for (uint32_t e = 0; e < 4; ++e) {
+                        uint32_t hb = 0;
+                        for (uint32_t r = 0; r < 4; ++r) hb |= static_cast<uint32_t>(v[16 * m + 4 * r + e] >> 4) << (2 * r);
+                        dw[8 + m] |= hb << (8 * e);
+                    }
+                }
+                for (uint32_t c = 0; c < 3; ++c) std::memcpy(lane_chunk(288, c, i + 16 * g), dw + 4 * c, 16);
+            }
+        }
         return;
     case kQ8_0:
-        main = static_cast<uint32_t>(cols / 32 * 32);
-        aux = static_cast<uint32_t>(cols / 32 * 2);
+        for (uint32_t i = 0; i < 16; ++i) {
+            if (!blk[i]) continue;
+            for (uint32_t j = 0; j < 8; ++j) std::memcpy(tile + 16 * i + 2 * j, blk[i] + 34 * j, 2);
+            for (uint32_t g = 0; g < 4; ++g) {
+                for (uint32_t c = 0; c < 4; ++c) {
+                    const uint8_t* b = blk[i] + 34 * (2 * g + c / 2) + 2 + 16 * (c % 2);
+                    std::memcpy(lane_chunk(256, c, i + 16 * g), b, 16);
+                }
+            }
+        }
         return;
     case kQ2_K:
-        main = static_cast<uint32_t>(cols / 256 * 80);
-        aux = static_cast<uint32_t>(cols / 256 * 4);
+        for (uint32_t i = 0; i < 16; ++i) {
+            if (!blk[i]) continue;
+            std::memcpy(tile + 4 * i, blk[i] + 80, 4);
+            std::memcpy(tile + 64 + 16 * i, blk[i], 16);
+            uint8_t code[256];
+            q2k_codes(blk[i], code);
+            for (uint32_t g = 0; g < 4; ++g) {
+                const uint8_t* v = code + 64 * g;
+                uint32_t dw[4] = {};
+                for (uint32_t m = 0; m < 4; ++m) {
+                    for (uint32_t e = 0; e < 4; ++e) {
+                        for (uint32_t r = 0; r < 4; ++r) {
+                            dw[m] |= static_cast<uint32_t>(v[16 * m + 4 * r + e]) << (8 * e + 2 * r);
+                        }
+                    }
+                }
+                std::memcpy(lane_chunk(320, 0, i + 16 * g), dw, 16);
+            }
+        }
         return;
     default:
         fail(Status::FormatError, std::string("unsupported tensor type ") + type_name(type) + " for a device matrix");
     }
 }
-
-// One GGML-encoded row split into the device planes: Q4_K/F32/F16 verbatim;
-// Q6_K ql|qh|scales (208) + d; Q8_0 qs (32) + d; Q2_K scales|qs (80) + d,dmin.
-void repack_row(uint32_t type, const uint8_t* src, uint64_t cols, uint8_t* main, uint8_t* aux) {
-    switch (type) {
-    case kQ6_K:
-        for (uint64_t b = 0; b < cols / 256; ++b) {
-            std::memcpy(main + b * 208, src + b * 210, 208);
-            std::memcpy(aux + b * 2, src + b * 210 + 208, 2);
-        }
-        return;
-    case kQ8_0:
-        for (uint64_t b = 0; b < cols / 32; ++b) {
-            std::memcpy(aux + b * 2, src + b * 34, 2);
-            std::memcpy(main + b * 32, src + b * 34 + 2, 32);
-        }
-        return;
-    case kQ2_K:
-        for (uint64_t b = 0; b < cols / 256; ++b) {
-            std::memcpy(main + b * 80, src + b * 84, 80);
-            std::memcpy(aux + b * 4, src + b * 84 + 80, 4);
-        }
-        return;
-    default:
-        std::memcpy(main, src, row_bytes(type, cols));
-        return;
-    }
-}
-
-}  // namespace
 
 uint32_t Engine::device_row(const TensorRef& r, uint32_t row) {
     switch (r.kind) {
@@ -159,29 +230,43 @@ uint32_t Engine::device_row(const TensorRef& r, uint32_t row) {
 const Engine::DeviceTensor& Engine::upload_rows(const std::string& key, uint32_t type, uint64_t cols,
                                                 const std::vector<RowSource>& rows, const float* bias) {
     DeviceTensor d;
-    uint32_t main_rb = 0, aux_rb = 0;
-    device_row_bytes(type, cols, main_rb, aux_rb);
     d.mat.type = type;
     d.mat.rows = static_cast<uint32_t>(rows.size());
     d.mat.cols = static_cast<uint32_t>(cols);
-    d.mat.main_row_bytes = main_rb;
-    d.mat.aux_row_bytes = aux_rb;
     const uint64_t src_rb = row_bytes(type, cols);
-    std::vector<uint8_t> main(rows.size() * main_rb), aux(rows.size() * aux_rb);
-    for (size_t r = 0; r < rows.size(); ++r) {
-        const RowSource& rs = rows[r];
-        repack_row(type, rs.tensor->data + static_cast<uint64_t>(rs.row) * src_rb, cols, main.data() + r * main_rb,
-                   aux.empty() ? nullptr : aux.data() + r * aux_rb);
-        d.bytes += src_rb;
+    std::vector<uint8_t> data;
+    const uint32_t TB = gpu::tile_bytes(type);
+    if (TB == 0) {
+        if (type != kF32 && type != kF16) {
+            fail(Status::FormatError, std::string("unsupported tensor type ") + type_name(type) + " for a device matrix");
+        }
+        d.mat.row_bytes = static_cast<uint32_t>(src_rb);
+        data.resize(rows.size() * src_rb);
+        for (size_t r = 0; r < rows.size(); ++r) {
+            std::memcpy(data.data() + r * src_rb, rows[r].tensor->data + static_cast<uint64_t>(rows[r].row) * src_rb, src_rb);
+        }
+    } else {
+        if (cols % 256 != 0) fail(Status::FormatError, "quantized matrices need row lengths that are multiples of 256");
+        const uint64_t nb = cols / 256, n_rg = (rows.size() + 15) / 16;
+        const uint64_t blk_bytes = src_rb / nb;  // one 256-value block (8 Q8_0 blocks)
+        data.resize(n_rg * nb * TB);
+        for (uint64_t rg = 0; rg < n_rg; ++rg) {
+            for (uint64_t b = 0; b < nb; ++b) {
+                const uint8_t* src[16];
+                for (uint32_t i = 0; i < 16; ++i) {
+                    const uint64_t r = rg * 16 + i;
+                    src[i] = r < rows.size()
+                                 ? rows[r].tensor->data + static_cast<uint64_t>(rows[r].row) * src_rb + b * blk_bytes
+                                 : nullptr;
+                }
+                build_tile(type, src, data.data() + (rg * nb + b) * TB);
+            }
+        }
     }
-    void* mp = device_alloc(main.size());
-    hip_check(hipMemcpy(mp, main.data(), main.size(), hipMemcpyHostToDevice), "upload matrix");
-    d.mat.main = static_cast<const uint8_t*>(mp);
-    if (!aux.empty()) {
-        void* ap = device_alloc(aux.size());
-        hip_check(hipMemcpy(ap, aux.data(), aux.size(), hipMemcpyHostToDevice), "upload matrix");
-        d.mat.aux = static_cast<const uint8_t*>(ap);
-    }
+    d.bytes = rows.size() * src_rb;
+    void* mp = device_alloc(data.size());
+    hip_check(hipMemcpy(mp, data.data(), data.size(), hipMemcpyHostToDevice), "upload matrix");
+    d.mat.data = static_cast<const uint8_t*>(mp);
     if (bias) {
         void* bp = device_alloc(rows.size() * sizeof(float));
         hip_check(hipMemcpy(bp, bias, rows.size() * sizeof(float), hipMemcpyHostToDevice), "upload bias");
@@ -326,10 +411,16 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
     ffn_ = static_cast<float*>(device_alloc(R * F * sizeof(float)));
     logits_ = static_cast<float*>(device_alloc(R * static_cast<size_t>(p.n_vocab) * sizeof(float)));
     best_ = static_cast<unsigned long long*>(device_alloc(R * sizeof(unsigned long long)));
-    // attention split counters: zero here, and every kernel that uses them leaves them zero
-    const size_t n_counters = static_cast<size_t>(gpu::kMaxSeq) * p.n_head_kv * gpu::kMaxAttnQGroups;
-    counters_ = static_cast<int32_t*>(device_alloc(n_counters * sizeof(int32_t)));
-    hip_check(hipMemset(counters_, 0, n_counters * sizeof(int32_t)), "clear attention counters");
+    auto act8 = [&](int32_t K) {
+        gpu::Act8 a;
+        a.K = K;
+        a.q = static_cast<int8_t*>(device_alloc(R * K));
+        a.d = static_cast<float*>(device_alloc(R * (K / 256) * sizeof(float)));
+        a.s = static_cast<int16_t*>(device_alloc(R * (K / 16) * sizeof(int16_t)));
+        return a;
+    };
+    if (quantized(layers_[0].o->mat.type) && Hq % 256 == 0) xq_attn_ = act8(Hq);
+    if (quantized(layers_[0].down->mat.type) && F % 256 == 0) xq_ffn_ = act8(F);
     step_dev_ = static_cast<gpu::StepDev*>(device_alloc(sizeof(gpu::StepDev)));
     out_dev_ = static_cast<gpu::StepOut*>(device_alloc(sizeof(gpu::StepOut)));
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&step_host_), sizeof(gpu::StepDev), hipHostMallocDefault),
@@ -389,7 +480,8 @@ std::string gemv_label(const gpu::GemvArgs& a) {
     const uint32_t t = a.mat.type;
     const bool fl = t == kF32 || t == kF16;
     const int nt = a.n_tok > 8 ? 8 : a.n_tok;
-    return std::string(fl ? "k_gemv_f<" : "k_gemv_q<") + (fl ? "" : std::to_string(t) + ",") + std::to_string(nt) + ">";
+    const int slot = nt <= 2 ? nt : nt <= 4 ? 4 : nt <= 6 ? 6 : 8;
+    return std::string(fl ? "k_gemv_f<" : "k_mm<") + (fl ? "" : std::to_string(t) + ",") + std::to_string(fl ? nt : slot) + ">";
 }
 
 // Algorithmic HBM bytes of one matmul launch: encoded weights and bias, the
@@ -398,7 +490,7 @@ std::string gemv_label(const gpu::GemvArgs& a) {
 double gemv_bytes(const gpu::GemvArgs& a) {
     const double rows = a.mat.rows, K = a.mat.cols, n = a.n_tok;
     double w = static_cast<double>(mat_bytes(a.mat)) + (a.mat.bias ? 4.0 * rows : 0.0);
-    double in = n * K * 4.0 + (a.x.gain ? K * 4.0 : 0.0);
+    double in = a.xq.q ? n * K * (1.0 + 4.0 / 256.0 + 2.0 / 16.0) : n * K * 4.0 + (a.x.gain ? K * 4.0 : 0.0);
     double out = n * rows * 4.0;
     switch (a.mode) {
     case gpu::kAdd: out *= 2.0; break;
@@ -457,16 +549,20 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         qkv.qkv.n_head_kv = static_cast<int32_t>(p.n_head_kv);
         qkv.qkv.head_dim = static_cast<int32_t>(p.head_dim);
         timed(gemv_label(qkv) + ":qkv", gemv_bytes(qkv), [&] { gpu::launch_gemv(qkv, s); });
-        timed("k_attention", attn_kv_bytes_ + n * Hq * 8.0, [&] {
+        timed("k_attention", attn_kv_bytes_ + n * Hq * 4.0, [&] {
             gpu::launch_attention(q_, step_dev_, max_len, n_seq, static_cast<int32_t>(l), static_cast<int32_t>(p.n_head),
-                                  static_cast<int32_t>(p.n_head_kv), static_cast<int32_t>(p.head_dim), splits_, partial_,
-                                  counters_, attn_, s);
+                                  static_cast<int32_t>(p.n_head_kv), static_cast<int32_t>(p.head_dim), splits_, partial_, s);
+        });
+        timed("k_attention_merge", n * Hq * 4.0 * (splits_ + 1.0) + (xq_attn_.q ? n * Hq * 1.1 : 0.0), [&] {
+            gpu::launch_attention_merge(partial_, step_dev_, n_rows, static_cast<int32_t>(p.n_head),
+                                        static_cast<int32_t>(p.head_dim), splits_, attn_, xq_attn_, s);
         });
         gpu::GemvArgs o;
         o.mat = L.o->mat;
         o.mode = gpu::kAdd;
         o.n_tok = n_rows;
-        o.x = {attn_, Hq, nullptr, nullptr, 0.0F};
+        if (xq_attn_.q && quantized(o.mat.type)) o.xq = xq_attn_;
+        else o.x = {attn_, Hq, nullptr, nullptr, 0.0F};
         o.y = h_;
         o.y_stride = H;
         timed(gemv_label(o) + ":attn_output", gemv_bytes(o), [&] { gpu::launch_gemv(o, s); });
@@ -482,7 +578,12 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         dn.mat = L.down->mat;
         dn.mode = gpu::kAdd;
         dn.n_tok = n_rows;
-        dn.x = {ffn_, F, nullptr, nullptr, 0.0F};
+        if (xq_ffn_.q && quantized(dn.mat.type)) {
+            timed("k_quantize", n * F * 5.1, [&] { gpu::launch_quantize(ffn_, F, n_rows, xq_ffn_, s); });
+            dn.xq = xq_ffn_;
+        } else {
+            dn.x = {ffn_, F, nullptr, nullptr, 0.0F};
+        }
         dn.y = h_;
         dn.y_stride = H;
         timed(gemv_label(dn) + ":ffn_down", gemv_bytes(dn), [&] { gpu::launch_gemv(dn, s); });

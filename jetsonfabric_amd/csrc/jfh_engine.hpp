@@ -19,6 +19,10 @@
 
 namespace jfh {
 
+// Builds one 16-row x 256-value device tile of a quantized type from the 16
+// rows' GGML blocks (nullptr rows are zero); tile holds gpu::tile_bytes(type).
+void build_tile(uint32_t type, const uint8_t* const* blocks, uint8_t* tile);
+
 struct EngineOptions {
     int device = 0;
     bool use_graphs = true;
@@ -180,7 +184,10 @@ private:
     float* rope_ = nullptr;
     uint32_t capacity_max_ = 0;
     int32_t splits_ = 0;
-    int32_t* counters_ = nullptr;
+    // int8 staging copies of the attention output and the SwiGLU output
+    // (set when the consuming matrix is quantized)
+    gpu::Act8 xq_attn_;
+    gpu::Act8 xq_ffn_;
 
     // captured step graphs keyed by (rows, seqs, outs, store_logits)
     std::map<uint64_t, hipGraphExec_t> graphs_;

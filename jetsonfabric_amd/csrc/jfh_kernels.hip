@@ -1,10 +1,12 @@
 // gfx950 kernels for the Qwen2 stage forward (decode, draft verify, prefill).
 //
 // Graph being implemented: runtime/engines/native/src/qwen2_architecture.cpp:522-598.
-// Weights stay in their GGML block encodings (tensor_store.cpp:185-196); the
-// matmuls quantize the activation row to int8 in 256-value blocks and use
-// v_dot4 integer dot products against the unpacked quants, the same scheme
-// GGML's CPU backend uses for K-quants (activation q8 blocks + integer dot).
+// Weights keep their GGML block encodings, rearranged into 16-row x 256-value
+// tiles (jfh_kernels.hpp, tile_bytes) so that every wave-wide load covers
+// 1 KiB of contiguous memory. The matmuls quantize each activation row to int8
+// in 256-value blocks (d = amax/127) and use v_dot4 integer dot products
+// against the unpacked codes, the scheme GGML's CPU backend uses for K-quants
+// (activation q8 blocks + integer dot).
 #include "jfh_kernels.hpp"
 
 #include <hip/hip_runtime.h>
@@ -16,10 +18,28 @@
 namespace jfh::gpu {
 namespace {
 
-constexpr int kThreads = 256;
 constexpr int kWave = 64;
 
-__device__ __forceinline__ float h2f(uint32_t bits16) {
+// Pointers read from device memory (the step description) are generic to
+// the compiler; routing them through the global address space lets it use
+// global (not FLAT) memory instructions, whose completion is tracked apart
+// from LDS traffic.
+template <typename T>
+using global_ptr = __attribute__((address_space(1))) T*;
+
+template <typename T>
+__device__ __forceinline__ global_ptr<T> as_global(T* p) {
+    return (global_ptr<T>) p;
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 load_u4(global_ptr<const uint16_t> p) {
+    const u32x4 v = *(global_ptr<const u32x4>) p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__host__ __device__ __forceinline__ float h2f(uint32_t bits16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16 & 0xFFFFu)));
 }
 
@@ -27,36 +47,59 @@ __device__ __forceinline__ uint16_t f2h(float f) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
+// DPP lane exchange within rows of 16 lanes (quad_perm / row_ror controls).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+
+__device__ __forceinline__ float lane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Whole-wave reductions: DPP within each 16-lane row (xor 1, xor 2, rotate 4,
+// rotate 8), then the four row results combined from lanes 0/16/32/48 in a
+// fixed order, so every lane gets the same value.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x124>(v);
+    v += dpp_f<0x128>(v);
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x124>(v));
+    v = fmaxf(v, dpp_f<0x128>(v));
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
+// Sum over the 4 lanes of a quad (DPP quad permutations [1,0,3,2], [2,3,0,1]).
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
     return v;
 }
 
-__device__ __forceinline__ int dot16(const uint32_t* w, const uint4& x, int acc) {
-    acc = __builtin_amdgcn_sdot4(static_cast<int>(w[0]), static_cast<int>(x.x), acc, false);
-    acc = __builtin_amdgcn_sdot4(static_cast<int>(w[1]), static_cast<int>(x.y), acc, false);
-    acc = __builtin_amdgcn_sdot4(static_cast<int>(w[2]), static_cast<int>(x.z), acc, false);
-    acc = __builtin_amdgcn_sdot4(static_cast<int>(w[3]), static_cast<int>(x.w), acc, false);
-    return acc;
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int acc) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), acc, false);
 }
 
 __device__ __forceinline__ uint32_t u4_word(const uint4& v, int i) {
     return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
 
-__device__ __forceinline__ uint32_t u4_byte(const uint4& v, int i) {
-    return (u4_word(v, i >> 2) >> (8 * (i & 3))) & 0xFFu;
-}
+__host__ __device__ __forceinline__ int sext8(uint32_t v) { return static_cast<int>(static_cast<int8_t>(v & 0xFFu)); }
 
-// Q4_K 6-bit scale/min of sub-block j from the header's scale bytes (hdr.y..w).
-__device__ __forceinline__ void q4k_scale_min(const uint4& h, int j, int& sc, int& m) {
+// Q4_K 6-bit scale/min of sub-block j from the header's scale bytes (h.y..w).
+__host__ __device__ __forceinline__ void q4k_scale_min(const uint4& h, int j, int& sc, int& m) {
     if (j < 4) {
         sc = (h.y >> (8 * j)) & 63;
         m = (h.z >> (8 * j)) & 63;
@@ -67,56 +110,58 @@ __device__ __forceinline__ void q4k_scale_min(const uint4& h, int j, int& sc, in
     }
 }
 
+__host__ __device__ __forceinline__ uint32_t byte_at(const uint8_t* p) { return *p; }
+
+__host__ __device__ __forceinline__ uint32_t u16_at(const uint8_t* p) {
+    return static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8);
+}
+
+__host__ __device__ __forceinline__ uint32_t u32_at(const uint8_t* p) {
+    return u16_at(p) | (u16_at(p + 2) << 16);
+}
+
 // ------------------------------------------------------------------ element dequantization
-// Exact GGML dequantization of one element from the device layout; the
-// arithmetic order matches the reference formulas (see oracle/jfo_quant.c).
-__device__ float dequant_elem(const DMat& m, uint32_t row, uint32_t c) {
-    const uint8_t* base = m.main + static_cast<size_t>(row) * m.main_row_bytes;
-    switch (m.type) {
-    case 1: return reinterpret_cast<const float*>(base)[c];
-    case 2: return h2f(reinterpret_cast<const uint16_t*>(base)[c]);
-    case 7: {
-        const uint32_t b = c / 32;
-        const float d = h2f(reinterpret_cast<const uint16_t*>(m.aux + static_cast<size_t>(row) * m.aux_row_bytes)[b]);
-        return static_cast<float>(static_cast<int8_t>(base[b * 32 + c % 32])) * d;
-    }
+// Exact GGML dequantization of value k of row i of one tile; the arithmetic
+// order matches the GGML formulas: Q4_K (d*sc)*q - dmin*m, Q6_K
+// (d*sc)*(q-32), Q8_0 q*d, Q2_K (d*sc)*q - dmin*m.
+__host__ __device__ float tile_value(uint32_t type, const uint8_t* tile, uint32_t i, uint32_t k) {
+    const uint32_t g = k / 64, v = k % 64, l = i + 16 * g;
+    auto code_dword = [&](uint32_t base, uint32_t idx) { return u32_at(tile + base + ((idx / 4) * 64 + l) * 16 + 4 * (idx % 4)); };
+    switch (type) {
     case 11: {
-        const uint8_t* blk = base + static_cast<size_t>(c / 256) * 144;
-        const uint32_t i = c % 256;
-        const float d = h2f(blk[0] | (blk[1] << 8)), dmin = h2f(blk[2] | (blk[3] << 8));
-        uint4 h;
-        h.x = 0;
-        h.y = blk[4] | (blk[5] << 8) | (blk[6] << 16) | (uint32_t(blk[7]) << 24);
-        h.z = blk[8] | (blk[9] << 8) | (blk[10] << 16) | (uint32_t(blk[11]) << 24);
-        h.w = blk[12] | (blk[13] << 8) | (blk[14] << 16) | (uint32_t(blk[15]) << 24);
-        const uint32_t byte = blk[16 + (i / 64) * 32 + (i % 32)];
-        const int q = (i % 64) < 32 ? (byte & 0xF) : (byte >> 4);
-        int sc, mn;
-        q4k_scale_min(h, static_cast<int>((i / 64) * 2 + (i % 64) / 32), sc, mn);
+        const uint8_t* hb = tile + 16 * i;
+        const float d = h2f(u16_at(hb)), dmin = h2f(u16_at(hb + 2));
+        const uint32_t f = byte_at(hb + 4 + 3 * g) | (byte_at(hb + 5 + 3 * g) << 8) | (byte_at(hb + 6 + 3 * g) << 16);
+        const uint32_t hi = v >= 32 ? 1u : 0u;
+        const int sc = static_cast<int>((f >> (6 * hi)) & 63), mn = static_cast<int>((f >> (12 + 6 * hi)) & 63);
+        const uint32_t b = v % 32;
+        const uint32_t byte = byte_at(tile + 256 + ((b / 16) * 64 + l) * 16 + b % 16);
+        const int q = hi ? static_cast<int>(byte >> 4) : static_cast<int>(byte & 0xF);
         const float d1 = d * static_cast<float>(sc), m1 = dmin * static_cast<float>(mn);
         return d1 * static_cast<float>(q) - m1;
     }
     case 13: {
-        const uint32_t b = c / 256, i = c % 256;
-        const uint8_t* blk = base + static_cast<size_t>(b) * 208;
-        const float d = h2f(reinterpret_cast<const uint16_t*>(m.aux + static_cast<size_t>(row) * m.aux_row_bytes)[b]);
-        const uint32_t half = i / 128, w = i % 128, quarter = w / 32, l = w % 32;
-        const uint32_t lo = blk[64 * half + l + (quarter & 1) * 32];
-        const uint32_t nib = quarter < 2 ? (lo & 0xF) : (lo >> 4);
-        const uint32_t hi = (blk[128 + 32 * half + l] >> (2 * quarter)) & 3;
-        const int q = static_cast<int>(nib | (hi << 4)) - 32;
-        const float sc = static_cast<float>(static_cast<int8_t>(blk[192 + i / 16]));
-        const float ds = d * sc;
+        const float d = h2f(u16_at(tile + 2 * i));
+        const int sc = sext8(byte_at(tile + 32 + 16 * i + k / 16));
+        const uint32_t w = v % 8;
+        const uint32_t lbyte = (code_dword(288, v / 8) >> (8 * (w % 4))) & 0xFF;
+        const uint32_t low4 = w >= 4 ? (lbyte >> 4) : (lbyte & 0xF);
+        const uint32_t m = v / 16, r = (v % 16) / 4, e = v % 4;
+        const uint32_t h2 = (code_dword(288, 8 + m) >> (8 * e + 2 * r)) & 3;
+        const int q = static_cast<int>(low4 | (h2 << 4)) - 32;
+        const float ds = d * static_cast<float>(sc);
         return ds * static_cast<float>(q);
     }
+    case 7: {
+        const float d = h2f(u16_at(tile + 16 * i + 2 * (k / 32)));
+        const int q = sext8(byte_at(tile + 256 + ((v / 16) * 64 + l) * 16 + v % 16));
+        return static_cast<float>(q) * d;
+    }
     case 9: {
-        const uint32_t b = c / 256, i = c % 256;
-        const uint8_t* blk = base + static_cast<size_t>(b) * 80;
-        const uint32_t dd = reinterpret_cast<const uint32_t*>(m.aux + static_cast<size_t>(row) * m.aux_row_bytes)[b];
-        const float d = h2f(dd), dmin = h2f(dd >> 16);
-        const uint32_t half = i / 128, w = i % 128, shift = w / 32, part = (w % 32) / 16, l = w % 16;
-        const int q = (blk[16 + 32 * half + 16 * part + l] >> (2 * shift)) & 3;
-        const uint32_t sb = blk[i / 16];
+        const float d = h2f(u16_at(tile + 4 * i)), dmin = h2f(u16_at(tile + 4 * i + 2));
+        const uint32_t sb = byte_at(tile + 64 + 16 * i + k / 16);
+        const uint32_t m = v / 16, r = (v % 16) / 4, e = v % 4;
+        const int q = static_cast<int>((code_dword(320, m) >> (8 * e + 2 * r)) & 3);
         const float dl = d * static_cast<float>(sb & 0xF), ml = dmin * static_cast<float>(sb >> 4);
         return dl * static_cast<float>(q) - ml;
     }
@@ -125,28 +170,36 @@ __device__ float dequant_elem(const DMat& m, uint32_t row, uint32_t c) {
     }
 }
 
-__global__ __launch_bounds__(kThreads) void k_dequant_rows(DMat m, int32_t row0, float* out) {
+__device__ float dequant_elem(const DMat& m, uint32_t row, uint32_t c) {
+    if (m.type == 1) return reinterpret_cast<const float*>(m.data + static_cast<size_t>(row) * m.row_bytes)[c];
+    if (m.type == 2) return h2f(reinterpret_cast<const uint16_t*>(m.data + static_cast<size_t>(row) * m.row_bytes)[c]);
+    const uint32_t nb = m.cols / 256;
+    const uint8_t* tile = m.data + (static_cast<size_t>(row / 16) * nb + c / 256) * tile_bytes(m.type);
+    return tile_value(m.type, tile, row % 16, c % 256);
+}
+
+__global__ __launch_bounds__(256) void k_dequant_rows(DMat m, int32_t row0, float* out) {
     const uint32_t r = blockIdx.y;
-    const uint32_t c = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
     if (c < m.cols) out[static_cast<size_t>(r) * m.cols + c] = dequant_elem(m, row0 + r, c);
 }
 
 // ------------------------------------------------------------------ embedding
-__global__ __launch_bounds__(kThreads) void k_embed(DMat table, const StepDev* step, float* h, int32_t H,
-                                                    unsigned long long* best, int32_t n_best) {
+__global__ __launch_bounds__(256) void k_embed(DMat table, const StepDev* step, float* h, int32_t H,
+                                               unsigned long long* best, int32_t n_best) {
     const int r = blockIdx.y;
     if (blockIdx.x == 0 && r == 0) {
-        for (int i = threadIdx.x; i < n_best; i += kThreads) best[i] = 0ull;
+        for (int i = threadIdx.x; i < n_best; i += 256) best[i] = 0ull;
     }
-    const int c = blockIdx.x * kThreads + threadIdx.x;
+    const int c = blockIdx.x * 256 + threadIdx.x;
     if (r < step->n_rows && c < H) {
         h[static_cast<size_t>(r) * H + c] = dequant_elem(table, static_cast<uint32_t>(step->token[r]), c);
     }
 }
 
 // ------------------------------------------------------------------ activation quantization
-// Quantizes 256 values held 4 per lane by one wave: d = amax/127,
-// q = roundf(x * (1/d)), plus the sum of every 16 quantized values.
+// Quantizes 256 values held 4 per lane (values 4L..4L+3 in lane L) by one
+// wave: d = amax/127, q = roundf(x * (1/d)), plus the sum of every 16 codes.
 #pragma clang fp contract(off)
 __device__ __forceinline__ void quant_block_wave(const float v[4], int lane, int8_t* q, float* d, int16_t* s) {
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
@@ -164,242 +217,371 @@ __device__ __forceinline__ void quant_block_wave(const float v[4], int lane, int
     }
     const uint32_t packed = (qi[0] & 0xFF) | ((qi[1] & 0xFF) << 8) | ((qi[2] & 0xFF) << 16) | ((qi[3] & 0xFF) << 24);
     reinterpret_cast<uint32_t*>(q)[lane] = packed;
-    sum += __shfl_xor(sum, 1);
-    sum += __shfl_xor(sum, 2);
+    sum += dpp_i<0xB1>(sum);
+    sum += dpp_i<0x4E>(sum);
     if ((lane & 3) == 0) s[lane >> 2] = static_cast<int16_t>(sum);
     if (lane == 0) *d = db;
 }
-
 #pragma clang fp contract(on)
 
-// ------------------------------------------------------------------ quantized matmul
-// Staged activation chunk in LDS: q [NT][chunk], d [NT][chunk/256], s [NT][chunk/16].
-struct Staged {
-    const int8_t* q;
-    const float* d;
-    const int16_t* s;
-    int32_t chunk;
-};
-
-struct RowRef {
-    const uint8_t* main;
-    const uint8_t* aux;
-    bool valid;
-};
-
-// --- Q4_K: lane part p (0..3) owns qs bytes [32p, 32p+32) = sub-blocks 2p (low nibbles) and 2p+1 (high).
-struct Q4KRegs {
-    uint4 hdr, q0, q1;
-};
-
-__device__ __forceinline__ Q4KRegs q4k_load(const RowRef& r, int gb, int part) {
-    const uint8_t* blk = r.main + static_cast<size_t>(gb) * 144;
-    Q4KRegs v;
-    v.hdr = *reinterpret_cast<const uint4*>(blk);
-    v.q0 = *reinterpret_cast<const uint4*>(blk + 16 + 32 * part);
-    v.q1 = *reinterpret_cast<const uint4*>(blk + 32 + 32 * part);
-    return v;
+__device__ __forceinline__ const float* x_row(const XIn& x, int t) {
+    return x.x + static_cast<size_t>(x.gather ? x.gather[t] : t) * x.stride;
 }
 
-template <int NT>
-__device__ __forceinline__ void q4k_compute(const Q4KRegs& v, int part, const Staged& x, int lb, float* acc) {
-    const float d = h2f(v.hdr.x), dmin = h2f(v.hdr.x >> 16);
-    int sc0, m0, sc1, m1;
-    q4k_scale_min(v.hdr, 2 * part, sc0, m0);
-    q4k_scale_min(v.hdr, 2 * part + 1, sc1, m1);
-    constexpr uint32_t M = 0x0F0F0F0Fu;
-    const uint32_t lo0[4] = {v.q0.x & M, v.q0.y & M, v.q0.z & M, v.q0.w & M};
-    const uint32_t lo1[4] = {v.q1.x & M, v.q1.y & M, v.q1.z & M, v.q1.w & M};
-    const uint32_t hi0[4] = {(v.q0.x >> 4) & M, (v.q0.y >> 4) & M, (v.q0.z >> 4) & M, (v.q0.w >> 4) & M};
-    const uint32_t hi1[4] = {(v.q1.x >> 4) & M, (v.q1.y >> 4) & M, (v.q1.z >> 4) & M, (v.q1.w >> 4) & M};
+// 1/sqrt(mean(x^2) + eps) of each token row (qwen2_architecture.cpp:373-376),
+// reduced by the whole work-group into rs[t]; red holds NT * waves floats.
+template <int NT, int NTHR>
+__device__ void row_rms(const XIn& x, int n_tok, int K, float* rs, float* red) {
+    constexpr int W = NTHR / kWave;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    for (int t = 0; t < n_tok; ++t) {
+        const float* xr = x_row(x, t);
+        float ss = 0.0F;
+        for (int i0 = 4 * threadIdx.x; i0 < K; i0 += 4 * 4 * NTHR) {
+            float4 v[4];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const int8_t* xb = x.q + t * x.chunk + lb * 256 + 64 * part;
-        const uint4 x0 = *reinterpret_cast<const uint4*>(xb);
-        const uint4 x1 = *reinterpret_cast<const uint4*>(xb + 16);
-        const uint4 x2 = *reinterpret_cast<const uint4*>(xb + 32);
-        const uint4 x3 = *reinterpret_cast<const uint4*>(xb + 48);
-        const int i0 = dot16(lo1, x1, dot16(lo0, x0, 0));
-        const int i1 = dot16(hi1, x3, dot16(hi0, x2, 0));
-        const int16_t* s = x.s + t * (x.chunk / 16) + lb * 16 + 4 * part;
-        const int s0 = s[0] + s[1], s1 = s[2] + s[3];
-        const int isum = sc0 * i0 + sc1 * i1;
-        const int msum = m0 * s0 + m1 * s1;
-        acc[t] += x.d[t * (x.chunk / 256) + lb] * (d * static_cast<float>(isum) - dmin * static_cast<float>(msum));
-    }
-}
-
-// --- Q6_K (main 208 B: ql 128 | qh 64 | scales 16; aux: d). Lane part: half = p>>1, s = p&1,
-// l in [16s, 16s+16): four quarters of 16 values each, groups 8*half + 2q + s.
-struct Q6KRegs {
-    uint4 l0, l1, h, sc;
-    uint32_t d;
-};
-
-__device__ __forceinline__ Q6KRegs q6k_load(const RowRef& r, int gb, int part) {
-    const uint8_t* blk = r.main + static_cast<size_t>(gb) * 208;
-    const int half = part >> 1, s = part & 1;
-    Q6KRegs v;
-    v.l0 = *reinterpret_cast<const uint4*>(blk + 64 * half + 16 * s);
-    v.l1 = *reinterpret_cast<const uint4*>(blk + 64 * half + 32 + 16 * s);
-    v.h = *reinterpret_cast<const uint4*>(blk + 128 + 32 * half + 16 * s);
-    v.sc = *reinterpret_cast<const uint4*>(blk + 192);
-    v.d = reinterpret_cast<const uint16_t*>(r.aux)[gb];
-    return v;
-}
-
-template <int NT>
-__device__ __forceinline__ void q6k_compute(const Q6KRegs& v, int part, const Staged& x, int lb, float* acc) {
-    const int half = part >> 1, s = part & 1;
-    const float d = h2f(v.d);
-    uint32_t q[4][4];
-    const uint32_t l0[4] = {v.l0.x, v.l0.y, v.l0.z, v.l0.w};
-    const uint32_t l1[4] = {v.l1.x, v.l1.y, v.l1.z, v.l1.w};
-    const uint32_t hh[4] = {v.h.x, v.h.y, v.h.z, v.h.w};
+            for (int u = 0; u < 4; ++u) {
+                const int i = i0 + u * 4 * NTHR;
+                v[u] = i < K ? *reinterpret_cast<const float4*>(xr + i) : make_float4(0.0F, 0.0F, 0.0F, 0.0F);
+            }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        q[0][i] = (l0[i] & 0x0F0F0F0Fu) | ((hh[i] & 0x03030303u) << 4);
-        q[1][i] = (l1[i] & 0x0F0F0F0Fu) | ((hh[i] << 2) & 0x30303030u);
-        q[2][i] = ((l0[i] >> 4) & 0x0F0F0F0Fu) | (hh[i] & 0x30303030u);
-        q[3][i] = ((l1[i] >> 4) & 0x0F0F0F0Fu) | ((hh[i] >> 2) & 0x30303030u);
-    }
-    int sc[4];
-#pragma unroll
-    for (int qq = 0; qq < 4; ++qq) sc[qq] = static_cast<int8_t>(u4_byte(v.sc, 8 * half + 2 * qq + s));
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const int8_t* xb = x.q + t * x.chunk + lb * 256 + 128 * half + 16 * s;
-        const int16_t* sb = x.s + t * (x.chunk / 16) + lb * 16 + 8 * half + s;
-        int isum = 0;
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-            const uint4 xv = *reinterpret_cast<const uint4*>(xb + 32 * qq);
-            const int iq = dot16(q[qq], xv, 0);
-            isum += sc[qq] * (iq - 32 * static_cast<int>(sb[2 * qq]));
+            for (int u = 0; u < 4; ++u) ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
         }
-        acc[t] += x.d[t * (x.chunk / 256) + lb] * (d * static_cast<float>(isum));
+        ss = wave_sum(ss);
+        if (lane == 0) red[t * W + wave] = ss;
     }
+    __syncthreads();
+    if (threadIdx.x < static_cast<unsigned>(n_tok)) {
+        const int t = threadIdx.x;
+        float ss = 0.0F;
+        for (int w = 0; w < W; ++w) ss += red[t * W + w];
+        rs[t] = 1.0F / sqrtf(ss / static_cast<float>(K) + x.eps);
+    }
+    __syncthreads();
 }
 
-// --- Q2_K (main 80 B: scales 16 | qs 64; aux: d, dmin). Lane part: half = p>>1, prt = p&1;
-// one 16-byte qs slice holds four 2-bit planes (shift k) of 16 values, group 8*half + 2k + prt.
-struct Q2KRegs {
-    uint4 qb, sc;
-    uint32_t dd;
-};
-
-__device__ __forceinline__ Q2KRegs q2k_load(const RowRef& r, int gb, int part) {
-    const uint8_t* blk = r.main + static_cast<size_t>(gb) * 80;
-    const int half = part >> 1, prt = part & 1;
-    Q2KRegs v;
-    v.qb = *reinterpret_cast<const uint4*>(blk + 16 + 32 * half + 16 * prt);
-    v.sc = *reinterpret_cast<const uint4*>(blk);
-    v.dd = reinterpret_cast<const uint32_t*>(r.aux)[gb];
-    return v;
-}
-
-template <int NT>
-__device__ __forceinline__ void q2k_compute(const Q2KRegs& v, int part, const Staged& x, int lb, float* acc) {
-    const int half = part >> 1, prt = part & 1;
-    const float d = h2f(v.dd), dmin = h2f(v.dd >> 16);
-    const uint32_t qw[4] = {v.qb.x, v.qb.y, v.qb.z, v.qb.w};
-    uint32_t vals[4][4];
-    int scl[4], mn[4];
+// Quantizes values [c0, c0 + nb*256) of every token row into the LDS chunk
+// (q [t][chunk] permuted per block, d [t][chunk/256], s [t][chunk/16]), one
+// wave per 256-value block, loads issued kStageBatch blocks at a time. With a
+// gain (RMSNorm input) the codes are those of x * gain and ssq[t][b] receives
+// the block's sum of x^2; the block scales are multiplied by the row's
+// 1/rms afterwards (finish_norm), so one pass over x serves both.
+constexpr int kStageBatch = 4;
+#pragma clang fp contract(off)
+template <int NT, int NTHR>
+__device__ void stage_f32(const XIn& x, const int* rowidx, int n_tok, int c0, int nb, int8_t* sq, float* sd,
+                          int16_t* ss, float* ssq, int chunk) {
+    constexpr int W = NTHR / kWave;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int total = n_tok * nb;
+    // a batch of kStageBatch blocks per wave is requested at once (indices
+    // clamped so that every load is issued unconditionally)
+    for (int j0 = wave; j0 < total; j0 += kStageBatch * W) {
+        float4 v[kStageBatch];
+        float4 gv[kStageBatch];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) vals[k][i] = (qw[i] >> (2 * k)) & 0x03030303u;
-        const uint32_t b = u4_byte(v.sc, 8 * half + 2 * k + prt);
-        scl[k] = static_cast<int>(b & 0xF);
-        mn[k] = static_cast<int>(b >> 4);
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const int8_t* xb = x.q + t * x.chunk + lb * 256 + 128 * half + 16 * prt;
-        const int16_t* sb = x.s + t * (x.chunk / 16) + lb * 16 + 8 * half + prt;
-        int isum = 0, msum = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint4 xv = *reinterpret_cast<const uint4*>(xb + 32 * k);
-            isum += scl[k] * dot16(vals[k], xv, 0);
-            msum += mn[k] * static_cast<int>(sb[2 * k]);
+        for (int u = 0; u < kStageBatch; ++u) {
+            const int j = min(j0 + u * W, total - 1);
+            const int t = j / nb, b = j - t * nb;
+            const int c = c0 + b * 256 + 4 * lane;
+            v[u] = *reinterpret_cast<const float4*>(x.x + static_cast<size_t>(rowidx[t]) * x.stride + c);
+            gv[u] = x.gain ? *reinterpret_cast<const float4*>(x.gain + c) : make_float4(1.0F, 1.0F, 1.0F, 1.0F);
         }
-        acc[t] += x.d[t * (x.chunk / 256) + lb] * (d * static_cast<float>(isum) - dmin * static_cast<float>(msum));
+#pragma unroll
+        for (int u = 0; u < kStageBatch; ++u) {
+            const int j = j0 + u * W;
+            if (j < total) {
+                const int t = j / nb, b = j - t * nb;
+                float vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+                if (x.gain) {
+                    const float sq2 = wave_sum(vv[0] * vv[0] + vv[1] * vv[1] + vv[2] * vv[2] + vv[3] * vv[3]);
+                    if (lane == 0) ssq[t * nb + b] = sq2;
+                    vv[0] = vv[0] * gv[u].x;
+                    vv[1] = vv[1] * gv[u].y;
+                    vv[2] = vv[2] * gv[u].z;
+                    vv[3] = vv[3] * gv[u].w;
+                }
+                quant_block_wave(vv, lane, sq + t * chunk + b * 256, sd + t * (chunk / 256) + b,
+                                 ss + t * (chunk / 16) + b * 16);
+            }
+        }
     }
 }
 
-// --- Q8_0 (main 32 B qs per 32 values; aux: d). Lane part p owns Q8_0 blocks 8*gb + 2p, +1.
-struct Q80Regs {
-    uint4 w0, w1, w2, w3;
-    uint32_t dd;
+// After stage_f32 with a gain over the whole row (nb blocks): rs = 1/sqrt(
+// sum(x^2)/K + eps) per token (block sums added in block order) scales the
+// token's block scales (qwen2_architecture.cpp:373-376).
+template <int NTHR>
+__device__ void finish_norm(int n_tok, int nb, int K, float eps, const float* ssq, float* sd, float* rs, int chunk) {
+    __syncthreads();
+    if (threadIdx.x < static_cast<unsigned>(n_tok)) {
+        const int t = threadIdx.x;
+        float sum = 0.0F;
+        for (int b = 0; b < nb; ++b) sum += ssq[t * nb + b];
+        rs[t] = 1.0F / sqrtf(sum / static_cast<float>(K) + eps);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n_tok * nb; i += NTHR) {
+        const int t = i / nb, b = i - t * nb;
+        sd[t * (chunk / 256) + b] = sd[t * (chunk / 256) + b] * rs[t];
+    }
+}
+#pragma clang fp contract(on)
+
+// Copies values [c0, c0 + nb*256) of pre-quantized rows into the LDS chunk,
+// every thread requesting up to 4 pieces before storing any.
+template <int NTHR>
+__device__ void stage_act8(const Act8& xq, int n_tok, int c0, int nb, int8_t* sq, float* sd, int16_t* ss, int chunk) {
+    const int n16 = nb * 16;                     // uint4 of codes per token
+    const int nq = n_tok * n16, ns = n_tok * nb * 2, nd = n_tok * nb;
+    const int total = nq + ns;                    // uint4 pieces (codes, then sums)
+    for (int i0 = threadIdx.x; i0 < total; i0 += 4 * NTHR) {
+        uint4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = min(i0 + u * NTHR, total - 1);
+            const bool codes = i < nq;
+            const int t = codes ? i / n16 : (i - nq) / (nb * 2);
+            const int k = codes ? i - t * n16 : (i - nq) - t * nb * 2;
+            const uint4* src = codes ? reinterpret_cast<const uint4*>(xq.q + static_cast<size_t>(t) * xq.K + c0)
+                                     : reinterpret_cast<const uint4*>(xq.s + static_cast<size_t>(t) * (xq.K / 16) + c0 / 16);
+            v[u] = src[k];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + u * NTHR;
+            if (i < nq) {
+                const int t = i / n16, k = i - t * n16;
+                reinterpret_cast<uint4*>(sq + t * chunk)[k] = v[u];
+            } else if (i < total) {
+                const int t = (i - nq) / (nb * 2), k = (i - nq) - t * nb * 2;
+                reinterpret_cast<uint4*>(ss + t * (chunk / 16))[k] = v[u];
+            }
+        }
+    }
+    for (int i = threadIdx.x; i < nd; i += NTHR) {
+        const int t = i / nb, b = i - t * nb;
+        sd[t * (chunk / 256) + b] = xq.d[static_cast<size_t>(t) * (xq.K / 256) + c0 / 256 + b];
+    }
+}
+
+// ------------------------------------------------------------------ tile dot products
+// Lane (i = lane % 16, g = lane / 16) of a wave holds row i's values
+// 64 g .. 64 g + 63 of one tile (whole sub-blocks of every type); for every
+// token it computes the integer dots of those codes with the int8
+// activation values 64 g .. 64 g + 63 of the block (LDS) and adds its share
+// of the block's scaled sum to acc[t].
+struct XLds {
+    const int8_t* q;    // token 0, block start + 64 g
+    const float* d;     // token 0 block scale
+    const int16_t* s;   // token 0 block sums (16 per block)
+    int32_t q_stride;   // bytes between tokens
+    int32_t d_stride;   // floats between tokens
+    int32_t s_stride;   // int16 between tokens
 };
 
-__device__ __forceinline__ Q80Regs q80_load(const RowRef& r, int gb, int part) {
-    const int b = gb * 8 + 2 * part;
-    const uint8_t* p = r.main + static_cast<size_t>(b) * 32;
-    Q80Regs v;
-    v.w0 = *reinterpret_cast<const uint4*>(p);
-    v.w1 = *reinterpret_cast<const uint4*>(p + 16);
-    v.w2 = *reinterpret_cast<const uint4*>(p + 32);
-    v.w3 = *reinterpret_cast<const uint4*>(p + 48);
-    v.dd = *reinterpret_cast<const uint32_t*>(r.aux + static_cast<size_t>(b) * 2);
-    return v;
-}
-
-template <int NT>
-__device__ __forceinline__ void q80_compute(const Q80Regs& v, int part, const Staged& x, int lb, float* acc) {
-    const float d0 = h2f(v.dd), d1 = h2f(v.dd >> 16);
-    const uint32_t w0[4] = {v.w0.x, v.w0.y, v.w0.z, v.w0.w};
-    const uint32_t w1[4] = {v.w1.x, v.w1.y, v.w1.z, v.w1.w};
-    const uint32_t w2[4] = {v.w2.x, v.w2.y, v.w2.z, v.w2.w};
-    const uint32_t w3[4] = {v.w3.x, v.w3.y, v.w3.z, v.w3.w};
+__device__ __forceinline__ void load_x(const XLds& x, int t, uint32_t (&xw)[16]) {
+    const uint4* p = reinterpret_cast<const uint4*>(x.q + t * x.q_stride);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const int8_t* xb = x.q + t * x.chunk + lb * 256 + 64 * part;
-        const int i0 = dot16(w1, *reinterpret_cast<const uint4*>(xb + 16), dot16(w0, *reinterpret_cast<const uint4*>(xb), 0));
-        const int i1 = dot16(w3, *reinterpret_cast<const uint4*>(xb + 48), dot16(w2, *reinterpret_cast<const uint4*>(xb + 32), 0));
-        acc[t] += x.d[t * (x.chunk / 256) + lb] * (d0 * static_cast<float>(i0) + d1 * static_cast<float>(i1));
+    for (int u = 0; u < 4; ++u) {
+        const uint4 v = p[u];
+        xw[4 * u] = v.x;
+        xw[4 * u + 1] = v.y;
+        xw[4 * u + 2] = v.z;
+        xw[4 * u + 3] = v.w;
     }
 }
 
-// Load/compute split per block type, so that a wave can issue the loads of
-// all of its rows (and two block iterations) before consuming any of them.
+__device__ __forceinline__ int mul24(int a, int b) { return __mul24(a, b); }
+
+
 template <uint32_t TYPE>
-struct QBlock;
+struct Tile;
+
+// Q4_K: header of row i | codes: the lane's 32 qs bytes (sub-blocks 2g, 2g+1).
+// The lane reads d|dmin and the 8 header bytes that hold its 24-bit scale
+// field (header byte 4 + 3g) starting at the enclosing word.
 template <>
-struct QBlock<11> {
-    using Regs = Q4KRegs;
-    static __device__ __forceinline__ Regs load(const RowRef& r, int gb, int part) { return q4k_load(r, gb, part); }
+struct Tile<11> {
+    struct Regs {
+        uint4 w0, w1;
+        uint2 f;
+        uint32_t dd;
+    };
+    static __device__ __forceinline__ Regs load(const uint8_t* t, int lane) {
+        Regs r;
+        const int i = lane & 15, g = lane >> 4;
+        r.dd = *reinterpret_cast<const uint32_t*>(t + 16 * i);
+        r.f = *reinterpret_cast<const uint2*>(t + 16 * i + 4 + 4 * ((3 * g) >> 2));
+        r.w0 = *reinterpret_cast<const uint4*>(t + 256 + 16 * lane);
+        r.w1 = *reinterpret_cast<const uint4*>(t + 1280 + 16 * lane);
+        return r;
+    }
     template <int NT>
-    static __device__ __forceinline__ void dot(const Regs& v, int part, const Staged& x, int lb, float* acc) {
-        q4k_compute<NT>(v, part, x, lb, acc);
+    static __device__ __forceinline__ void dot(const Regs& r, int g, const XLds& x, int nt, float* acc) {
+        const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
+        // the lane group's 24-bit field: sc 2g | sc 2g+1 | m 2g | m 2g+1
+        const uint32_t f = __builtin_amdgcn_alignbyte(r.f.y, r.f.x, (3 * g) & 3);
+        const int sca = f & 63, scb = (f >> 6) & 63, ma = (f >> 12) & 63, mb = (f >> 18) & 63;
+        const uint32_t pw[8] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w, r.w1.x, r.w1.y, r.w1.z, r.w1.w};
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            lo[k] = pw[k] & 0x0F0F0F0Fu;
+            hi[k] = (pw[k] >> 4) & 0x0F0F0F0Fu;
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (t < nt) {
+                uint32_t xw[16];
+                load_x(x, t, xw);
+                int da = 0, db = 0;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    da = sdot4(lo[k], xw[k], da);
+                    db = sdot4(hi[k], xw[8 + k], db);
+                }
+                const int16_t* s = x.s + t * x.s_stride + 4 * g;
+                const int isum = mul24(sca, da) + mul24(scb, db);
+                const int msum = mul24(ma, s[0] + s[1]) + mul24(mb, s[2] + s[3]);
+                acc[t] += x.d[t * x.d_stride] * (d * static_cast<float>(isum) - dmin * static_cast<float>(msum));
+            }
+        }
     }
 };
+
+// Q6_K: d[16] | scales[16][16] | codes (8 low-nibble + 4 high-bit dwords per lane).
 template <>
-struct QBlock<13> {
-    using Regs = Q6KRegs;
-    static __device__ __forceinline__ Regs load(const RowRef& r, int gb, int part) { return q6k_load(r, gb, part); }
+struct Tile<13> {
+    struct Regs {
+        uint4 c0, c1, c2;
+        uint32_t scw, d;
+    };
+    static __device__ __forceinline__ Regs load(const uint8_t* t, int lane) {
+        Regs r;
+        r.c0 = *reinterpret_cast<const uint4*>(t + 288 + 16 * lane);
+        r.c1 = *reinterpret_cast<const uint4*>(t + 1312 + 16 * lane);
+        r.c2 = *reinterpret_cast<const uint4*>(t + 2336 + 16 * lane);
+        r.scw = *reinterpret_cast<const uint32_t*>(t + 32 + 16 * (lane & 15) + 4 * (lane >> 4));
+        r.d = *reinterpret_cast<const uint16_t*>(t + 2 * (lane & 15));
+        return r;
+    }
     template <int NT>
-    static __device__ __forceinline__ void dot(const Regs& v, int part, const Staged& x, int lb, float* acc) {
-        q6k_compute<NT>(v, part, x, lb, acc);
+    static __device__ __forceinline__ void dot(const Regs& r, int g, const XLds& x, int nt, float* acc) {
+        const float d = h2f(r.d);
+        const uint32_t L[8] = {r.c0.x, r.c0.y, r.c0.z, r.c0.w, r.c1.x, r.c1.y, r.c1.z, r.c1.w};
+        const uint32_t Hb[4] = {r.c2.x, r.c2.y, r.c2.z, r.c2.w};
+        constexpr uint32_t M4 = 0x0F0F0F0Fu, M30 = 0x30303030u;
+        uint32_t w[16];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            w[4 * m] = (L[2 * m] & M4) | ((Hb[m] << 4) & M30);
+            w[4 * m + 1] = ((L[2 * m] >> 4) & M4) | ((Hb[m] << 2) & M30);
+            w[4 * m + 2] = (L[2 * m + 1] & M4) | (Hb[m] & M30);
+            w[4 * m + 3] = ((L[2 * m + 1] >> 4) & M4) | ((Hb[m] >> 2) & M30);
+        }
+        int sc[4];  // scales of sub-blocks 4g .. 4g+3
+#pragma unroll
+        for (int m = 0; m < 4; ++m) sc[m] = sext8(r.scw >> (8 * m));
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (t < nt) {
+                uint32_t xw[16];
+                load_x(x, t, xw);
+                const int16_t* s = x.s + t * x.s_stride + 4 * g;
+                int isum = 0;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    int dm = 0;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) dm = sdot4(w[4 * m + q], xw[4 * m + q], dm);
+                    isum += mul24(sc[m], dm - 32 * s[m]);
+                }
+                acc[t] += x.d[t * x.d_stride] * (d * static_cast<float>(isum));
+            }
+        }
     }
 };
+
+// Q8_0: d[16][8] | codes (the int8 values of GGML blocks 2g, 2g+1).
 template <>
-struct QBlock<9> {
-    using Regs = Q2KRegs;
-    static __device__ __forceinline__ Regs load(const RowRef& r, int gb, int part) { return q2k_load(r, gb, part); }
+struct Tile<7> {
+    struct Regs {
+        uint4 c[4];
+        uint32_t dd;
+    };
+    static __device__ __forceinline__ Regs load(const uint8_t* t, int lane) {
+        Regs r;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) r.c[u] = *reinterpret_cast<const uint4*>(t + 256 + 1024 * u + 16 * lane);
+        r.dd = *reinterpret_cast<const uint32_t*>(t + 16 * (lane & 15) + 4 * (lane >> 4));
+        return r;
+    }
     template <int NT>
-    static __device__ __forceinline__ void dot(const Regs& v, int part, const Staged& x, int lb, float* acc) {
-        q2k_compute<NT>(v, part, x, lb, acc);
+    static __device__ __forceinline__ void dot(const Regs& r, int g, const XLds& x, int nt, float* acc) {
+        (void) g;
+        const float da = h2f(r.dd), db = h2f(r.dd >> 16);
+        const uint32_t w[16] = {r.c[0].x, r.c[0].y, r.c[0].z, r.c[0].w, r.c[1].x, r.c[1].y, r.c[1].z, r.c[1].w,
+                                r.c[2].x, r.c[2].y, r.c[2].z, r.c[2].w, r.c[3].x, r.c[3].y, r.c[3].z, r.c[3].w};
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (t < nt) {
+                uint32_t xw[16];
+                load_x(x, t, xw);
+                int ia = 0, ib = 0;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    ia = sdot4(w[k], xw[k], ia);
+                    ib = sdot4(w[8 + k], xw[8 + k], ib);
+                }
+                acc[t] += x.d[t * x.d_stride] * (da * static_cast<float>(ia) + db * static_cast<float>(ib));
+            }
+        }
     }
 };
+
+// Q2_K: (d, dmin)[16] | scales[16][16] | codes (4 dwords per lane).
 template <>
-struct QBlock<7> {
-    using Regs = Q80Regs;
-    static __device__ __forceinline__ Regs load(const RowRef& r, int gb, int part) { return q80_load(r, gb, part); }
+struct Tile<9> {
+    struct Regs {
+        uint4 c;
+        uint32_t scw, dd;
+    };
+    static __device__ __forceinline__ Regs load(const uint8_t* t, int lane) {
+        Regs r;
+        r.c = *reinterpret_cast<const uint4*>(t + 320 + 16 * lane);
+        r.scw = *reinterpret_cast<const uint32_t*>(t + 64 + 16 * (lane & 15) + 4 * (lane >> 4));
+        r.dd = *reinterpret_cast<const uint32_t*>(t + 4 * (lane & 15));
+        return r;
+    }
     template <int NT>
-    static __device__ __forceinline__ void dot(const Regs& v, int part, const Staged& x, int lb, float* acc) {
-        q80_compute<NT>(v, part, x, lb, acc);
+    static __device__ __forceinline__ void dot(const Regs& r, int g, const XLds& x, int nt, float* acc) {
+        const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
+        const uint32_t Q[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
+        int sc[4], mn[4];  // scale bytes of sub-blocks 4g .. 4g+3
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            sc[m] = (r.scw >> (8 * m)) & 0xF;
+            mn[m] = (r.scw >> (8 * m + 4)) & 0xF;
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (t < nt) {
+                uint32_t xw[16];
+                load_x(x, t, xw);
+                const int16_t* s = x.s + t * x.s_stride + 4 * g;
+                int isum = 0, msum = 0;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    int dm = 0;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) dm = sdot4((Q[m] >> (2 * q)) & 0x03030303u, xw[4 * m + q], dm);
+                    isum += mul24(sc[m], dm);
+                    msum += mul24(mn[m], s[m]);
+                }
+                acc[t] += x.d[t * x.d_stride] * (d * static_cast<float>(isum) - dmin * static_cast<float>(msum));
+            }
+        }
     }
 };
 
@@ -409,98 +591,7 @@ __device__ __forceinline__ unsigned long long pack_best(float v, uint32_t idx) {
     return (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFu - idx);
 }
 
-// Sum over the 4 lanes of a quad (DPP quad permutations [1,0,3,2], [2,3,0,1]).
-__device__ __forceinline__ float quad_sum(float v) {
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
-    return v;
-}
-
-__device__ __forceinline__ const float* x_row(const XIn& x, int t) {
-    return x.x + static_cast<size_t>(x.gather ? x.gather[t] : t) * x.stride;
-}
-
-// 1/sqrt(mean(x^2) + eps) of each token row (qwen2_architecture.cpp:373-376),
-// reduced by the whole work-group into rs[t].
-template <int NT>
-__device__ void row_rms(const XIn& x, int n_tok, int K, float* rs, float* red) {
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    for (int t = 0; t < n_tok; ++t) {
-        const float* xr = x_row(x, t);
-        float ss = 0.0F;
-        for (int i0 = 4 * threadIdx.x; i0 < K; i0 += 4 * 4 * kThreads) {
-            float4 v[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int i = i0 + u * 4 * kThreads;
-                v[u] = i < K ? *reinterpret_cast<const float4*>(xr + i) : make_float4(0.0F, 0.0F, 0.0F, 0.0F);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
-        }
-        ss = wave_sum(ss);
-        if (lane == 0) red[t * (kThreads / kWave) + wave] = ss;
-    }
-    __syncthreads();
-    if (threadIdx.x < static_cast<unsigned>(n_tok)) {
-        const int t = threadIdx.x;
-        float ss = 0.0F;
-        for (int w = 0; w < kThreads / kWave; ++w) ss += red[t * (kThreads / kWave) + w];
-        rs[t] = 1.0F / sqrtf(ss / static_cast<float>(K) + x.eps);
-    }
-    __syncthreads();
-}
-
-// Quantizes values [c0, c0 + nb*256) of every token row into the LDS chunk
-// (int8, scale per 256 values, int16 sums per 16), one wave per 256-value
-// block, loads issued four blocks at a time.
-#pragma clang fp contract(off)
-template <int NT>
-__device__ void stage_chunk(const XIn& x, int n_tok, int c0, int nb, const float* rs, int8_t* sq, float* sd,
-                            int16_t* ss, int chunk) {
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    constexpr int W = kThreads / kWave;
-    const int total = n_tok * nb;
-    for (int j0 = wave; j0 < total; j0 += 4 * W) {
-        float4 v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int j = j0 + u * W;
-            if (j < total) {
-                const int t = j / nb, b = j - t * nb;
-                const int c = c0 + b * 256 + 4 * lane;
-                v[u] = *reinterpret_cast<const float4*>(x_row(x, t) + c);
-                if (x.gain) {
-                    const float r = rs[t];
-                    const float4 g = *reinterpret_cast<const float4*>(x.gain + c);
-                    v[u].x = v[u].x * r * g.x;
-                    v[u].y = v[u].y * r * g.y;
-                    v[u].z = v[u].z * r * g.z;
-                    v[u].w = v[u].w * r * g.w;
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int j = j0 + u * W;
-            if (j < total) {
-                const int t = j / nb, b = j - t * nb;
-                const float vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-                quant_block_wave(vv, lane, sq + t * chunk + b * 256, sd + t * (chunk / 256) + b,
-                                 ss + t * (chunk / 16) + b * 16);
-            }
-        }
-    }
-}
-#pragma clang fp contract(on)
-
-// Launch geometry of one quantized matmul, fixed by the host.
-struct GemvGeom {
-    int32_t rows_per_wg;  // rows of one work-group (even; a multiple of 2*kGluGroup for SwiGLU)
-    int32_t chunk;        // K values staged per pass (multiple of 256)
-    uint64_t nbc_magic;   // ceil(2^32 / nbc), nbc = chunk / 256: f / nbc = (f * magic) >> 32
-};
-
+// ------------------------------------------------------------------ matmul epilogues
 #pragma clang fp contract(off)
 __device__ __forceinline__ void qkv_store(const GemvArgs& a, int t, int gr, float va, float vb, bool pair) {
     // gr: first fused row of a rotated pair (q or k) or a v row (pair == false)
@@ -523,27 +614,30 @@ __device__ __forceinline__ void qkv_store(const GemvArgs& a, int t, int gr, floa
             q[i + half] = r1;
         } else {
             const size_t row = ((static_cast<size_t>(o.layer) * o.n_head_kv + head) * sd.capacity + pos) * hd;
-            sd.k[row + i] = f2h(r0);
-            sd.k[row + i + half] = f2h(r1);
+            global_ptr<uint16_t> kc = as_global(sd.k);
+            kc[row + i] = f2h(r0);
+            kc[row + i + half] = f2h(r1);
         }
     } else {
         const int g = gr - Hq - kv;
         const int head = g / hd, dcol = g % hd;
         const size_t row = ((static_cast<size_t>(o.layer) * o.n_head_kv + head) * sd.capacity + pos) * hd;
-        sd.v[row + dcol] = f2h(va);
+        as_global(sd.v)[row + dcol] = f2h(va);
     }
 }
 #pragma clang fp contract(on)
 
-// Row results of a work-group (sums in LDS) -> bias / residual / SwiGLU /
-// RoPE + cache / greedy argmax. `sum(j, t)` returns the dot of local row j.
-template <int NT, typename Sum>
+// Row results of a work-group -> bias / residual / SwiGLU / RoPE + cache /
+// greedy argmax. `sum(j, t)` returns the dot of local row j for token t;
+// lv holds nrows * n_tok floats of scratch.
+template <int NTHR, typename Sum>
 __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, float* lv) {
+    constexpr int W = NTHR / kWave;
     const int n = nrows * a.n_tok;
     switch (a.mode) {
     case kStore:
     case kAdd:
-        for (int idx = threadIdx.x; idx < n; idx += kThreads) {
+        for (int idx = threadIdx.x; idx < n; idx += NTHR) {
             const int t = idx / nrows, j = idx - t * nrows, gr = row0 + j;
             float* out = a.y + static_cast<size_t>(t) * a.y_stride + gr;
             if (a.mode == kAdd) *out += sum(j, t);
@@ -552,7 +646,7 @@ __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, f
         break;
     case kSwiGLU: {
         const int half = nrows / 2;
-        for (int idx = threadIdx.x; idx < half * a.n_tok; idx += kThreads) {
+        for (int idx = threadIdx.x; idx < half * a.n_tok; idx += NTHR) {
             const int t = idx / half, jj = idx - t * half;
             const int j = (jj / kGluGroup) * 2 * kGluGroup + jj % kGluGroup;
             const float g = sum(j, t), u = sum(j + kGluGroup, t);
@@ -563,7 +657,7 @@ __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, f
     }
     case kQKV: {
         const int Hq = a.qkv.n_head * a.qkv.head_dim, kv = a.qkv.n_head_kv * a.qkv.head_dim;
-        for (int idx = threadIdx.x; idx < n; idx += kThreads) {
+        for (int idx = threadIdx.x; idx < n; idx += NTHR) {
             const int t = idx / nrows, j = idx - t * nrows, gr = row0 + j;
             const float* bias = a.mat.bias;
             if (gr < Hq + kv) {
@@ -577,7 +671,7 @@ __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, f
         break;
     }
     case kLogits: {
-        for (int idx = threadIdx.x; idx < n; idx += kThreads) {
+        for (int idx = threadIdx.x; idx < n; idx += NTHR) {
             const int t = idx / nrows, j = idx - t * nrows, gr = row0 + j;
             const float v = sum(j, t) + (a.mat.bias ? a.mat.bias[gr] : 0.0F);
             if (a.store_logits) a.y[static_cast<size_t>(t) * a.y_stride + gr] = v;
@@ -586,7 +680,7 @@ __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, f
         __syncthreads();
         // one wave per token: lanes scan rows, then a wave argmax (first maximum)
         const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-        for (int t = wave; t < a.n_tok; t += kThreads / kWave) {
+        for (int t = wave; t < a.n_tok; t += W) {
             float bv = -INFINITY;
             int bi = -1;
             for (int j = lane; j < nrows; j += kWave) {
@@ -611,104 +705,204 @@ __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, f
     }
 }
 
-// Quantized matmul. Work-group w owns rows [w*RW, w*RW + RW) and streams
-// their blocks as one flat list (row-major, so contiguous in memory): quad q
-// of the 64 lane quads takes flat blocks q, q + 64, ..., two per iteration
-// with both loads issued first. Each block's dot (4 lanes, one per quarter)
-// is quad-reduced and added to its own LDS slot; rows are then summed over
-// their slots in a fixed order, so results do not depend on scheduling.
-// The activation is quantized into LDS by the work-group itself (after the
-// optional RMSNorm), chunk by chunk when it does not fit at once.
+// ------------------------------------------------------------------ quantized matmul
+// Work-group = kMmWaves waves owning `rgw` consecutive 16-row groups. For
+// every staged K chunk, wave w takes the chunk's tiles b = w, w + W, ... of
+// each of the group's row groups, as one flat item stream with the next
+// kMmDepth tiles' loads in flight (the first ones issued before the
+// activation prologue). A lane accumulates its share of a row group's 16
+// rows; when the stream leaves a row group, the four lane groups are summed
+// and the wave's partial row sums added to its own LDS slot. Row results are
+// the sum of the waves' slots in wave order, so they do not depend on
+// scheduling.
+#ifndef JFH_MM_WAVES
+#define JFH_MM_WAVES 8
+#endif
+#ifndef JFH_MM_DEPTH
+#define JFH_MM_DEPTH 3
+#endif
+#ifndef JFH_MM_MIN_WGS
+#define JFH_MM_MIN_WGS 1
+#endif
+constexpr int kMmWaves = JFH_MM_WAVES;
+constexpr int kMmThreads = kMmWaves * kWave;
+constexpr int kMmDepth = JFH_MM_DEPTH;
+
+struct MmGeom {
+    int32_t rgw;    // row groups per work-group
+    int32_t chunk;  // K values staged per pass (multiple of 256)
+};
+
 template <uint32_t TYPE, int NT>
-__global__ __launch_bounds__(kThreads) void k_gemv_q(GemvArgs a, GemvGeom g) {
-    using B = QBlock<TYPE>;
+__global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, MmGeom geo) {
+    using T = Tile<TYPE>;
+    using Regs = typename T::Regs;
+    constexpr int W = kMmWaves;
+    constexpr uint32_t TB = tile_bytes(TYPE);
     extern __shared__ __align__(16) uint8_t lds_raw[];
-    const int K = static_cast<int>(a.mat.cols);
-    const int chunk = g.chunk, nbc = chunk / 256, RW = g.rows_per_wg;
-    const int n_tok = NT;  // token groups are launched with exactly NT rows
+    const int K = static_cast<int>(a.mat.cols), nb = K / 256;
+    const int chunk = geo.chunk, nbc = chunk / 256, rgw = geo.rgw;
+    const int n_tok = a.n_tok;
     int8_t* sq = reinterpret_cast<int8_t*>(lds_raw);
     float* sd = reinterpret_cast<float*>(lds_raw + NT * chunk);
     int16_t* ss = reinterpret_cast<int16_t*>(sd + NT * nbc);
-    float* part = reinterpret_cast<float*>(ss + NT * (chunk / 16));
-    float* small = part + RW * nbc * NT;  // rs[NT], red[NT*4], logits values [RW*NT]
-    float* rs = small;
-    float* red = small + NT;
-    float* lv = red + NT * (kThreads / kWave);
+    float* part = reinterpret_cast<float*>(ss + NT * (chunk / 16));  // [rgw][W][64 lanes][NT]
+    float* rs = part + rgw * W * 64 * NT;
+    float* ssq = rs + NT;       // [NT][nbc] block sums of squares (normed inputs)
+    float* lv = ssq + NT * nbc;  // [rgw * 16 * NT]
+    int* rowidx = reinterpret_cast<int*>(lv + rgw * 16 * NT);  // [NT] source row of each token
 
-    const int row0 = blockIdx.x * RW;
-    const int nrows = min(RW, static_cast<int>(a.mat.rows) - row0);
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int part_id = lane & 3, quad = wave * (kWave / 4) + (lane >> 2);
-    const Staged st{sq, sd, ss, chunk};
+    const int n_rg = (static_cast<int>(a.mat.rows) + 15) / 16;
+    const int rg0 = blockIdx.x * rgw;
+    const int rgn = min(rgw, n_rg - rg0);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+    const int grp = lane >> 4;
+    const uint8_t* base = a.mat.data + static_cast<size_t>(rg0) * nb * TB;
+    const int row0 = rg0 * 16;
+    const int nrows = min(rgn * 16, static_cast<int>(a.mat.rows) - row0);
 
-    if (a.x.gain) row_rms<NT>(a.x, n_tok, K, rs, red);
-    for (int i = threadIdx.x; i < RW * nbc * NT; i += kThreads) part[i] = 0.0F;
+    // items of the wave in a chunk of nbcur tiles: per row group the tiles w, w+W, ...
+    auto per_rg = [&](int nbcur) { return nbcur > wave ? (nbcur - wave + W - 1) / W : 0; };
 
-    const size_t rb = a.mat.main_row_bytes, ab = a.mat.aux_row_bytes;
-    const uint8_t* main0 = a.mat.main + static_cast<size_t>(row0) * rb;
-    const uint8_t* aux0 = a.mat.aux ? a.mat.aux + static_cast<size_t>(row0) * ab : nullptr;
-    const int total = nrows * nbc;
-    for (int c0 = 0; c0 < K; c0 += chunk) {
-        const int nb = min(chunk, K - c0) / 256;
-        __syncthreads();
-        stage_chunk<NT>(a.x, n_tok, c0, nb, rs, sq, sd, ss, chunk);
-        __syncthreads();
-        for (int f0 = quad; f0 < total; f0 += 2 * kWave) {
-            const int f1 = f0 + kWave;
-            const int r0 = static_cast<int>((static_cast<uint64_t>(f0) * g.nbc_magic) >> 32);
-            const int r1 = static_cast<int>((static_cast<uint64_t>(f1) * g.nbc_magic) >> 32);
-            const int b0 = f0 - r0 * nbc, b1 = f1 - r1 * nbc;
-            const bool ok0 = b0 < nb, ok1 = f1 < total && b1 < nb;
-            typename B::Regs v0, v1;
-            if (ok0) v0 = B::load(RowRef{main0 + r0 * rb, aux0 ? aux0 + r0 * ab : nullptr, true}, c0 / 256 + b0, part_id);
-            if (ok1) v1 = B::load(RowRef{main0 + r1 * rb, aux0 ? aux0 + r1 * ab : nullptr, true}, c0 / 256 + b1, part_id);
-            float s0[NT], s1[NT];
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                s0[t] = 0.0F;
-                s1[t] = 0.0F;
+    // The wave's stream of (row group r, tile m) items keeps kMmDepth tile
+    // loads in flight: slot u is consumed, then refilled with the item
+    // kMmDepth ahead. The load cursor stops at the stream's last item, so
+    // every load is issued unconditionally and the compiler counts
+    // outstanding loads exactly.
+    Regs ring[kMmDepth];
+    int nbcur = min(nbc, nb);
+    int pr = per_rg(nbcur);
+    int total = pr * rgn;
+    // load cursor: byte offset of the next item, its tile index in the row
+    // group and the number of items still to be loaded after it
+    uint32_t loff = 0;
+    int lm = 0, lleft = 0;
+    auto load_next = [&](Regs& slot) {
+        slot = T::load(base + loff, lane);
+        if (lleft > 0) {
+            --lleft;
+            if (lm + 1 < pr) {
+                ++lm;
+                loff += W * TB;
+            } else {
+                lm = 0;
+                loff += (nb - (pr - 1) * W) * TB;
             }
-            if (ok0) B::template dot<NT>(v0, part_id, st, b0, s0);
-            if (ok1) B::template dot<NT>(v1, part_id, st, b1, s1);
+        }
+    };
+    auto prefetch = [&](int c0b) {
+        loff = static_cast<uint32_t>(c0b + wave) * TB;
+        lm = 0;
+        lleft = total - 1;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                s0[t] = quad_sum(s0[t]);
-                s1[t] = quad_sum(s1[t]);
-            }
-            if (part_id == 0) {
+        for (int u = 0; u < kMmDepth; ++u) load_next(ring[u]);
+    };
+    if (total > 0) prefetch(0);
+    // the residual the epilogue adds to is fetched with the first weights
+    float y_pre = 0.0F;
+    if (a.mode == kAdd && threadIdx.x < static_cast<unsigned>(nrows * n_tok)) {
+        const int t = threadIdx.x / nrows, j = threadIdx.x - t * nrows;
+        y_pre = a.y[static_cast<size_t>(t) * a.y_stride + row0 + j];
+    }
+    const bool act8 = a.xq.q != nullptr;
+    if (threadIdx.x < NT) {
+        const int t = min(static_cast<int>(threadIdx.x), n_tok - 1);
+        rowidx[threadIdx.x] = act8 ? t : (a.x.gather ? a.x.gather[t] : t);
+    }
+    for (int i = threadIdx.x; i < rgw * W * 64 * NT; i += kMmThreads) part[i] = 0.0F;
+
+    for (int c0b = 0;;) {
+        __syncthreads();
+        if (act8) {
+            stage_act8<kMmThreads>(a.xq, n_tok, c0b * 256, nbcur, sq, sd, ss, chunk);
+        } else {
+            stage_f32<NT, kMmThreads>(a.x, rowidx, n_tok, c0b * 256, nbcur, sq, sd, ss, ssq, chunk);
+            if (a.x.gain) finish_norm<kMmThreads>(n_tok, nbcur, K, a.x.eps, ssq, sd, rs, chunk);
+        }
+        __syncthreads();
+        if (total > 0) {
+            float acc[NT];
+            int cm = 0;                                             // tile of the row group being computed
+            float* slot = part + (wave * 64 + lane) * NT;          // the lane's running sums of that row group
+            const int8_t* xq0 = sq + wave * 256 + 64 * grp;         // its activation slice
+            for (int n0 = 0; n0 < total; n0 += kMmDepth) {
 #pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    if (ok0) part[f0 * NT + t] += s0[t];
-                    if (ok1) part[f1 * NT + t] += s1[t];
+                for (int u = 0; u < kMmDepth; ++u) {
+                    if (n0 + u < total) {
+                        if (cm == 0) {
+#pragma unroll
+                            for (int t = 0; t < NT; ++t) acc[t] = slot[t];
+                        }
+                        const int bl = wave + W * cm;
+                        XLds x;
+                        x.q = xq0 + W * 256 * cm;
+                        x.d = sd + bl;
+                        x.s = ss + bl * 16;
+                        x.q_stride = chunk;
+                        x.d_stride = nbc;
+                        x.s_stride = chunk / 16;
+                        T::template dot<NT>(ring[u], grp, x, n_tok, acc);
+                        if (++cm == pr) {
+                            cm = 0;
+#pragma unroll
+                            for (int t = 0; t < NT; ++t) slot[t] = acc[t];
+                            slot += W * 64 * NT;
+                        }
+                    }
+                    load_next(ring[u]);
                 }
             }
         }
+        c0b += nbc;
+        if (c0b >= nb) break;
+        nbcur = min(nbc, nb - c0b);
+        pr = per_rg(nbcur);
+        total = pr * rgn;
+        if (total > 0) prefetch(c0b);
     }
     __syncthreads();
-    gemv_epilogue<NT>(a, row0, nrows,
-                      [&](int j, int t) {
-                          float acc = 0.0F;
-                          const float* p = part + j * nbc * NT + t;
-                          for (int b = 0; b < nbc; ++b) acc += p[b * NT];
-                          return acc;
-                      },
-                      lv);
+    auto sum = [&](int j, int t) {
+        const int r = j >> 4, i = j & 15;
+        float v = 0.0F;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) v += part[((r * W + w) * 64 + i + 16 * g) * NT + t];
+        }
+        return v;
+    };
+    if (a.mode == kAdd) {
+        // residual add with the prefetched values
+        const int n = nrows * n_tok;
+        for (int idx = threadIdx.x; idx < n; idx += kMmThreads) {
+            const int t = idx / nrows, j = idx - t * nrows;
+            float* out = a.y + static_cast<size_t>(t) * a.y_stride + row0 + j;
+            *out = (idx == static_cast<int>(threadIdx.x) ? y_pre : *out) + sum(j, t);
+        }
+        return;
+    }
+    gemv_epilogue<kMmThreads>(a, row0, nrows, sum, lv);
 }
 
 // Float weights (F32/F16, small models): one wave per row, lanes over K,
 // float activations (RMS-normalized in the prologue when a gain is given).
+constexpr int kFloatThreads = 256;
+constexpr int kGemvFloatRows = 2 * kGluGroup;
+
 template <int NT>
-__global__ __launch_bounds__(kThreads) void k_gemv_f(GemvArgs a, int32_t rows_per_wg) {
-    __shared__ float rs[NT], red[NT * (kThreads / kWave)];
-    __shared__ float sums[kThreads / kWave * 2][NT];
+__global__ __launch_bounds__(kFloatThreads) void k_gemv_f(GemvArgs a, int32_t rows_per_wg) {
+    constexpr int W = kFloatThreads / kWave;
+    __shared__ float rs[NT], red[NT * W];
+    __shared__ float sums[kGemvFloatRows][NT];
     extern __shared__ float lv_f[];
     const int K = static_cast<int>(a.mat.cols);
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int n_tok = a.n_tok < NT ? a.n_tok : NT;
-    if (a.x.gain) row_rms<NT>(a.x, n_tok, K, rs, red);
+    if (a.x.gain) row_rms<NT, kFloatThreads>(a.x, n_tok, K, rs, red);
     const int RW = rows_per_wg, row0 = blockIdx.x * RW;
     const int nrows = min(RW, static_cast<int>(a.mat.rows) - row0);
-    for (int j = wave; j < RW; j += kThreads / kWave) {
+    for (int j = wave; j < RW; j += W) {
         float acc[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[t] = 0.0F;
@@ -735,7 +929,21 @@ __global__ __launch_bounds__(kThreads) void k_gemv_f(GemvArgs a, int32_t rows_pe
     __syncthreads();
     GemvArgs b = a;
     b.n_tok = n_tok;
-    gemv_epilogue<NT>(b, row0, nrows, [&](int j, int t) { return sums[j][t]; }, lv_f);
+    gemv_epilogue<kFloatThreads>(b, row0, nrows, [&](int j, int t) { return sums[j][t]; }, lv_f);
+}
+
+// ------------------------------------------------------------------ activation quantization kernel
+// One wave per 256-value block: rows [0, n_rows) of x (stride floats apart)
+// into the staging layout of `out`.
+__global__ __launch_bounds__(256) void k_quantize(const float* x, int32_t stride, Act8 out) {
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int b = blockIdx.x * 4 + wave, row = blockIdx.y;
+    if (b * 256 >= out.K) return;
+    const float4 v4 = *reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * stride + b * 256 + 4 * lane);
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    quant_block_wave(v, lane, out.q + static_cast<size_t>(row) * out.K + b * 256,
+                     out.d + static_cast<size_t>(row) * (out.K / 256) + b,
+                     out.s + static_cast<size_t>(row) * (out.K / 16) + b * 16);
 }
 
 // ------------------------------------------------------------------ attention
@@ -746,33 +954,48 @@ __global__ __launch_bounds__(kThreads) void k_gemv_f(GemvArgs a, int32_t rows_pe
 // quad of lanes holds one key (a quarter of its dims each) and the score is
 // quad-reduced; for P.V the lanes own two head dims each. K and V of a tile
 // are loaded together. The four waves' online-softmax states are merged in
-// LDS; with several splits the last work-group to finish (atomic counter,
-// reset by it) merges the splits' partials.
+// LDS and written as the split's (max, sum, output) partial;
+// k_attention_merge combines the splits.
+constexpr int kAttnThreads = 256;
 constexpr int kAttnQPW = 8;
 constexpr int kAttnTile = 16;
-constexpr int kAttnWgKeys = kAttnTile * (kThreads / kWave);
+constexpr int kAttnWgKeys = kAttnTile * (kAttnThreads / kWave);
+constexpr int kAttnMaxSplits = 32;
 
+__device__ __forceinline__ int attn_split_len(int n_keys, int splits_max) {
+    int L = (n_keys + splits_max - 1) / splits_max;
+    return (L + kAttnWgKeys - 1) / kAttnWgKeys * kAttnWgKeys;
+}
+
+// K quarter of the lane's key (HD > 0) and the lane's V pair of all 16 keys of the tile at t0.
 template <int HD>
-__device__ __forceinline__ void attn_load_k(const uint16_t* krow, int hd, int qq, uint4* kr) {
+__device__ __forceinline__ void attn_load_tile(global_ptr<const uint16_t> kc, global_ptr<const uint16_t> vc, int t0,
+                                               int capacity, int hd, int kk, int qq, int lane, uint4* kr,
+                                               uint32_t* vv) {
     if constexpr (HD > 0) {
+        global_ptr<const uint16_t> krow = kc + static_cast<size_t>(min(t0 + kk, capacity - 1)) * HD;
 #pragma unroll
-        for (int c = 0; c < HD / 32; ++c) kr[c] = *reinterpret_cast<const uint4*>(krow + qq * (HD / 4) + 8 * c);
+        for (int c = 0; c < HD / 32; ++c) kr[c] = load_u4(krow + qq * (HD / 4) + 8 * c);
+    }
+#pragma unroll
+    for (int u = 0; u < kAttnTile; ++u) {
+        const int kj = min(t0 + u, capacity - 1);
+        vv[u] = 2 * lane < hd ? *(global_ptr<const uint32_t>) (vc + static_cast<size_t>(kj) * hd + 2 * lane) : 0u;
     }
 }
 
 template <int HD>
-__global__ __launch_bounds__(kThreads) void k_attention(const float* __restrict__ q, const StepDev* __restrict__ step,
-                                                        int32_t layer, int32_t n_head, int32_t n_head_kv,
-                                                        int32_t hd_arg, int32_t splits_max, int32_t qgroups,
-                                                        float* __restrict__ partial, int32_t* __restrict__ counters,
-                                                        float* __restrict__ out) {
-    constexpr int QPW = kAttnQPW, W = kThreads / kWave;
+__global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restrict__ q,
+                                                            const StepDev* __restrict__ step, int32_t layer,
+                                                            int32_t n_head, int32_t n_head_kv, int32_t hd_arg,
+                                                            int32_t splits_max, int32_t qgroups,
+                                                            float* __restrict__ partial) {
+    constexpr int QPW = kAttnQPW, W = kAttnThreads / kWave;
     constexpr int QS = (HD > 0 ? HD : 128) + 16;  // LDS row stride of a query (quarters padded by 4)
     __shared__ __align__(16) float Qs[QPW][QS];
     __shared__ __align__(16) float P[W][QPW][kAttnTile];
     __shared__ float Ms[W][QPW], Ls[W][QPW];
     __shared__ __align__(16) float Os[W][QPW][128];
-    __shared__ int last;
     const int hd = HD > 0 ? HD : hd_arg;
     const int DQ = hd / 4;
     const int seq = blockIdx.z;
@@ -785,8 +1008,7 @@ __global__ __launch_bounds__(kThreads) void k_attention(const float* __restrict_
     if (q_begin >= NQ) return;
     const int nq = min(QPW, NQ - q_begin);
     const int n_keys = pos0 + len;
-    int L = (n_keys + splits_max - 1) / splits_max;
-    L = (L + kAttnWgKeys - 1) / kAttnWgKeys * kAttnWgKeys;
+    const int L = attn_split_len(n_keys, splits_max);
     const int n_splits = (n_keys + L - 1) / L;
     const int split = blockIdx.x;
     if (split >= n_splits) return;
@@ -795,15 +1017,34 @@ __global__ __launch_bounds__(kThreads) void k_attention(const float* __restrict_
     const int kk = lane >> 2, qq = lane & 3;
     const float scale = 1.0F / sqrtf(static_cast<float>(hd));
     const size_t head_base = (static_cast<size_t>(layer) * n_head_kv + kvh) * capacity;
-    const uint16_t* kc = step->seqs[seq].k + head_base * hd;
-    const uint16_t* vc = step->seqs[seq].v + head_base * hd;
+    global_ptr<const uint16_t> kc = as_global(static_cast<const uint16_t*>(step->seqs[seq].k)) + head_base * hd;
+    global_ptr<const uint16_t> vc = as_global(static_cast<const uint16_t*>(step->seqs[seq].v)) + head_base * hd;
 
+    // K and V of the wave's first tile are requested before the queries are
+    // staged; every load index is clamped so that the loads are issued
+    // unconditionally and overlap
+    int t0 = k0 + wave * kAttnTile;
+    uint4 kr[HD > 0 ? HD / 32 : 1];
+    uint32_t vv[kAttnTile];
+    attn_load_tile<HD>(kc, vc, min(t0, k1 - 1), capacity, hd, kk, qq, lane, kr, vv);
     // queries -> LDS, quarter c of row i at Qs[i][c * (DQ + 4)]
-    for (int e = threadIdx.x; e < QPW * hd; e += kThreads) {
+    constexpr int QE = (QPW * (HD > 0 ? HD : 128) + kAttnThreads - 1) / kAttnThreads;
+    float qv[QE];
+#pragma unroll
+    for (int u = 0; u < QE; ++u) {
+        const int e = min(static_cast<int>(threadIdx.x) + u * kAttnThreads, QPW * hd - 1);
         const int i = e / hd, d = e - i * hd;
         const int qi = q_begin + min(i, nq - 1);
         const int t = qi / G, head = kvh * G + qi % G;
-        Qs[i][(d / DQ) * (DQ + 4) + d % DQ] = q[static_cast<size_t>(row0 + t) * H + head * hd + d];
+        qv[u] = q[static_cast<size_t>(row0 + t) * H + head * hd + d];
+    }
+#pragma unroll
+    for (int u = 0; u < QE; ++u) {
+        const int e = threadIdx.x + u * kAttnThreads;
+        if (e < QPW * hd) {
+            const int i = e / hd, d = e - i * hd;
+            Qs[i][(d / DQ) * (DQ + 4) + d % DQ] = qv[u];
+        }
     }
     int limit[QPW];
 #pragma unroll
@@ -818,18 +1059,14 @@ __global__ __launch_bounds__(kThreads) void k_attention(const float* __restrict_
         o0[i] = 0.0F;
         o1[i] = 0.0F;
     }
-    for (int t0 = k0 + wave * kAttnTile; t0 < k1; t0 += W * kAttnTile) {
+    for (; t0 < k1; t0 += W * kAttnTile) {
         const int key = t0 + kk;
         const int keyc = min(key, capacity - 1);
-        // K quarter of this lane's key and V pairs of the tile's 16 keys, loaded together
-        uint4 kr[HD > 0 ? HD / 32 : 1];
-        attn_load_k<HD>(kc + static_cast<size_t>(keyc) * hd, hd, qq, kr);
-        uint32_t vv[kAttnTile];
-#pragma unroll
-        for (int u = 0; u < kAttnTile; ++u) {
-            const int kj = min(t0 + u, capacity - 1);
-            vv[u] = 2 * lane < hd ? *reinterpret_cast<const uint32_t*>(vc + static_cast<size_t>(kj) * hd + 2 * lane) : 0u;
-        }
+        // next tile's K and V are requested before this tile is consumed
+        const int tn = t0 + W * kAttnTile;
+        uint4 krn[HD > 0 ? HD / 32 : 1];
+        uint32_t vvn[kAttnTile];
+        attn_load_tile<HD>(kc, vc, min(tn, k1 - 1), capacity, hd, kk, qq, lane, krn, vvn);
         float sc[QPW];
 #pragma unroll
         for (int i = 0; i < QPW; ++i) sc[i] = 0.0F;
@@ -847,7 +1084,7 @@ __global__ __launch_bounds__(kThreads) void k_attention(const float* __restrict_
                 }
             }
         } else {
-            const uint16_t* kq = kc + static_cast<size_t>(keyc) * hd + qq * DQ;
+            global_ptr<const uint16_t> kq = kc + static_cast<size_t>(keyc) * hd + qq * DQ;
             for (int d = 0; d < DQ; ++d) {
                 const float kf = h2f(kq[d]);
 #pragma unroll
@@ -892,6 +1129,10 @@ __global__ __launch_bounds__(kThreads) void k_attention(const float* __restrict_
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int c = 0; c < (HD > 0 ? HD / 32 : 1); ++c) kr[c] = krn[c];
+#pragma unroll
+        for (int u = 0; u < kAttnTile; ++u) vv[u] = vvn[u];
     }
     // merge the four waves
 #pragma unroll
@@ -908,7 +1149,7 @@ __global__ __launch_bounds__(kThreads) void k_attention(const float* __restrict_
     }
     __syncthreads();
     const int half_hd = hd / 2;
-    for (int e = threadIdx.x; e < nq * half_hd; e += kThreads) {
+    for (int e = threadIdx.x; e < nq * half_hd; e += kAttnThreads) {
         const int i = e / half_hd, dp = e - i * half_hd;
         float M = -INFINITY;
 #pragma unroll
@@ -925,49 +1166,70 @@ __global__ __launch_bounds__(kThreads) void k_attention(const float* __restrict_
         }
         const int qi = q_begin + i;
         const int t = qi / G, head = kvh * G + qi % G;
-        if (n_splits == 1) {
-            float* o = out + static_cast<size_t>(row0 + t) * H + head * hd;
-            o[2 * dp] = a0 / Lsum;
-            o[2 * dp + 1] = a1 / Lsum;
-        } else {
-            float* dst = partial + ((static_cast<size_t>(row0 + t) * n_head + head) * splits_max + split) * (hd + 2);
-            if (dp == 0) {
-                dst[0] = M;
-                dst[1] = Lsum;
-            }
-            dst[2 + 2 * dp] = a0;
-            dst[3 + 2 * dp] = a1;
+        float* dst = partial + ((static_cast<size_t>(row0 + t) * n_head + head) * splits_max + split) * (hd + 2);
+        if (dp == 0) {
+            dst[0] = M;
+            dst[1] = Lsum;
         }
+        dst[2 + 2 * dp] = a0;
+        dst[3 + 2 * dp] = a1;
     }
-    if (n_splits == 1) return;
-    __threadfence();
-    __syncthreads();
-    int32_t* counter = counters + (static_cast<size_t>(seq) * n_head_kv + kvh) * qgroups + qg;
-    if (threadIdx.x == 0) last = atomicAdd(counter, 1) == n_splits - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    for (int e = threadIdx.x; e < nq * half_hd; e += kThreads) {
-        const int i = e / half_hd, dp = e - i * half_hd;
-        const int qi = q_begin + i;
-        const int t = qi / G, head = kvh * G + qi % G;
-        const float* base = partial + (static_cast<size_t>(row0 + t) * n_head + head) * splits_max * (hd + 2);
+}
+
+// Combines the split partials of every (row, head): one work-group per
+// (row, 256 output values); with xq set the 256 values are quantized into xq.
+__global__ __launch_bounds__(256) void k_attention_merge(const float* __restrict__ partial,
+                                                         const StepDev* __restrict__ step, int32_t n_head,
+                                                         int32_t hd, int32_t splits_max, float* __restrict__ out,
+                                                         Act8 xq) {
+    __shared__ float vals[256];
+    const int row = blockIdx.y, H = n_head * hd;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    const SeqDev& sd = step->seqs[step->seq[row]];
+    const int n_keys = sd.pos0 + sd.len;
+    const int L = attn_split_len(n_keys, splits_max);
+    const int n_splits = (n_keys + L - 1) / L;
+    float v = 0.0F;
+    if (c < H) {
+        const int head = c / hd, dcol = c - head * hd;
+        const float* base = partial + (static_cast<size_t>(row) * n_head + head) * splits_max * (hd + 2);
+        // every split's (max, sum, value) requested at once
+        float pm[kAttnMaxSplits], pl[kAttnMaxSplits], po[kAttnMaxSplits];
+#pragma unroll
+        for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
+            const float* p = base + min(sp, n_splits - 1) * (hd + 2);
+            pm[sp] = p[0];
+            pl[sp] = p[1];
+            po[sp] = p[2 + dcol];
+        }
+#pragma unroll
+        for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
+            if (sp >= n_splits) pm[sp] = -INFINITY;
+        }
         float M = -INFINITY;
-        for (int sp = 0; sp < n_splits; ++sp) M = fmaxf(M, base[sp * (hd + 2)]);
-        float Lsum = 0.0F, a0 = 0.0F, a1 = 0.0F;
-        for (int sp = 0; sp < n_splits; ++sp) {
-            const float* src = base + sp * (hd + 2);
-            const float ms = src[0];
-            const float f = ms == -INFINITY ? 0.0F : expf(ms - M);
-            Lsum += f * src[1];
-            a0 += f * src[2 + 2 * dp];
-            a1 += f * src[3 + 2 * dp];
+#pragma unroll
+        for (int sp = 0; sp < kAttnMaxSplits; ++sp) M = fmaxf(M, pm[sp]);
+        float total = 0.0F, acc = 0.0F;
+#pragma unroll
+        for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
+            const float f = pm[sp] == -INFINITY ? 0.0F : expf(pm[sp] - M);
+            total += f * pl[sp];
+            acc += f * po[sp];
         }
-        float* o = out + static_cast<size_t>(row0 + t) * H + head * hd;
-        o[2 * dp] = a0 / Lsum;
-        o[2 * dp + 1] = a1 / Lsum;
+        v = acc / total;
+        out[static_cast<size_t>(row) * H + c] = v;
     }
-    if (threadIdx.x == 0) *counter = 0;
+    if (xq.q == nullptr) return;
+    vals[threadIdx.x] = v;
+    __syncthreads();
+    if (threadIdx.x < kWave) {
+        const int lane = threadIdx.x;
+        const float4 v4 = *reinterpret_cast<const float4*>(&vals[4 * lane]);
+        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+        quant_block_wave(vv, lane, xq.q + static_cast<size_t>(row) * xq.K + blockIdx.x * 256,
+                         xq.d + static_cast<size_t>(row) * (xq.K / 256) + blockIdx.x,
+                         xq.s + static_cast<size_t>(row) * (xq.K / 16) + blockIdx.x * 16);
+    }
 }
 
 // ------------------------------------------------------------------ argmax + acceptance
@@ -999,59 +1261,60 @@ void check(hipError_t e, const char* what) {
     if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
 
-// Host-side geometry: the activation chunk fits kGemvActBytes of LDS, the
-// per-block partial sums kGemvPartBytes, and the row count per work-group
-// aims at kGemvTargetWgs work-groups.
-constexpr int kGemvActBytes = 28672;
-constexpr int kGemvPartBytes = 16384;
-constexpr int kGemvTargetWgs = 512;
-constexpr int kGemvFloatRows = 2 * kGluGroup;
+// Host-side geometry. The K chunk staged per pass is fixed (kMmChunk values)
+// whatever the token count, so every row's partial sums are added in the
+// same order for 1 and for 8 tokens: a draft-verify step reproduces serial
+// decode bit for bit. The per-wave row partials take at most kMmPartBytes of
+// LDS, and the row groups per work-group aim at kMmTargetWgs work-groups.
+#ifndef JFH_MM_CHUNK
+#define JFH_MM_CHUNK 8192
+#endif
+#ifndef JFH_MM_TARGET_WGS
+#define JFH_MM_TARGET_WGS 512
+#endif
+constexpr int kMmChunk = JFH_MM_CHUNK;
+constexpr int kMmPartBytes = 65536;
+constexpr int kMmTargetWgs = JFH_MM_TARGET_WGS;
 
-GemvGeom gemv_geom(const GemvArgs& a, int nt, size_t& lds) {
+MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds) {
     const int K = static_cast<int>(a.mat.cols);
-    const double per_value = nt * (1.0 + 4.0 / 256.0 + 2.0 / 16.0);
-    int chunk = static_cast<int>(kGemvActBytes / per_value) / 256 * 256;
-    if (chunk < 256) chunk = 256;
-    const int k_round = (K + 255) / 256 * 256;
-    if (chunk > k_round) chunk = k_round;
-    const int nbc = chunk / 256;
-    const int rows = static_cast<int>(a.mat.rows);
-    int rw = (rows + kGemvTargetWgs - 1) / kGemvTargetWgs;
-    const int cap = kGemvPartBytes / (nbc * nt * 4);
-    if (rw > cap) rw = cap;
-    if (rw < 1) rw = 1;
-    const int align = a.mode == kSwiGLU ? 2 * kGluGroup : a.mode == kQKV ? 2 : 1;
-    rw = (rw + align - 1) / align * align;
-    GemvGeom g;
-    g.rows_per_wg = rw;
+    // a normalized input is staged whole: its block scales need the full row's rms
+    const int chunk = (K < kMmChunk || (a.xq.q == nullptr && a.x.gain != nullptr)) ? K : kMmChunk;
+    const int n_rg = (static_cast<int>(a.mat.rows) + 15) / 16;
+    int rgw = (n_rg + kMmTargetWgs - 1) / kMmTargetWgs;
+    const int cap = kMmPartBytes / (kMmWaves * 64 * nt * 4);
+    if (rgw > cap) rgw = cap;
+    if (rgw < 1) rgw = 1;
+    MmGeom g;
+    g.rgw = rgw;
     g.chunk = chunk;
-    g.nbc_magic = ((1ull << 32) + static_cast<uint64_t>(nbc) - 1) / static_cast<uint64_t>(nbc);
-    lds = static_cast<size_t>(nt) * chunk + static_cast<size_t>(nt) * nbc * 4 + static_cast<size_t>(nt) * chunk / 8 +
-          static_cast<size_t>(rw) * nbc * nt * 4 + static_cast<size_t>(nt + nt * (kThreads / kWave) + rw * nt) * 4;
+    const size_t nbc = static_cast<size_t>(chunk) / 256;
+    lds = static_cast<size_t>(nt) * chunk + nt * nbc * 4 + static_cast<size_t>(nt) * chunk / 8 +
+          static_cast<size_t>(rgw) * kMmWaves * 64 * nt * 4 + static_cast<size_t>(nt) * 4 + nt * nbc * 4 +
+          static_cast<size_t>(rgw) * 16 * nt * 4 + static_cast<size_t>(nt) * 4;
+    if (lds > 160 * 1024) throw std::invalid_argument("matmul staging does not fit the LDS");
     return g;
 }
 
 template <uint32_t TYPE, int NT>
-void gemv_q(const GemvArgs& a, hipStream_t stream) {
+void mm(const GemvArgs& a, hipStream_t stream) {
     size_t lds = 0;
-    const GemvGeom g = gemv_geom(a, NT, lds);
-    const int grid = (static_cast<int>(a.mat.rows) + g.rows_per_wg - 1) / g.rows_per_wg;
-    hipLaunchKernelGGL((k_gemv_q<TYPE, NT>), dim3(grid), dim3(kThreads), lds, stream, a, g);
-    check(hipGetLastError(), "gemv launch");
+    const MmGeom g = mm_geom(a, NT, lds);
+    const int n_rg = (static_cast<int>(a.mat.rows) + 15) / 16;
+    const int grid = (n_rg + g.rgw - 1) / g.rgw;
+    hipLaunchKernelGGL((k_mm<TYPE, NT>), dim3(grid), dim3(kMmThreads), lds, stream, a, g);
+    check(hipGetLastError(), "matmul launch");
 }
 
 template <uint32_t TYPE>
-void gemv_q_nt(const GemvArgs& a, hipStream_t stream) {
+void mm_nt(const GemvArgs& a, hipStream_t stream) {
     switch (a.n_tok) {
-    case 1: gemv_q<TYPE, 1>(a, stream); break;
-    case 2: gemv_q<TYPE, 2>(a, stream); break;
-    case 3: gemv_q<TYPE, 3>(a, stream); break;
-    case 4: gemv_q<TYPE, 4>(a, stream); break;
-    case 5: gemv_q<TYPE, 5>(a, stream); break;
-    case 6: gemv_q<TYPE, 6>(a, stream); break;
-    case 7: gemv_q<TYPE, 7>(a, stream); break;
-    case 8: gemv_q<TYPE, 8>(a, stream); break;
-    default: throw std::invalid_argument("gemv token group must be 1..8");
+    case 1: mm<TYPE, 1>(a, stream); break;
+    case 2: mm<TYPE, 2>(a, stream); break;
+    case 3: case 4: mm<TYPE, 4>(a, stream); break;
+    case 5: case 6: mm<TYPE, 6>(a, stream); break;
+    case 7: case 8: mm<TYPE, 8>(a, stream); break;
+    default: throw std::invalid_argument("matmul token group must be 1..8");
     }
 }
 
@@ -1059,17 +1322,25 @@ template <int NT>
 void gemv_f(const GemvArgs& a, hipStream_t stream) {
     const int grid = (static_cast<int>(a.mat.rows) + kGemvFloatRows - 1) / kGemvFloatRows;
     const size_t lds = static_cast<size_t>(kGemvFloatRows) * NT * sizeof(float);
-    hipLaunchKernelGGL((k_gemv_f<NT>), dim3(grid), dim3(kThreads), lds, stream, a, kGemvFloatRows);
+    hipLaunchKernelGGL((k_gemv_f<NT>), dim3(grid), dim3(kFloatThreads), lds, stream, a, kGemvFloatRows);
     check(hipGetLastError(), "gemv launch");
 }
 
 }  // namespace
 
+float dequant_tile_value(uint32_t type, const uint8_t* tile, uint32_t row, uint32_t k) {
+    return tile_value(type, tile, row, k);
+}
+
 void launch_gemv(const GemvArgs& a_in, hipStream_t stream) {
     const uint32_t type = a_in.mat.type;
-    const bool quantized = type == 7 || type == 9 || type == 11 || type == 13;
-    if (quantized && (a_in.mat.cols % kActBlock != 0 || a_in.x.stride % 4 != 0)) {
+    const bool quantized = tile_bytes(type) != 0;
+    if (quantized && (a_in.mat.cols % kActBlock != 0 || (a_in.xq.q == nullptr && a_in.x.stride % 4 != 0))) {
         throw std::invalid_argument("quantized matmul needs rows of a multiple of 256 values");
+    }
+    if (!quantized && a_in.xq.q != nullptr) throw std::invalid_argument("float matmuls take float activations");
+    if (a_in.xq.q != nullptr && (a_in.xq.K != static_cast<int32_t>(a_in.mat.cols) || a_in.x.gain != nullptr)) {
+        throw std::invalid_argument("pre-quantized activations must match the matrix and carry no norm");
     }
     if ((a_in.mode == kSwiGLU && a_in.mat.rows % (2 * kGluGroup) != 0) || (a_in.mode == kQKV && a_in.mat.rows % 2 != 0)) {
         throw std::invalid_argument("matmul rows do not fit the fused row layout");
@@ -1078,8 +1349,15 @@ void launch_gemv(const GemvArgs& a_in, hipStream_t stream) {
     for (int t0 = 0; t0 < a_in.n_tok; t0 += 8) {
         GemvArgs a = a_in;
         a.n_tok = a_in.n_tok - t0 < 8 ? a_in.n_tok - t0 : 8;
-        if (a.x.gather) a.x.gather += t0;
-        else a.x.x += static_cast<size_t>(t0) * a.x.stride;
+        if (a.xq.q) {
+            a.xq.q += static_cast<size_t>(t0) * a.xq.K;
+            a.xq.d += static_cast<size_t>(t0) * (a.xq.K / 256);
+            a.xq.s += static_cast<size_t>(t0) * (a.xq.K / 16);
+        } else if (a.x.gather) {
+            a.x.gather += t0;
+        } else {
+            a.x.x += static_cast<size_t>(t0) * a.x.stride;
+        }
         if (a.y) a.y += static_cast<size_t>(t0) * a.y_stride;
         if (a.best) a.best += t0;
         if (a.mode == kQKV) {
@@ -1096,25 +1374,32 @@ void launch_gemv(const GemvArgs& a_in, hipStream_t stream) {
             continue;
         }
         switch (type) {
-        case 11: gemv_q_nt<11>(a, stream); break;
-        case 13: gemv_q_nt<13>(a, stream); break;
-        case 9: gemv_q_nt<9>(a, stream); break;
-        case 7: gemv_q_nt<7>(a, stream); break;
+        case 11: mm_nt<11>(a, stream); break;
+        case 13: mm_nt<13>(a, stream); break;
+        case 9: mm_nt<9>(a, stream); break;
+        case 7: mm_nt<7>(a, stream); break;
         default: throw std::invalid_argument("unsupported weight type for gemv");
         }
     }
 }
 
+void launch_quantize(const float* x, int32_t stride, int32_t n_rows, const Act8& out, hipStream_t stream) {
+    if (out.K % 256 != 0 || stride % 4 != 0) throw std::invalid_argument("quantized rows need multiples of 256 values");
+    dim3 grid((out.K / 256 + 3) / 4, n_rows);
+    hipLaunchKernelGGL(k_quantize, grid, dim3(256), 0, stream, x, stride, out);
+    check(hipGetLastError(), "quantize launch");
+}
+
 void launch_embed(const DMat& table, const StepDev* step, float* h, int32_t n_rows, int32_t H,
                   unsigned long long* best, int32_t n_best, hipStream_t stream) {
-    dim3 grid((H + kThreads - 1) / kThreads, n_rows);
-    hipLaunchKernelGGL(k_embed, grid, dim3(kThreads), 0, stream, table, step, h, H, best, n_best);
+    dim3 grid((H + 255) / 256, n_rows);
+    hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, stream, table, step, h, H, best, n_best);
     check(hipGetLastError(), "embed launch");
 }
 
 int32_t attention_splits(int32_t capacity) {
     const int32_t s = (capacity + kAttnWgKeys - 1) / kAttnWgKeys;
-    return s < 1 ? 1 : (s > 32 ? 32 : s);
+    return s < 1 ? 1 : (s > kAttnMaxSplits ? kAttnMaxSplits : s);
 }
 
 size_t attention_partial_floats(int32_t rows, int32_t n_head, int32_t head_dim, int32_t splits) {
@@ -1123,25 +1408,34 @@ size_t attention_partial_floats(int32_t rows, int32_t n_head, int32_t head_dim, 
 
 void launch_attention(const float* q, const StepDev* step, int32_t max_len, int32_t n_seq, int32_t layer,
                       int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t splits, float* partial,
-                      int32_t* counters, float* out, hipStream_t stream) {
+                      hipStream_t stream) {
     const int G = n_head / n_head_kv;
     const int qgroups = (G * max_len + kAttnQPW - 1) / kAttnQPW;
     if (head_dim > 2 * kWave || head_dim % 4 != 0) {
         throw std::invalid_argument("attention supports head dims that are multiples of 4 up to 128");
     }
     if (qgroups > kMaxAttnQGroups) throw std::invalid_argument("attention step has too many query rows per kv head");
-    dim3 grid(splits, n_head_kv * qgroups, n_seq), block(kThreads);
+    dim3 grid(splits, n_head_kv * qgroups, n_seq), block(kAttnThreads);
     if (head_dim == 128) {
         hipLaunchKernelGGL(k_attention<128>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
-                           qgroups, partial, counters, out);
+                           qgroups, partial);
     } else if (head_dim == 64) {
         hipLaunchKernelGGL(k_attention<64>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
-                           qgroups, partial, counters, out);
+                           qgroups, partial);
     } else {
         hipLaunchKernelGGL(k_attention<0>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
-                           qgroups, partial, counters, out);
+                           qgroups, partial);
     }
     check(hipGetLastError(), "attention launch");
+}
+
+void launch_attention_merge(const float* partial, const StepDev* step, int32_t n_rows, int32_t n_head,
+                            int32_t head_dim, int32_t splits, float* out, const Act8& xq, hipStream_t stream) {
+    const int H = n_head * head_dim;
+    if (xq.q != nullptr && (H % 256 != 0 || xq.K != H)) throw std::invalid_argument("merge quantization shape mismatch");
+    dim3 grid((H + 255) / 256, n_rows);
+    hipLaunchKernelGGL(k_attention_merge, grid, dim3(256), 0, stream, partial, step, n_head, head_dim, splits, out, xq);
+    check(hipGetLastError(), "attention merge launch");
 }
 
 void launch_finish(const unsigned long long* best, const StepDev* step, int32_t n_out, StepOut* out,
@@ -1151,8 +1445,8 @@ void launch_finish(const unsigned long long* best, const StepDev* step, int32_t 
 }
 
 void launch_dequant_rows(const DMat& m, int32_t row0, int32_t n_rows, float* out, hipStream_t stream) {
-    dim3 grid((m.cols + kThreads - 1) / kThreads, n_rows);
-    hipLaunchKernelGGL(k_dequant_rows, grid, dim3(kThreads), 0, stream, m, row0, out);
+    dim3 grid((m.cols + 255) / 256, n_rows);
+    hipLaunchKernelGGL(k_dequant_rows, grid, dim3(256), 0, stream, m, row0, out);
     check(hipGetLastError(), "dequant launch");
 }
 

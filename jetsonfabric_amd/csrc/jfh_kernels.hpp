@@ -4,30 +4,55 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <cstddef>
 #include <cstdint>
 
 namespace jfh::gpu {
 
-constexpr int kMaxRows = 64;   // token rows of one step (sum over sequences)
-constexpr int kMaxSeq = 16;    // sequences of one batched step
-constexpr int kActBlock = 256; // activation quantization block (values)
+constexpr int kMaxRows = 64;        // token rows of one step (sum over sequences)
+constexpr int kMaxSeq = 16;         // sequences of one batched step
+constexpr int kActBlock = 256;      // activation quantization block (values)
+constexpr int kTileRows = 16;       // rows of one weight tile
 constexpr int kMaxAttnQGroups = 8;  // query groups of 8 rows per kv head in one step
 
-// A weight matrix in device memory. Quantized types are stored as a 16-byte
-// aligned main plane [rows][blocks][main_block_bytes] plus an aux plane
-// [rows][blocks][aux_block_bytes] holding the f16 scales that do not fit the
-// alignment: Q4_K main 144 / aux 0 (GGML bytes verbatim), Q6_K main 208
-// (ql|qh|scales) / aux 2 (d), Q8_0 main 32 (qs) / aux 2 (d), Q2_K main 80
-// (scales|qs) / aux 4 (d, dmin). F32/F16 are verbatim with no aux plane.
+// Bytes of one weight tile (16 rows x 256 values) of a quantized type, 0 for
+// float types. The tile holds the 16 rows' GGML blocks rearranged so that
+// lane l of a wave (row i = l % 16, group g = l / 16) owns row i's values
+// 64 g .. 64 g + 63 and reads their codes with 16-byte loads that cover
+// 1 KiB of contiguous memory per wave (chunk c of lane l at
+// codes + (64 c + l) * 16):
+//   Q4_K 2304: 16 headers (d, dmin, then per lane group g a 24-bit field
+//              sc 2g | sc 2g+1 | m 2g | m 2g+1 at bit 24 g) | 2 chunks: GGML qs
+//              bytes 32 g .. 32 g + 31 (low nibbles values 0..31, high 32..63)
+//   Q6_K 3360: 16 d | 16 x 16 int8 scales | 3 chunks: 8 low-nibble dwords
+//              (dword k: values 8k..8k+3 low, 8k+4..8k+7 high nibbles) and 4
+//              high-bit dwords (dword m, byte e, bits 2r: value 16m + 4r + e)
+//   Q8_0 4352: 16 x 8 d | 4 chunks: the int8 codes of GGML blocks 2g, 2g+1
+//   Q2_K 1344: 16 (d, dmin) | 16 x 16 scale bytes | 1 chunk: dword m, byte e,
+//              bits 2r: value 16m + 4r + e
+constexpr uint32_t tile_bytes(uint32_t type) {
+    return type == 11 ? 2304u : type == 13 ? 3360u : type == 7 ? 4352u : type == 9 ? 1344u : 0u;
+}
+
+// A weight matrix in device memory. Quantized types: tiles
+// [ceil(rows/16)][cols/256][tile_bytes] (rows past `rows` are zero). F32/F16:
+// rows verbatim, `row_bytes` apart.
 struct DMat {
-    const uint8_t* main = nullptr;
-    const uint8_t* aux = nullptr;
+    const uint8_t* data = nullptr;
     const float* bias = nullptr;  // optional f32 [rows]
     uint32_t type = 0;
     uint32_t rows = 0;
     uint32_t cols = 0;
-    uint32_t main_row_bytes = 0;
-    uint32_t aux_row_bytes = 0;
+    uint32_t row_bytes = 0;  // float types only
+};
+
+// int8 activation rows: per row, q holds the K codes, d one scale per 256
+// values and s the sum of every 16 codes.
+struct Act8 {
+    int8_t* q = nullptr;
+    float* d = nullptr;
+    int16_t* s = nullptr;
+    int32_t K = 0;  // values per row (multiple of 256)
 };
 
 // Per-sequence cache description for a step.
@@ -68,7 +93,7 @@ enum GemvMode : int32_t {
     kQKV = 4,     // fused q|k|v rows: bias, NEOX RoPE of q and k, q to qkv.q, k and v to the f16 cache
 };
 
-// Gate/up rows are interleaved in groups of this many rows per matrix.
+// Gate/up rows are interleaved in groups of this many rows per matrix (half a tile).
 constexpr int kGluGroup = 8;
 
 // Float activation rows feeding a matmul. With `gain` set the rows are
@@ -84,7 +109,7 @@ struct XIn {
 
 // kQKV epilogue: q/k rows of every head are stored pair-interleaved
 // (physical row 2i = head row i, 2i + 1 = head row i + head_dim/2) so one
-// work-group holds both halves of every rotated pair.
+// tile holds both halves of every rotated pair.
 struct QkvOut {
     const StepDev* step = nullptr;
     const float* rope = nullptr;  // [position][head_dim/2] (cos, sin)
@@ -100,7 +125,8 @@ struct GemvArgs {
     DMat mat;
     int32_t mode = kStore;
     int32_t n_tok = 1;
-    XIn x;
+    XIn x;                            // float activations (quantized by the matmul), or
+    Act8 xq;                          // pre-quantized activations (used when xq.q is set)
     float* y = nullptr;               // output [tok][y_stride]
     int32_t y_stride = 0;
     unsigned long long* best = nullptr;  // kLogits: packed (value, -index) per token
@@ -113,19 +139,25 @@ void launch_embed(const DMat& table, const StepDev* step, float* h, int32_t n_ro
                   unsigned long long* best, int32_t n_best, hipStream_t stream);
 // Matmul of up to kMaxRows token rows (in groups of 8) against one matrix.
 void launch_gemv(const GemvArgs& a, hipStream_t stream);
+// Quantizes n_rows float rows of K values (K % 256 == 0) into `out`.
+void launch_quantize(const float* x, int32_t stride, int32_t n_rows, const Act8& out, hipStream_t stream);
 // Split-K causal GQA flash attention over the f16 caches of the step's
-// sequences, writing float rows out[row][n_head * head_dim]. `splits` is
-// fixed per capacity (attention_splits); `counters` holds
-// kMaxSeq * n_head_kv * kMaxAttnQGroups zero-initialized ints that the kernel
-// leaves zero.
+// sequences. Every (row, head, split) writes its (max, sum, unnormalized
+// output) to `partial`; launch_attention_merge combines the splits.
 void launch_attention(const float* q, const StepDev* step, int32_t max_len, int32_t n_seq, int32_t layer,
                       int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t splits, float* partial,
-                      int32_t* counters, float* out, hipStream_t stream);
+                      hipStream_t stream);
+// Merges the splits of every (row, head) into out[row][n_head * head_dim]
+// and, when xq.q is set, quantizes the rows into xq.
+void launch_attention_merge(const float* partial, const StepDev* step, int32_t n_rows, int32_t n_head,
+                            int32_t head_dim, int32_t splits, float* out, const Act8& xq, hipStream_t stream);
 int32_t attention_splits(int32_t capacity);
 // Floats of the attention split scratch for `rows` token rows.
 size_t attention_partial_floats(int32_t rows, int32_t n_head, int32_t head_dim, int32_t splits);
 void launch_finish(const unsigned long long* best, const StepDev* step, int32_t n_out, StepOut* out,
                    hipStream_t stream);
 void launch_dequant_rows(const DMat& m, int32_t row0, int32_t n_rows, float* out, hipStream_t stream);
+// Host evaluation of the device tile decoder: value k (< 256) of row (< 16) of one tile.
+float dequant_tile_value(uint32_t type, const uint8_t* tile, uint32_t row, uint32_t k);
 
 }  // namespace jfh::gpu

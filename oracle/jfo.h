@@ -70,6 +70,19 @@ int jfo_dequantize_row(int type, const void * src, float * dst, int64_t n);
  */
 void jfo_quantize_act(const float * x, int64_t n, int8_t * q, float * d, int16_t * s16);
 
+/*
+ * Quantization of an RMS-normalized row as the HIP engine stages it: the codes
+ * of x[i] * gain[i] per 256-value block (d' = amax/127, q = roundf(v / d')),
+ * each block scale multiplied by the row's 1 / sqrtf(mean(x^2) + eps), so
+ * that d[b] * q[i] approximates (x[i] * rms_scale) * gain[i].
+ */
+void jfo_quantize_act_normed(const float * x, const float * gain, int64_t n, float eps, int8_t * q, float * d,
+                             int16_t * s16);
+
+/* y[t * rows + r] = W[r] . (q, d, s16)[t]: jfo_matmul's JFO_MODE_Q8 on pre-quantized rows. */
+int jfo_matmul_q8(int type, const void * w, int64_t n, int64_t rows, const int8_t * q, const float * d,
+                  const int16_t * s16, int64_t tokens, float * y, int threads);
+
 /* Dot product of one weight row with a quantized activation (n % 256 == 0):
  * integer dot per sub-block scaled by the sub-block scale, one float combine
  * per 256-value block (K-quants) or per 32-value block (Q8_0). */

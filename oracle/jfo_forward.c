@@ -95,6 +95,42 @@ int jfo_matmul(int type, const void * w, int64_t n, int64_t rows,
     return 0;
 }
 
+int jfo_matmul_q8(int type, const void * w, int64_t n, int64_t rows, const int8_t * q, const float * d,
+                  const int16_t * s16, int64_t tokens, float * y, int threads) {
+    uint32_t be = 0, bb = 0;
+    if (!jfo_type_block(type, &be, &bb) || n % 256 != 0 || type == JFO_F32 || type == JFO_F16) return -1;
+    const size_t row_bytes = (size_t) (n / be) * bb;
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+#endif
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint8_t * row = (const uint8_t *) w + (size_t) r * row_bytes;
+        for (int64_t t = 0; t < tokens; ++t) {
+            y[t * rows + r] = (float) jfo_vec_dot_q8(type, row, q + t * n, d + t * n / 256, s16 + t * n / 16, n);
+        }
+    }
+    (void) threads;
+    return 0;
+}
+
+static float rms_scale(const float * x, int64_t n, float eps) {
+    double sum = 0.0;
+    for (int64_t i = 0; i < n; ++i) sum += (double) x[i] * (double) x[i];
+    const float mean = (float) (sum / (double) n);
+    return 1.0f / sqrtf(mean + eps);
+}
+
+void jfo_quantize_act_normed(const float * x, const float * gain, int64_t n, float eps, int8_t * q, float * d,
+                             int16_t * s16) {
+    float * v = calloc((size_t) n, sizeof(float));
+    if (!v) return;
+    for (int64_t i = 0; i < n; ++i) v[i] = x[i] * gain[i];
+    jfo_quantize_act(v, n, q, d, s16);
+    const float scale = rms_scale(x, n, eps);
+    for (int64_t b = 0; b < n / 256; ++b) d[b] = d[b] * scale;
+    free(v);
+}
+
 static void rms_norm(const float * x, const jfo_tensor * gain, int64_t n, float eps, float * out) {
     double sum = 0.0;
     for (int64_t i = 0; i < n; ++i) sum += (double) x[i] * (double) x[i];
@@ -121,8 +157,69 @@ static void add_bias(float * y, const jfo_tensor * b, int64_t tokens, int64_t n)
     free(tmp);
 }
 
-static int linear(const jfo_session * s, const jfo_tensor * w, const float * x, int64_t tokens, float * y) {
-    return jfo_matmul(w->type, w->data, w->ne0, w->ne1, x, tokens, y, s->mode, s->threads);
+/*
+ * Input rows of one or more matmuls. In JFO_MODE_Q8 they are quantized once,
+ * the way the HIP engine stages them: plain rows as jfo_quantize_act; rows
+ * behind an RMSNorm as jfo_quantize_act_normed (codes of x*gain, block
+ * scales times the row's 1/rms). Float weights and JFO_MODE_EXACT use the
+ * float rows ((x*rms_scale)*gain for normed inputs, as the reference graph).
+ */
+typedef struct act_rows {
+    const float * x;   /* float rows (normed when a gain was given) */
+    int8_t * q;
+    float * d;
+    int16_t * s16;
+    int64_t n, tokens;
+} act_rows;
+
+static void act_prepare(const jfo_session * s, act_rows * a, const float * x, const jfo_tensor * gain, int64_t n,
+                        int64_t tokens, float * xn) {
+    a->n = n;
+    a->tokens = tokens;
+    a->q = NULL;
+    a->d = NULL;
+    a->s16 = NULL;
+    if (gain) {
+        for (int64_t t = 0; t < tokens; ++t) rms_norm(x + t * n, gain, n, s->m->rms_eps, xn + t * n);
+        a->x = xn;
+    } else {
+        a->x = x;
+    }
+    if (s->mode != JFO_MODE_Q8 || n % 256 != 0) return;
+    a->q = malloc((size_t) (tokens * n));
+    a->d = malloc(sizeof(float) * (size_t) (tokens * n / 256));
+    a->s16 = malloc(sizeof(int16_t) * (size_t) (tokens * n / 16));
+    float * g = NULL;
+    if (gain) {
+        g = malloc(sizeof(float) * (size_t) n);
+        jfo_dequantize_row(gain->type, gain->data, g, n);
+    }
+    for (int64_t t = 0; t < tokens; ++t) {
+        if (gain) {
+            jfo_quantize_act_normed(x + t * n, g, n, s->m->rms_eps, a->q + t * n, a->d + t * n / 256,
+                                    a->s16 + t * n / 16);
+        } else {
+            jfo_quantize_act(x + t * n, n, a->q + t * n, a->d + t * n / 256, a->s16 + t * n / 16);
+        }
+    }
+    free(g);
+}
+
+static void act_release(act_rows * a) {
+    free(a->q);
+    free(a->d);
+    free(a->s16);
+    a->q = NULL;
+    a->d = NULL;
+    a->s16 = NULL;
+}
+
+static int linear(const jfo_session * s, const jfo_tensor * w, const act_rows * a, float * y) {
+    const int float_weights = w->type == JFO_F32 || w->type == JFO_F16;
+    if (a->q && !float_weights) {
+        return jfo_matmul_q8(w->type, w->data, w->ne0, w->ne1, a->q, a->d, a->s16, a->tokens, y, s->threads);
+    }
+    return jfo_matmul(w->type, w->data, w->ne0, w->ne1, a->x, a->tokens, y, JFO_MODE_EXACT, s->threads);
 }
 
 static void rope_rows(const jfo_session * s, float * x, int64_t tokens, int32_t heads, int32_t pos0) {
@@ -265,13 +362,15 @@ int32_t jfo_session_forward(jfo_session * s, const int32_t * tokens, int32_t n,
     }
     for (int32_t l = 0; l < m->n_layer; ++l) {
         const jfo_layer * L = &m->layers[l];
-        for (int32_t t = 0; t < n; ++t) rms_norm(h + t * H, &L->attn_norm, H, m->rms_eps, xn + t * H);
-        linear(s, &L->wq, xn, n, q);
+        act_rows in;
+        act_prepare(s, &in, h, &L->attn_norm, H, n, xn);
+        linear(s, &L->wq, &in, q);
         add_bias(q, &L->bq, n, H);
-        linear(s, &L->wk, xn, n, k);
+        linear(s, &L->wk, &in, k);
         add_bias(k, &L->bk, n, kv);
-        linear(s, &L->wv, xn, n, v);
+        linear(s, &L->wv, &in, v);
         add_bias(v, &L->bv, n, kv);
+        act_release(&in);
         rope_rows(s, q, n, m->n_head, pos0);
         rope_rows(s, k, n, m->n_head_kv, pos0);
         for (int32_t t = 0; t < n; ++t) {
@@ -285,23 +384,28 @@ int32_t jfo_session_forward(jfo_session * s, const int32_t * tokens, int32_t n,
             }
         }
         attention(s, l, q, n, pos0, att);
-        linear(s, &L->wo, att, n, o);
+        act_prepare(s, &in, att, NULL, H, n, NULL);
+        linear(s, &L->wo, &in, o);
+        act_release(&in);
         for (int64_t i = 0; i < n * H; ++i) h[i] += o[i];
-        for (int32_t t = 0; t < n; ++t) rms_norm(h + t * H, &L->ffn_norm, H, m->rms_eps, xn + t * H);
-        linear(s, &L->w_up, xn, n, u);
-        linear(s, &L->w_gate, xn, n, g);
+        act_prepare(s, &in, h, &L->ffn_norm, H, n, xn);
+        linear(s, &L->w_up, &in, u);
+        linear(s, &L->w_gate, &in, g);
+        act_release(&in);
         for (int64_t i = 0; i < n * F; ++i) g[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
-        linear(s, &L->w_down, g, n, o);
+        act_prepare(s, &in, g, NULL, F, n, NULL);
+        linear(s, &L->w_down, &in, o);
+        act_release(&in);
         for (int64_t i = 0; i < n * H; ++i) h[i] += o[i];
     }
     if (logits_rows > 0) {
         const int32_t first = n - logits_rows;
         const int64_t V = m->n_vocab;
         float * lg = logits ? logits : malloc(sizeof(float) * (size_t) (logits_rows * V));
-        for (int32_t r = 0; r < logits_rows; ++r) {
-            rms_norm(h + (first + r) * H, &m->output_norm, H, m->rms_eps, xn + r * H);
-        }
-        linear(s, &m->output, xn, logits_rows, lg);
+        act_rows in;
+        act_prepare(s, &in, h + (size_t) first * H, &m->output_norm, H, logits_rows, xn);
+        linear(s, &m->output, &in, lg);
+        act_release(&in);
         add_bias(lg, &m->output_bias, logits_rows, V);
         if (argmax_out) {
             for (int32_t r = 0; r < logits_rows; ++r) argmax_out[r] = jfo_argmax(lg + r * V, V);
