@@ -16,6 +16,7 @@ the CPU oracle (C, OpenMP) on the host cores over a bounded sample.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -49,6 +50,8 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=None)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--copy-probe-mib", type=int, default=256,
+                    help="size of the device-to-device copy that calibrates PMC byte counters (0: none)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -69,6 +72,8 @@ def main() -> int:
     engine = jf.NativeEngine(model)
     log(f"engine on {engine.device_name}: {engine.weight_bytes / 1e9:.3f} GB of weights uploaded in "
         f"{time.perf_counter() - t0:.1f}s")
+
+    copy_gbs = copy_probe(args.copy_probe_mib) if args.copy_probe_mib > 0 else None
 
     rng = np.random.default_rng(args.seed)
     prompt = [int(t) for t in rng.integers(0, cfg.n_vocab, context)]
@@ -169,6 +174,7 @@ def main() -> int:
         "verify_hbm_fraction": round(verify_bytes / (verify_mean * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "decode_step_bytes": round(step_bytes),
         "prefill_ms": round(prefill_ms, 1),
+        "copy_probe_gbs": copy_gbs,
         "roofline": {
             "bound": "hbm",
             "kernel": dominant["kernel"],
@@ -176,7 +182,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic_per_launch(wl.name, dominant["kernel"]),
             "launch_us": round(per_launch_ms * 1e3, 2),
             "launch_bytes": round(per_launch_bytes),
         },
@@ -186,6 +192,52 @@ def main() -> int:
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def copy_probe(mib: int) -> float:
+    """One device-to-device copy of `mib` MiB through the HIP runtime (its blit
+    kernel reads and writes exactly that many bytes): the known-size kernel
+    that scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings. Returns its
+    copy rate in GB/s (bytes read + written per second)."""
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    n = ctypes.c_size_t(mib << 20)
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    start, stop = ctypes.c_void_p(), ctypes.c_void_p()
+    for call, what in ((lambda: hip.hipMalloc(ctypes.byref(src), n), "hipMalloc"),
+                       (lambda: hip.hipMalloc(ctypes.byref(dst), n), "hipMalloc"),
+                       (lambda: hip.hipMemset(src, 1, n), "hipMemset"),
+                       (lambda: hip.hipEventCreate(ctypes.byref(start)), "hipEventCreate"),
+                       (lambda: hip.hipEventCreate(ctypes.byref(stop)), "hipEventCreate"),
+                       (lambda: hip.hipDeviceSynchronize(), "hipDeviceSynchronize"),
+                       (lambda: hip.hipEventRecord(start, None), "hipEventRecord"),
+                       (lambda: hip.hipMemcpyAsync(dst, src, n, 3, None), "hipMemcpyAsync"),
+                       (lambda: hip.hipEventRecord(stop, None), "hipEventRecord"),
+                       (lambda: hip.hipEventSynchronize(stop), "hipEventSynchronize")):
+        rc = call()
+        if rc != 0:
+            raise RuntimeError(f"copy probe: {what} failed ({rc})")
+    ms = ctypes.c_float()
+    hip.hipEventElapsedTime(ctypes.byref(ms), start, stop)
+    hip.hipEventDestroy(start)
+    hip.hipEventDestroy(stop)
+    hip.hipFree(src)
+    hip.hipFree(dst)
+    gbs = 2 * n.value / (ms.value * 1e-3) / 1e9
+    log(f"copy probe: {mib} MiB device-to-device in {ms.value * 1e3:.1f} us = {gbs:.0f} GB/s (read + write)")
+    return round(gbs, 1)
+
+
+def traffic_per_launch(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed PMC summary of this
+    workload (FETCH_SIZE + WRITE_SIZE, scaled by the copy probe), else None."""
+    path = os.path.join(ROOT, "profiles", f"pmc_traffic_{workload}.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+            return int(parts[2])
+    return None
 
 
 def cpu_baseline(model, cfg, context, args):

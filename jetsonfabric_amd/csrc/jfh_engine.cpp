@@ -519,10 +519,15 @@ void Engine::timed(const std::string& label, double bytes, F&& fn) {
     e.bytes = bytes;
     hip_check(hipEventCreate(&e.begin), "profile event");
     hip_check(hipEventCreate(&e.end), "profile event");
-    hip_check(hipEventRecord(e.begin, stream_), "profile event");
-    fn();
-    hip_check(hipEventRecord(e.end, stream_), "profile event");
     prof_->push_back(e);
+    gpu::set_launch_events(e.begin, e.end);
+    try {
+        fn();
+    } catch (...) {
+        gpu::set_launch_events(nullptr, nullptr);
+        throw;
+    }
+    gpu::set_launch_events(nullptr, nullptr);
 }
 
 void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_out, bool store_logits) {

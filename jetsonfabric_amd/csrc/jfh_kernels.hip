@@ -9,6 +9,7 @@
 // (activation q8 blocks + integer dot).
 #include "jfh_kernels.hpp"
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -1261,6 +1262,24 @@ void check(hipError_t e, const char* what) {
     if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// Events of the launch being timed (set_launch_events). The first launch
+// records `start` when its dispatch begins; every launch records `stop` when
+// it ends, so a launcher that issues several kernels is timed from the first
+// dispatch to the last.
+thread_local hipEvent_t t_start = nullptr;
+thread_local hipEvent_t t_stop = nullptr;
+
+template <typename... KArgs, typename... Args>
+void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStream_t stream, Args... args) {
+    if (t_stop != nullptr) {
+        hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), stream, t_start, t_stop, 0u,
+                              static_cast<KArgs>(args)...);
+        t_start = nullptr;
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, static_cast<KArgs>(args)...);
+    }
+}
+
 // Host-side geometry. The K chunk staged per pass is fixed (kMmChunk values)
 // whatever the token count, so every row's partial sums are added in the
 // same order for 1 and for 8 tokens: a draft-verify step reproduces serial
@@ -1302,7 +1321,7 @@ void mm(const GemvArgs& a, hipStream_t stream) {
     const MmGeom g = mm_geom(a, NT, lds);
     const int n_rg = (static_cast<int>(a.mat.rows) + 15) / 16;
     const int grid = (n_rg + g.rgw - 1) / g.rgw;
-    hipLaunchKernelGGL((k_mm<TYPE, NT>), dim3(grid), dim3(kMmThreads), lds, stream, a, g);
+    launch(k_mm<TYPE, NT>, dim3(grid), dim3(kMmThreads), lds, stream, a, g);
     check(hipGetLastError(), "matmul launch");
 }
 
@@ -1322,11 +1341,16 @@ template <int NT>
 void gemv_f(const GemvArgs& a, hipStream_t stream) {
     const int grid = (static_cast<int>(a.mat.rows) + kGemvFloatRows - 1) / kGemvFloatRows;
     const size_t lds = static_cast<size_t>(kGemvFloatRows) * NT * sizeof(float);
-    hipLaunchKernelGGL((k_gemv_f<NT>), dim3(grid), dim3(kFloatThreads), lds, stream, a, kGemvFloatRows);
+    launch(k_gemv_f<NT>, dim3(grid), dim3(kFloatThreads), lds, stream, a, kGemvFloatRows);
     check(hipGetLastError(), "gemv launch");
 }
 
 }  // namespace
+
+void set_launch_events(hipEvent_t start, hipEvent_t stop) {
+    t_start = start;
+    t_stop = stop;
+}
 
 float dequant_tile_value(uint32_t type, const uint8_t* tile, uint32_t row, uint32_t k) {
     return tile_value(type, tile, row, k);
@@ -1386,14 +1410,14 @@ void launch_gemv(const GemvArgs& a_in, hipStream_t stream) {
 void launch_quantize(const float* x, int32_t stride, int32_t n_rows, const Act8& out, hipStream_t stream) {
     if (out.K % 256 != 0 || stride % 4 != 0) throw std::invalid_argument("quantized rows need multiples of 256 values");
     dim3 grid((out.K / 256 + 3) / 4, n_rows);
-    hipLaunchKernelGGL(k_quantize, grid, dim3(256), 0, stream, x, stride, out);
+    launch(k_quantize, grid, dim3(256), 0, stream, x, stride, out);
     check(hipGetLastError(), "quantize launch");
 }
 
 void launch_embed(const DMat& table, const StepDev* step, float* h, int32_t n_rows, int32_t H,
                   unsigned long long* best, int32_t n_best, hipStream_t stream) {
     dim3 grid((H + 255) / 256, n_rows);
-    hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, stream, table, step, h, H, best, n_best);
+    launch(k_embed, grid, dim3(256), 0, stream, table, step, h, H, best, n_best);
     check(hipGetLastError(), "embed launch");
 }
 
@@ -1417,13 +1441,13 @@ void launch_attention(const float* q, const StepDev* step, int32_t max_len, int3
     if (qgroups > kMaxAttnQGroups) throw std::invalid_argument("attention step has too many query rows per kv head");
     dim3 grid(splits, n_head_kv * qgroups, n_seq), block(kAttnThreads);
     if (head_dim == 128) {
-        hipLaunchKernelGGL(k_attention<128>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
+        launch(k_attention<128>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
                            qgroups, partial);
     } else if (head_dim == 64) {
-        hipLaunchKernelGGL(k_attention<64>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
+        launch(k_attention<64>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
                            qgroups, partial);
     } else {
-        hipLaunchKernelGGL(k_attention<0>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
+        launch(k_attention<0>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
                            qgroups, partial);
     }
     check(hipGetLastError(), "attention launch");
@@ -1434,19 +1458,19 @@ void launch_attention_merge(const float* partial, const StepDev* step, int32_t n
     const int H = n_head * head_dim;
     if (xq.q != nullptr && (H % 256 != 0 || xq.K != H)) throw std::invalid_argument("merge quantization shape mismatch");
     dim3 grid((H + 255) / 256, n_rows);
-    hipLaunchKernelGGL(k_attention_merge, grid, dim3(256), 0, stream, partial, step, n_head, head_dim, splits, out, xq);
+    launch(k_attention_merge, grid, dim3(256), 0, stream, partial, step, n_head, head_dim, splits, out, xq);
     check(hipGetLastError(), "attention merge launch");
 }
 
 void launch_finish(const unsigned long long* best, const StepDev* step, int32_t n_out, StepOut* out,
                    hipStream_t stream) {
-    hipLaunchKernelGGL(k_finish, dim3(1), dim3(64), 0, stream, best, step, n_out, out);
+    launch(k_finish, dim3(1), dim3(64), 0, stream, best, step, n_out, out);
     check(hipGetLastError(), "finish launch");
 }
 
 void launch_dequant_rows(const DMat& m, int32_t row0, int32_t n_rows, float* out, hipStream_t stream) {
     dim3 grid((m.cols + 255) / 256, n_rows);
-    hipLaunchKernelGGL(k_dequant_rows, grid, dim3(256), 0, stream, m, row0, out);
+    launch(k_dequant_rows, grid, dim3(256), 0, stream, m, row0, out);
     check(hipGetLastError(), "dequant launch");
 }
 

@@ -135,6 +135,13 @@ struct GemvArgs {
 };
 
 // Launchers (all asynchronous on `stream`).
+//
+// Kernel timing for profiles: while `stop` is set, the launchers of the
+// calling thread attach the events to their kernel dispatches
+// (hipExtLaunchKernel): `start` takes the begin time of the next dispatch,
+// `stop` the end time of the last, so the elapsed time excludes queueing and
+// launch gaps. Pass nullptrs to switch it off.
+void set_launch_events(hipEvent_t start, hipEvent_t stop);
 void launch_embed(const DMat& table, const StepDev* step, float* h, int32_t n_rows, int32_t H,
                   unsigned long long* best, int32_t n_best, hipStream_t stream);
 // Matmul of up to kMaxRows token rows (in groups of 8) against one matrix.
