@@ -240,8 +240,9 @@ jfh_status jfh_session_time_steps(jfh_session * session, const int32_t * tokens,
 
 /* Per-kernel profile of one step (no reference counterpart: the reference
  * measures with Nsight, docs/benchmarks/evidence/...kernels_cuda_gpu_kern_sum.csv).
- * The step runs `iterations` times without graphs with HIP events around every
- * launch on the engine stream; one entry per kernel, sorted by device time. */
+ * The step runs `iterations` times without graphs with HIP events attached to
+ * every kernel dispatch (hipExtLaunchKernel) on the engine stream; one entry
+ * per kernel and role, sorted by device time. */
 typedef struct jfh_kernel_stat {
     char label[64];
     double launches; /* per step */

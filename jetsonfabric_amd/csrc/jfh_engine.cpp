@@ -312,6 +312,9 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
     hipDeviceProp_t prop{};
     hip_check(hipGetDeviceProperties(&prop, options.device), "device properties");
     device_name_ = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0) {
+        fail(Status::DeviceError, "the native engine's kernels are built for gfx950 only; device is " + device_name_);
+    }
     hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "create stream");
 
     if (model.layer_start() != 0 || model.layer_end() != params_.n_layer) {

@@ -66,8 +66,8 @@ struct SeqStep {
     int logits = 1;
 };
 
-// Per-kernel device time of one step, measured with HIP events around every
-// launch of an un-graphed step (averaged over iterations).
+// Per-kernel device time of one step, measured with HIP events attached to
+// the kernel dispatches of an un-graphed step (averaged over iterations).
 struct KernelStat {
     std::string label;
     double launches = 0.0;   // launches per step

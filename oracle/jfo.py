@@ -292,11 +292,14 @@ def prompt_lookup(history: Sequence[int], max_tokens: int, max_ngram: int = 4, m
 
 def speculative_generate(prefill: Callable[[Sequence[int]], int], verify: Callable[[Sequence[int]], list[int]],
                          rollback: Callable[[int], None], prompt: Sequence[int], max_tokens: int, draft_max: int,
-                         max_ngram: int = 4, min_ngram: int = 2, is_eog: Callable[[int], bool] = lambda t: False):
+                         max_ngram: int = 4, min_ngram: int = 2, is_eog: Callable[[int], bool] = lambda t: False,
+                         propose: Callable[[list[int], int], list[int]] | None = None):
     """GenerationRunner::run speculative section (generation_runner.cpp:398-566) for one stage.
 
     prefill(prompt) -> first token; verify([prev, draft...]) -> greedy id after every row;
-    rollback(n) removes n decoded positions. Returns (tokens, stats).
+    rollback(n) removes n decoded positions. `propose(history, budget)` replaces
+    the prompt-lookup draft strategy (the runner takes any DraftStrategy,
+    generation_runner.hpp). Returns (tokens, stats).
     """
     stats = {"target_decode_passes": 0, "speculative_draft_tokens": 0, "speculative_accepted_tokens": 0,
              "rollbacks": []}
@@ -313,7 +316,9 @@ def speculative_generate(prefill: Callable[[Sequence[int]], int], verify: Callab
         remaining = max_tokens - len(out)
         draft = []
         if draft_max > 0 and remaining > 1 and not recover:
-            draft = prompt_lookup(history, min(draft_max, remaining - 1), max_ngram, min_ngram)
+            budget = min(draft_max, remaining - 1)
+            draft = (propose(list(history), budget) if propose is not None
+                     else prompt_lookup(history, budget, max_ngram, min_ngram))
         recover = False
         verification = [previous] + draft
         target = verify(verification)

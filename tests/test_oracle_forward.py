@@ -249,6 +249,29 @@ def test_speculative_loop_is_greedy_invariant():
     assert stats["speculative_accepted_tokens"] <= stats["speculative_draft_tokens"]
 
 
+def test_speculative_loop_reference_harness_case():
+    """generation_runner_test.cpp:355-389: history [1,2,1,2,10], a fixed draft
+    [20,21] and a target that answers [20,99,30] emit [10,20,99] in one pass
+    with one rejected token rolled back."""
+    rollbacks = []
+
+    def fixed_draft(history, budget):
+        return [20, 21] if history == [1, 2, 1, 2, 10] else []
+
+    out, stats = jo.speculative_generate(lambda p: 10, lambda rows: [20, 99, 30][:len(rows)], rollbacks.append,
+                                         [1, 2, 1, 2], 3, 2, propose=fixed_draft)
+    assert out == [10, 20, 99]
+    assert stats["target_decode_passes"] == 1
+    assert stats["speculative_draft_tokens"] == 2 and stats["speculative_accepted_tokens"] == 1
+    assert rollbacks == [1]
+
+
+def test_argmax_first_maximum():
+    x = np.array([1.0, 3.0, -2.0, 3.0, 3.0], dtype=np.float32)
+    assert jo.argmax(x) == 1
+    assert jo.argmax(np.full(7, -np.inf, dtype=np.float32)) == 0
+
+
 # ------------------------------------------------------------------ prompt lookup
 
 def test_prompt_lookup_reference_known_answers():

@@ -161,6 +161,17 @@ def test_f16_conversion_is_ieee_binary16():
     for x in [0.0, 1.0, -2.5, 65504.0, 6.1035156e-05, 5.9604645e-08, 0.1, 1e-3]:
         assert jo.f32_to_f16(x) == f16_bits(x)
         assert jo.f16_to_f32(f16_bits(x)) == np.float32(np.float16(x))
+    # every finite binary16 code decodes exactly; rounding ties go to even
+    codes = np.arange(65536, dtype=np.uint16)
+    vals = codes.view(F16).astype(np.float32)
+    for c in range(65536):
+        if np.isfinite(vals[c]):
+            assert jo.f16_to_f32(int(c)) == vals[c], c
+    rng = np.random.default_rng(3)
+    for x in np.concatenate([rng.standard_normal(500) * 10.0, rng.standard_normal(200) * 1e-5]).astype(np.float32):
+        assert jo.f32_to_f16(float(x)) == f16_bits(x), x
+    halfway = np.float32(1.0 + 2.0 ** -11)  # between 1.0 and the next binary16 value: ties to even (1.0)
+    assert jo.f32_to_f16(float(halfway)) == f16_bits(1.0)
 
 
 # ------------------------------------------------------------------ special blocks
