@@ -267,45 +267,71 @@ __device__ void row_rms(const XIn& x, int n_tok, int K, float* rs, float* red) {
 // gain (RMSNorm input) the codes are those of x * gain and ssq[t][b] receives
 // the block's sum of x^2; the block scales are multiplied by the row's
 // 1/rms afterwards (finish_norm), so one pass over x serves both.
+//
+// The first batch of a pass is loaded ahead (stage_f32_load) and handed in:
+// a wave's loads complete in issue order, so activations requested before the
+// weight prefetch are not held up behind the weight tiles.
 constexpr int kStageBatch = 4;
-#pragma clang fp contract(off)
-template <int NT, int NTHR>
-__device__ void stage_f32(const XIn& x, const int* rowidx, int n_tok, int c0, int nb, int8_t* sq, float* sd,
-                          int16_t* ss, float* ssq, int chunk) {
+
+// Registers of one staging batch: values and gains of kStageBatch pieces.
+using StageF32Regs = float4[2 * kStageBatch];
+
+// Loads the batch of blocks j0, j0 + W, ... (indices clamped so that every
+// load is issued unconditionally).
+template <int NTHR>
+__device__ __forceinline__ void stage_f32_load(const XIn& x, int n_tok, int c0, int nb, int j0, StageF32Regs& r) {
     constexpr int W = NTHR / kWave;
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
     const int total = n_tok * nb;
-    // a batch of kStageBatch blocks per wave is requested at once (indices
-    // clamped so that every load is issued unconditionally)
-    for (int j0 = wave; j0 < total; j0 += kStageBatch * W) {
-        float4 v[kStageBatch];
-        float4 gv[kStageBatch];
 #pragma unroll
-        for (int u = 0; u < kStageBatch; ++u) {
-            const int j = min(j0 + u * W, total - 1);
+    for (int u = 0; u < kStageBatch; ++u) {
+        const int j = min(j0 + u * W, total - 1);
+        const int t = j / nb, b = j - t * nb;
+        const int c = c0 + b * 256 + 4 * lane;
+        r[u] = *reinterpret_cast<const float4*>(x_row(x, t) + c);
+        r[kStageBatch + u] = *reinterpret_cast<const float4*>((x.gain ? x.gain : x.x) + c);  // unused without a gain
+    }
+}
+
+#pragma clang fp contract(off)
+template <int NTHR>
+__device__ __forceinline__ void stage_f32_store(const XIn& x, int n_tok, int nb, int j0, const StageF32Regs& r,
+                                                int8_t* sq, float* sd, int16_t* ss, float* ssq, int chunk) {
+    constexpr int W = NTHR / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int total = n_tok * nb;
+#pragma unroll
+    for (int u = 0; u < kStageBatch; ++u) {
+        const int j = j0 + u * W;
+        if (j < total) {
             const int t = j / nb, b = j - t * nb;
-            const int c = c0 + b * 256 + 4 * lane;
-            v[u] = *reinterpret_cast<const float4*>(x.x + static_cast<size_t>(rowidx[t]) * x.stride + c);
-            gv[u] = x.gain ? *reinterpret_cast<const float4*>(x.gain + c) : make_float4(1.0F, 1.0F, 1.0F, 1.0F);
-        }
-#pragma unroll
-        for (int u = 0; u < kStageBatch; ++u) {
-            const int j = j0 + u * W;
-            if (j < total) {
-                const int t = j / nb, b = j - t * nb;
-                float vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-                if (x.gain) {
-                    const float sq2 = wave_sum(vv[0] * vv[0] + vv[1] * vv[1] + vv[2] * vv[2] + vv[3] * vv[3]);
-                    if (lane == 0) ssq[t * nb + b] = sq2;
-                    vv[0] = vv[0] * gv[u].x;
-                    vv[1] = vv[1] * gv[u].y;
-                    vv[2] = vv[2] * gv[u].z;
-                    vv[3] = vv[3] * gv[u].w;
-                }
-                quant_block_wave(vv, lane, sq + t * chunk + b * 256, sd + t * (chunk / 256) + b,
-                                 ss + t * (chunk / 16) + b * 16);
+            float vv[4] = {r[u].x, r[u].y, r[u].z, r[u].w};
+            if (x.gain) {
+                const float sq2 = wave_sum(vv[0] * vv[0] + vv[1] * vv[1] + vv[2] * vv[2] + vv[3] * vv[3]);
+                if (lane == 0) ssq[t * nb + b] = sq2;
+                vv[0] = vv[0] * r[kStageBatch + u].x;
+                vv[1] = vv[1] * r[kStageBatch + u].y;
+                vv[2] = vv[2] * r[kStageBatch + u].z;
+                vv[3] = vv[3] * r[kStageBatch + u].w;
             }
+            quant_block_wave(vv, lane, sq + t * chunk + b * 256, sd + t * (chunk / 256) + b,
+                             ss + t * (chunk / 16) + b * 16);
         }
+    }
+}
+#pragma clang fp contract(on)
+
+template <int NTHR>
+__device__ __forceinline__ void stage_f32(const XIn& x, int n_tok, int c0, int nb, int8_t* sq, float* sd, int16_t* ss,
+                                          float* ssq, int chunk, const StageF32Regs& first) {
+    constexpr int W = NTHR / kWave;
+    const int wave = threadIdx.x / kWave;
+    const int total = n_tok * nb;
+    stage_f32_store<NTHR>(x, n_tok, nb, wave, first, sq, sd, ss, ssq, chunk);
+    for (int j0 = wave + kStageBatch * W; j0 < total; j0 += kStageBatch * W) {
+        StageF32Regs r;
+        stage_f32_load<NTHR>(x, n_tok, c0, nb, j0, r);
+        stage_f32_store<NTHR>(x, n_tok, nb, j0, r, sq, sd, ss, ssq, chunk);
     }
 }
 
@@ -329,40 +355,66 @@ __device__ void finish_norm(int n_tok, int nb, int K, float eps, const float* ss
 }
 #pragma clang fp contract(on)
 
-// Copies values [c0, c0 + nb*256) of pre-quantized rows into the LDS chunk,
-// every thread requesting up to 4 pieces before storing any.
+// Copies values [c0, c0 + nb*256) of pre-quantized rows into the LDS chunk.
+// Batch b of a thread holds code pieces tid + (4 b + u) NTHR (uint4, u < 4),
+// sum piece tid + b NTHR (uint4 of 8 int16) and block scale tid + b NTHR;
+// indices are clamped so that every load is issued unconditionally. As with
+// stage_f32, the first batch is loaded ahead of the weights.
+using StageA8Regs = u32x4[6];
+
 template <int NTHR>
-__device__ void stage_act8(const Act8& xq, int n_tok, int c0, int nb, int8_t* sq, float* sd, int16_t* ss, int chunk) {
-    const int n16 = nb * 16;                     // uint4 of codes per token
-    const int nq = n_tok * n16, ns = n_tok * nb * 2, nd = n_tok * nb;
-    const int total = nq + ns;                    // uint4 pieces (codes, then sums)
-    for (int i0 = threadIdx.x; i0 < total; i0 += 4 * NTHR) {
-        uint4 v[4];
+__device__ __forceinline__ void stage_act8_load(const Act8& xq, int n_tok, int c0, int nb, int batch, StageA8Regs& r) {
+    const int tid = threadIdx.x, n16 = nb * 16, nq = n_tok * n16, ns = n_tok * nb * 2, nd = n_tok * nb;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = min(i0 + u * NTHR, total - 1);
-            const bool codes = i < nq;
-            const int t = codes ? i / n16 : (i - nq) / (nb * 2);
-            const int k = codes ? i - t * n16 : (i - nq) - t * nb * 2;
-            const uint4* src = codes ? reinterpret_cast<const uint4*>(xq.q + static_cast<size_t>(t) * xq.K + c0)
-                                     : reinterpret_cast<const uint4*>(xq.s + static_cast<size_t>(t) * (xq.K / 16) + c0 / 16);
-            v[u] = src[k];
-        }
+    for (int u = 0; u < 4; ++u) {
+        const int i = min(tid + (4 * batch + u) * NTHR, nq - 1);
+        const int t = i / n16, k = i - t * n16;
+        r[u] = *reinterpret_cast<const u32x4*>(xq.q + static_cast<size_t>(t) * xq.K + c0 + 16 * k);
+    }
+    {
+        const int i = min(tid + batch * NTHR, ns - 1);
+        const int t = i / (2 * nb), k = i - t * 2 * nb;
+        r[4] = *reinterpret_cast<const u32x4*>(xq.s + static_cast<size_t>(t) * (xq.K / 16) + c0 / 16 + 8 * k);
+    }
+    {
+        const int i = min(tid + batch * NTHR, nd - 1);
+        const int t = i / nb, b = i - t * nb;
+        r[5].x = __float_as_uint(xq.d[static_cast<size_t>(t) * (xq.K / 256) + c0 / 256 + b]);
+    }
+}
+
+template <int NTHR>
+__device__ __forceinline__ void stage_act8_store(int n_tok, int nb, int batch, const StageA8Regs& r, int8_t* sq,
+                                                 float* sd, int16_t* ss, int chunk) {
+    const int tid = threadIdx.x, n16 = nb * 16, nq = n_tok * n16, ns = n_tok * nb * 2, nd = n_tok * nb;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = i0 + u * NTHR;
-            if (i < nq) {
-                const int t = i / n16, k = i - t * n16;
-                reinterpret_cast<uint4*>(sq + t * chunk)[k] = v[u];
-            } else if (i < total) {
-                const int t = (i - nq) / (nb * 2), k = (i - nq) - t * nb * 2;
-                reinterpret_cast<uint4*>(ss + t * (chunk / 16))[k] = v[u];
-            }
+    for (int u = 0; u < 4; ++u) {
+        const int i = tid + (4 * batch + u) * NTHR;
+        if (i < nq) {
+            const int t = i / n16, k = i - t * n16;
+            reinterpret_cast<u32x4*>(sq + t * chunk)[k] = r[u];
         }
     }
-    for (int i = threadIdx.x; i < nd; i += NTHR) {
+    const int i = tid + batch * NTHR;
+    if (i < ns) {
+        const int t = i / (2 * nb), k = i - t * 2 * nb;
+        reinterpret_cast<u32x4*>(ss + t * (chunk / 16))[k] = r[4];
+    }
+    if (i < nd) {
         const int t = i / nb, b = i - t * nb;
-        sd[t * (chunk / 256) + b] = xq.d[static_cast<size_t>(t) * (xq.K / 256) + c0 / 256 + b];
+        sd[t * (chunk / 256) + b] = __uint_as_float(r[5].x);
+    }
+}
+
+template <int NTHR>
+__device__ __forceinline__ void stage_act8(const Act8& xq, int n_tok, int c0, int nb, int8_t* sq, float* sd,
+                                           int16_t* ss, int chunk, const StageA8Regs& first) {
+    const int nq = n_tok * nb * 16, ns = n_tok * nb * 2;
+    stage_act8_store<NTHR>(n_tok, nb, 0, first, sq, sd, ss, chunk);
+    for (int batch = 1; batch * 4 * NTHR < nq || batch * NTHR < ns; ++batch) {
+        StageA8Regs r;
+        stage_act8_load<NTHR>(xq, n_tok, c0, nb, batch, r);
+        stage_act8_store<NTHR>(n_tok, nb, batch, r, sq, sd, ss, chunk);
     }
 }
 
@@ -734,7 +786,8 @@ struct MmGeom {
     int32_t chunk;  // K values staged per pass (multiple of 256)
 };
 
-template <uint32_t TYPE, int NT>
+// A8: the activations arrive pre-quantized (a.xq), else as float rows (a.x).
+template <uint32_t TYPE, int NT, bool A8>
 __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, MmGeom geo) {
     using T = Tile<TYPE>;
     using Regs = typename T::Regs;
@@ -751,7 +804,6 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
     float* rs = part + rgw * W * 64 * NT;
     float* ssq = rs + NT;       // [NT][nbc] block sums of squares (normed inputs)
     float* lv = ssq + NT * nbc;  // [rgw * 16 * NT]
-    int* rowidx = reinterpret_cast<int*>(lv + rgw * 16 * NT);  // [NT] source row of each token
 
     const int n_rg = (static_cast<int>(a.mat.rows) + 15) / 16;
     const int rg0 = blockIdx.x * rgw;
@@ -792,35 +844,42 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
             }
         }
     };
+    // A wave without tiles in the pass (total == 0) loads its ring from the
+    // pass's last tile and never uses it: loads stay unconditional.
     auto prefetch = [&](int c0b) {
-        loff = static_cast<uint32_t>(c0b + wave) * TB;
+        loff = static_cast<uint32_t>(c0b + min(wave, nbcur - 1)) * TB;
         lm = 0;
         lleft = total - 1;
 #pragma unroll
         for (int u = 0; u < kMmDepth; ++u) load_next(ring[u]);
     };
-    if (total > 0) prefetch(0);
+    // the first staging batch is requested before the weights (loads complete
+    // in issue order, so the activations do not wait behind weight tiles)
+    StageF32Regs f0;
+    StageA8Regs q0;
+    if constexpr (A8) stage_act8_load<kMmThreads>(a.xq, n_tok, 0, nbcur, 0, q0);
+    else stage_f32_load<kMmThreads>(a.x, n_tok, 0, nbcur, wave, f0);
+    prefetch(0);
     // the residual the epilogue adds to is fetched with the first weights
-    float y_pre = 0.0F;
-    if (a.mode == kAdd && threadIdx.x < static_cast<unsigned>(nrows * n_tok)) {
-        const int t = threadIdx.x / nrows, j = threadIdx.x - t * nrows;
-        y_pre = a.y[static_cast<size_t>(t) * a.y_stride + row0 + j];
-    }
-    const bool act8 = a.xq.q != nullptr;
-    if (threadIdx.x < NT) {
-        const int t = min(static_cast<int>(threadIdx.x), n_tok - 1);
-        rowidx[threadIdx.x] = act8 ? t : (a.x.gather ? a.x.gather[t] : t);
+    // (issued unconditionally from a clamped index, so that the compiler's
+    // count of outstanding loads stays exact)
+    float y_pre;
+    {
+        const int idx = min(static_cast<int>(threadIdx.x), nrows * n_tok - 1);
+        const int t = idx / nrows, j = idx - t * nrows;
+        const float* src = a.mode == kAdd ? a.y + static_cast<size_t>(t) * a.y_stride + row0 + j
+                                          : reinterpret_cast<const float*>(a.mat.data);
+        y_pre = *src;
     }
     for (int i = threadIdx.x; i < rgw * W * 64 * NT; i += kMmThreads) part[i] = 0.0F;
+    if constexpr (A8) {
+        stage_act8<kMmThreads>(a.xq, n_tok, 0, nbcur, sq, sd, ss, chunk, q0);
+    } else {
+        stage_f32<kMmThreads>(a.x, n_tok, 0, nbcur, sq, sd, ss, ssq, chunk, f0);
+        if (a.x.gain) finish_norm<kMmThreads>(n_tok, nbcur, K, a.x.eps, ssq, sd, rs, chunk);
+    }
 
     for (int c0b = 0;;) {
-        __syncthreads();
-        if (act8) {
-            stage_act8<kMmThreads>(a.xq, n_tok, c0b * 256, nbcur, sq, sd, ss, chunk);
-        } else {
-            stage_f32<NT, kMmThreads>(a.x, rowidx, n_tok, c0b * 256, nbcur, sq, sd, ss, ssq, chunk);
-            if (a.x.gain) finish_norm<kMmThreads>(n_tok, nbcur, K, a.x.eps, ssq, sd, rs, chunk);
-        }
         __syncthreads();
         if (total > 0) {
             float acc[NT];
@@ -857,10 +916,23 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
         }
         c0b += nbc;
         if (c0b >= nb) break;
+        // next pass (rows that are not normalized): activations first, then weights
         nbcur = min(nbc, nb - c0b);
         pr = per_rg(nbcur);
         total = pr * rgn;
-        if (total > 0) prefetch(c0b);
+        if constexpr (A8) {
+            StageA8Regs qn;
+            stage_act8_load<kMmThreads>(a.xq, n_tok, c0b * 256, nbcur, 0, qn);
+            prefetch(c0b);
+            __syncthreads();  // every wave is done with the previous pass's activations
+            stage_act8<kMmThreads>(a.xq, n_tok, c0b * 256, nbcur, sq, sd, ss, chunk, qn);
+        } else {
+            StageF32Regs fn;
+            stage_f32_load<kMmThreads>(a.x, n_tok, c0b * 256, nbcur, wave, fn);
+            prefetch(c0b);
+            __syncthreads();
+            stage_f32<kMmThreads>(a.x, n_tok, c0b * 256, nbcur, sq, sd, ss, ssq, chunk, fn);
+        }
     }
     __syncthreads();
     auto sum = [&](int j, int t) {
@@ -1280,11 +1352,11 @@ void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStre
     }
 }
 
-// Host-side geometry. The K chunk staged per pass is fixed (kMmChunk values)
-// whatever the token count, so every row's partial sums are added in the
-// same order for 1 and for 8 tokens: a draft-verify step reproduces serial
-// decode bit for bit. The per-wave row partials take at most kMmPartBytes of
-// LDS, and the row groups per work-group aim at kMmTargetWgs work-groups.
+// Host-side geometry. Rows are staged in one pass or in passes of kMmChunk
+// values; either way every row's partial sums are added in the same order
+// for 1 and for 8 tokens, so a draft-verify step reproduces serial decode bit
+// for bit. The per-wave row partials take at most kMmPartBytes of LDS, and
+// the row groups per work-group aim at kMmTargetWgs work-groups.
 #ifndef JFH_MM_CHUNK
 #define JFH_MM_CHUNK 8192
 #endif
@@ -1294,23 +1366,35 @@ void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStre
 constexpr int kMmChunk = JFH_MM_CHUNK;
 constexpr int kMmPartBytes = 65536;
 constexpr int kMmTargetWgs = JFH_MM_TARGET_WGS;
+constexpr size_t kMmOnePassLds = 64 * 1024;  // largest one-pass staging of a row that is not normalized
+
+size_t mm_lds_bytes(int nt, int chunk, int rgw) {
+    const size_t nbc = static_cast<size_t>(chunk) / 256;
+    return static_cast<size_t>(nt) * chunk + nt * nbc * 4 + static_cast<size_t>(nt) * chunk / 8 +
+           static_cast<size_t>(rgw) * kMmWaves * 64 * nt * 4 + static_cast<size_t>(nt) * 4 + nt * nbc * 4 +
+           static_cast<size_t>(rgw) * 16 * nt * 4;
+}
 
 MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds) {
+    static_assert(kMmChunk % (256 * kMmWaves) == 0, "a chunk must hold whole rounds of the waves' tiles");
     const int K = static_cast<int>(a.mat.cols);
-    // a normalized input is staged whole: its block scales need the full row's rms
-    const int chunk = (K < kMmChunk || (a.xq.q == nullptr && a.x.gain != nullptr)) ? K : kMmChunk;
     const int n_rg = (static_cast<int>(a.mat.rows) + 15) / 16;
     int rgw = (n_rg + kMmTargetWgs - 1) / kMmTargetWgs;
     const int cap = kMmPartBytes / (kMmWaves * 64 * nt * 4);
     if (rgw > cap) rgw = cap;
     if (rgw < 1) rgw = 1;
+    // The whole row is staged in one pass when it fits (a normalized input
+    // always is: its block scales need the full row's rms), else in passes of
+    // kMmChunk values. Wave w takes tiles w, w + W, ... of the row either way
+    // and adds them in increasing order, so the pass length does not change
+    // any sum.
+    const bool normed = a.xq.q == nullptr && a.x.gain != nullptr;
+    int chunk = K;
+    if (!normed && K > kMmChunk && mm_lds_bytes(nt, K, rgw) > kMmOnePassLds) chunk = kMmChunk;
     MmGeom g;
     g.rgw = rgw;
     g.chunk = chunk;
-    const size_t nbc = static_cast<size_t>(chunk) / 256;
-    lds = static_cast<size_t>(nt) * chunk + nt * nbc * 4 + static_cast<size_t>(nt) * chunk / 8 +
-          static_cast<size_t>(rgw) * kMmWaves * 64 * nt * 4 + static_cast<size_t>(nt) * 4 + nt * nbc * 4 +
-          static_cast<size_t>(rgw) * 16 * nt * 4 + static_cast<size_t>(nt) * 4;
+    lds = mm_lds_bytes(nt, chunk, rgw);
     if (lds > 160 * 1024) throw std::invalid_argument("matmul staging does not fit the LDS");
     return g;
 }
@@ -1321,7 +1405,8 @@ void mm(const GemvArgs& a, hipStream_t stream) {
     const MmGeom g = mm_geom(a, NT, lds);
     const int n_rg = (static_cast<int>(a.mat.rows) + 15) / 16;
     const int grid = (n_rg + g.rgw - 1) / g.rgw;
-    launch(k_mm<TYPE, NT>, dim3(grid), dim3(kMmThreads), lds, stream, a, g);
+    if (a.xq.q != nullptr) launch(k_mm<TYPE, NT, true>, dim3(grid), dim3(kMmThreads), lds, stream, a, g);
+    else launch(k_mm<TYPE, NT, false>, dim3(grid), dim3(kMmThreads), lds, stream, a, g);
     check(hipGetLastError(), "matmul launch");
 }
 
