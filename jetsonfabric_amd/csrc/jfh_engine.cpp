@@ -9,6 +9,9 @@
 namespace jfh {
 namespace {
 
+// Token rows up to which the down projection reads the float SwiGLU output.
+constexpr int32_t kFloatDownRows = 2;
+
 void hip_check(hipError_t e, const char* what) {
     if (e != hipSuccess) throw Error(Status::DeviceError, std::string(what) + ": " + hipGetErrorString(e));
 }
@@ -586,7 +589,10 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         dn.mat = L.down->mat;
         dn.mode = gpu::kAdd;
         dn.n_tok = n_rows;
-        if (xq_ffn_.q && quantized(dn.mat.type)) {
+        // Decode steps stage the float SwiGLU rows directly (the matmul
+        // quantizes them in its prologue); larger steps quantize them once.
+        // Both use the same block quantization, so the codes are identical.
+        if (xq_ffn_.q && quantized(dn.mat.type) && n_rows > kFloatDownRows) {
             timed("k_quantize", n * F * 5.1, [&] { gpu::launch_quantize(ffn_, F, n_rows, xq_ffn_, s); });
             dn.xq = xq_ffn_;
         } else {

@@ -271,48 +271,49 @@ __device__ void row_rms(const XIn& x, int n_tok, int K, float* rs, float* red) {
 // The first batch of a pass is loaded ahead (stage_f32_load) and handed in:
 // a wave's loads complete in issue order, so activations requested before the
 // weight prefetch are not held up behind the weight tiles.
-constexpr int kStageBatch = 4;
+constexpr int kStageBatch = 4;        // blocks per wave of a staging batch (normalized rows: values + gains)
+constexpr int kStageBatchFloat = 10;  // blocks per wave of a batch of plain float rows
 
-// Registers of one staging batch: values and gains of kStageBatch pieces.
-using StageF32Regs = float4[2 * kStageBatch];
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// Loads the batch of blocks j0, j0 + W, ... (indices clamped so that every
-// load is issued unconditionally).
-template <int NTHR>
-__device__ __forceinline__ void stage_f32_load(const XIn& x, int n_tok, int c0, int nb, int j0, StageF32Regs& r) {
+// A staging batch of NB blocks per wave lives in f32x4 r[2 NB]: the lane's 4
+// values of each block, then (GAIN) the matching gains. Loads the blocks j0,
+// j0 + W, ... (indices clamped so that every load is issued unconditionally).
+template <int NTHR, int NB, bool GAIN>
+__device__ __forceinline__ void stage_f32_load(const XIn& x, int n_tok, int c0, int nb, int j0, f32x4 (&r)[2 * NB]) {
     constexpr int W = NTHR / kWave;
     const int lane = threadIdx.x & (kWave - 1);
     const int total = n_tok * nb;
 #pragma unroll
-    for (int u = 0; u < kStageBatch; ++u) {
+    for (int u = 0; u < NB; ++u) {
         const int j = min(j0 + u * W, total - 1);
         const int t = j / nb, b = j - t * nb;
         const int c = c0 + b * 256 + 4 * lane;
-        r[u] = *reinterpret_cast<const float4*>(x_row(x, t) + c);
-        r[kStageBatch + u] = *reinterpret_cast<const float4*>((x.gain ? x.gain : x.x) + c);  // unused without a gain
+        r[u] = *reinterpret_cast<const f32x4*>(x_row(x, t) + c);
+        if constexpr (GAIN) r[NB + u] = *reinterpret_cast<const f32x4*>(x.gain + c);
     }
 }
 
 #pragma clang fp contract(off)
-template <int NTHR>
-__device__ __forceinline__ void stage_f32_store(const XIn& x, int n_tok, int nb, int j0, const StageF32Regs& r,
-                                                int8_t* sq, float* sd, int16_t* ss, float* ssq, int chunk) {
+template <int NTHR, int NB, bool GAIN>
+__device__ __forceinline__ void stage_f32_store(int n_tok, int nb, int j0, const f32x4 (&r)[2 * NB], int8_t* sq,
+                                                float* sd, int16_t* ss, float* ssq, int chunk) {
     constexpr int W = NTHR / kWave;
     const int lane = threadIdx.x & (kWave - 1);
     const int total = n_tok * nb;
 #pragma unroll
-    for (int u = 0; u < kStageBatch; ++u) {
+    for (int u = 0; u < NB; ++u) {
         const int j = j0 + u * W;
         if (j < total) {
             const int t = j / nb, b = j - t * nb;
             float vv[4] = {r[u].x, r[u].y, r[u].z, r[u].w};
-            if (x.gain) {
+            if constexpr (GAIN) {
                 const float sq2 = wave_sum(vv[0] * vv[0] + vv[1] * vv[1] + vv[2] * vv[2] + vv[3] * vv[3]);
                 if (lane == 0) ssq[t * nb + b] = sq2;
-                vv[0] = vv[0] * r[kStageBatch + u].x;
-                vv[1] = vv[1] * r[kStageBatch + u].y;
-                vv[2] = vv[2] * r[kStageBatch + u].z;
-                vv[3] = vv[3] * r[kStageBatch + u].w;
+                vv[0] = vv[0] * r[NB + u].x;
+                vv[1] = vv[1] * r[NB + u].y;
+                vv[2] = vv[2] * r[NB + u].z;
+                vv[3] = vv[3] * r[NB + u].w;
             }
             quant_block_wave(vv, lane, sq + t * chunk + b * 256, sd + t * (chunk / 256) + b,
                              ss + t * (chunk / 16) + b * 16);
@@ -321,17 +322,18 @@ __device__ __forceinline__ void stage_f32_store(const XIn& x, int n_tok, int nb,
 }
 #pragma clang fp contract(on)
 
-template <int NTHR>
+// Stages a pass whose first batch (blocks wave, wave + W, ...) is already loaded.
+template <int NTHR, int NB, bool GAIN>
 __device__ __forceinline__ void stage_f32(const XIn& x, int n_tok, int c0, int nb, int8_t* sq, float* sd, int16_t* ss,
-                                          float* ssq, int chunk, const StageF32Regs& first) {
+                                          float* ssq, int chunk, const f32x4 (&first)[2 * NB]) {
     constexpr int W = NTHR / kWave;
     const int wave = threadIdx.x / kWave;
     const int total = n_tok * nb;
-    stage_f32_store<NTHR>(x, n_tok, nb, wave, first, sq, sd, ss, ssq, chunk);
-    for (int j0 = wave + kStageBatch * W; j0 < total; j0 += kStageBatch * W) {
-        StageF32Regs r;
-        stage_f32_load<NTHR>(x, n_tok, c0, nb, j0, r);
-        stage_f32_store<NTHR>(x, n_tok, nb, j0, r, sq, sd, ss, ssq, chunk);
+    stage_f32_store<NTHR, NB, GAIN>(n_tok, nb, wave, first, sq, sd, ss, ssq, chunk);
+    for (int j0 = wave + NB * W; j0 < total; j0 += NB * W) {
+        f32x4 r[2 * NB];
+        stage_f32_load<NTHR, NB, GAIN>(x, n_tok, c0, nb, j0, r);
+        stage_f32_store<NTHR, NB, GAIN>(n_tok, nb, j0, r, sq, sd, ss, ssq, chunk);
     }
 }
 
@@ -772,7 +774,7 @@ __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, f
 #define JFH_MM_WAVES 8
 #endif
 #ifndef JFH_MM_DEPTH
-#define JFH_MM_DEPTH 3
+#define JFH_MM_DEPTH 2
 #endif
 #ifndef JFH_MM_MIN_WGS
 #define JFH_MM_MIN_WGS 1
@@ -786,9 +788,15 @@ struct MmGeom {
     int32_t chunk;  // K values staged per pass (multiple of 256)
 };
 
-// A8: the activations arrive pre-quantized (a.xq), else as float rows (a.x).
-template <uint32_t TYPE, int NT, bool A8>
+// Kinds of matmul input: pre-quantized rows (a.xq), float rows RMS-normalized
+// with a gain in the prologue (a.x with a.x.gain), plain float rows (a.x).
+enum MmInput : int { kInAct8 = 0, kInNormed = 1, kInFloat = 2 };
+
+template <uint32_t TYPE, int NT, int IN>
 __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, MmGeom geo) {
+    constexpr bool A8 = IN == kInAct8;
+    constexpr bool GAIN = IN == kInNormed;
+    constexpr int NB = GAIN ? kStageBatch : kStageBatchFloat;  // blocks per wave of a float staging batch
     using T = Tile<TYPE>;
     using Regs = typename T::Regs;
     constexpr int W = kMmWaves;
@@ -855,10 +863,10 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
     };
     // the first staging batch is requested before the weights (loads complete
     // in issue order, so the activations do not wait behind weight tiles)
-    StageF32Regs f0;
+    f32x4 f0[2 * NB];
     StageA8Regs q0;
     if constexpr (A8) stage_act8_load<kMmThreads>(a.xq, n_tok, 0, nbcur, 0, q0);
-    else stage_f32_load<kMmThreads>(a.x, n_tok, 0, nbcur, wave, f0);
+    else stage_f32_load<kMmThreads, NB, GAIN>(a.x, n_tok, 0, nbcur, wave, f0);
     prefetch(0);
     // the residual the epilogue adds to is fetched with the first weights
     // (issued unconditionally from a clamped index, so that the compiler's
@@ -875,8 +883,8 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
     if constexpr (A8) {
         stage_act8<kMmThreads>(a.xq, n_tok, 0, nbcur, sq, sd, ss, chunk, q0);
     } else {
-        stage_f32<kMmThreads>(a.x, n_tok, 0, nbcur, sq, sd, ss, ssq, chunk, f0);
-        if (a.x.gain) finish_norm<kMmThreads>(n_tok, nbcur, K, a.x.eps, ssq, sd, rs, chunk);
+        stage_f32<kMmThreads, NB, GAIN>(a.x, n_tok, 0, nbcur, sq, sd, ss, ssq, chunk, f0);
+        if constexpr (GAIN) finish_norm<kMmThreads>(n_tok, nbcur, K, a.x.eps, ssq, sd, rs, chunk);
     }
 
     for (int c0b = 0;;) {
@@ -927,11 +935,11 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
             __syncthreads();  // every wave is done with the previous pass's activations
             stage_act8<kMmThreads>(a.xq, n_tok, c0b * 256, nbcur, sq, sd, ss, chunk, qn);
         } else {
-            StageF32Regs fn;
-            stage_f32_load<kMmThreads>(a.x, n_tok, c0b * 256, nbcur, wave, fn);
+            f32x4 fn[2 * NB];
+            stage_f32_load<kMmThreads, NB, GAIN>(a.x, n_tok, c0b * 256, nbcur, wave, fn);
             prefetch(c0b);
             __syncthreads();
-            stage_f32<kMmThreads>(a.x, n_tok, c0b * 256, nbcur, sq, sd, ss, ssq, chunk, fn);
+            stage_f32<kMmThreads, NB, GAIN>(a.x, n_tok, c0b * 256, nbcur, sq, sd, ss, ssq, chunk, fn);
         }
     }
     __syncthreads();
@@ -1356,12 +1364,12 @@ void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStre
 // values; either way every row's partial sums are added in the same order
 // for 1 and for 8 tokens, so a draft-verify step reproduces serial decode bit
 // for bit. The per-wave row partials take at most kMmPartBytes of LDS, and
-// the row groups per work-group aim at kMmTargetWgs work-groups.
+// the row groups per work-group follow from kMmTargetWgs (mm_geom).
 #ifndef JFH_MM_CHUNK
 #define JFH_MM_CHUNK 8192
 #endif
 #ifndef JFH_MM_TARGET_WGS
-#define JFH_MM_TARGET_WGS 512
+#define JFH_MM_TARGET_WGS 256
 #endif
 constexpr int kMmChunk = JFH_MM_CHUNK;
 constexpr int kMmPartBytes = 65536;
@@ -1379,7 +1387,11 @@ MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds) {
     static_assert(kMmChunk % (256 * kMmWaves) == 0, "a chunk must hold whole rounds of the waves' tiles");
     const int K = static_cast<int>(a.mat.cols);
     const int n_rg = (static_cast<int>(a.mat.rows) + 15) / 16;
-    int rgw = (n_rg + kMmTargetWgs - 1) / kMmTargetWgs;
+    // Up to 2 x kMmTargetWgs row groups: one work-group per CU (a few CUs
+    // with two work-groups would set the kernel's time); larger matrices: two
+    // work-groups per CU.
+    const int wgs = n_rg <= 2 * kMmTargetWgs ? kMmTargetWgs : 2 * kMmTargetWgs;
+    int rgw = (n_rg + wgs - 1) / wgs;
     const int cap = kMmPartBytes / (kMmWaves * 64 * nt * 4);
     if (rgw > cap) rgw = cap;
     if (rgw < 1) rgw = 1;
@@ -1405,8 +1417,9 @@ void mm(const GemvArgs& a, hipStream_t stream) {
     const MmGeom g = mm_geom(a, NT, lds);
     const int n_rg = (static_cast<int>(a.mat.rows) + 15) / 16;
     const int grid = (n_rg + g.rgw - 1) / g.rgw;
-    if (a.xq.q != nullptr) launch(k_mm<TYPE, NT, true>, dim3(grid), dim3(kMmThreads), lds, stream, a, g);
-    else launch(k_mm<TYPE, NT, false>, dim3(grid), dim3(kMmThreads), lds, stream, a, g);
+    if (a.xq.q != nullptr) launch(k_mm<TYPE, NT, kInAct8>, dim3(grid), dim3(kMmThreads), lds, stream, a, g);
+    else if (a.x.gain != nullptr) launch(k_mm<TYPE, NT, kInNormed>, dim3(grid), dim3(kMmThreads), lds, stream, a, g);
+    else launch(k_mm<TYPE, NT, kInFloat>, dim3(grid), dim3(kMmThreads), lds, stream, a, g);
     check(hipGetLastError(), "matmul launch");
 }
 
