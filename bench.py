@@ -144,7 +144,9 @@ def main() -> int:
     verify_bytes = sum(p["bytes"] for p in vprof)
 
     cpu = None
+    parity = None
     if not args.no_cpu:
+        parity = parity_sample(engine, model, cfg, args)
         cpu = cpu_baseline(model, cfg, context, args)
 
     line = {
@@ -187,6 +189,7 @@ def main() -> int:
             "launch_bytes": round(per_launch_bytes),
         },
         "cpu_baseline": cpu,
+        "parity": parity,
         "kernels": [{"kernel": p["kernel"], "launches": p["launches"], "us_per_step": round(p["ms"] * 1e3, 1),
                      "bytes_per_step": round(p["bytes"])} for p in prof],
     }
@@ -238,6 +241,79 @@ def traffic_per_launch(workload: str, kernel: str):
         if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
             return int(parts[2])
     return None
+
+
+PARITY_NRMSE = 5e-3   # the GPU tests' logits tolerance vs the CPU oracle (shallow models)
+PARITY_COSINE = 0.9995
+REFERENCE_NRMSE = 0.025  # the reference's logit gates (tools/bench/native_engine_matrix.py:341-342)
+REFERENCE_COSINE = 0.999
+
+
+def parity_sample(engine, model, cfg, args, prompt_len: int = 12, steps: int = 10):
+    """Agreement of the engine with the CPU oracle on the benchmarked model:
+    logits error, greedy-token agreement over a teacher-forced decode, and
+    accepted-draft-length agreement of verify steps whose drafts are the
+    oracle's own continuation with the first `a` tokens kept (a = 0..k)."""
+    import oracle as jo
+
+    t0 = time.perf_counter()
+    threads = args.cpu_threads or min(16, os.cpu_count() or 8)
+    k = args.draft
+    rng = np.random.default_rng(args.seed + 7)
+    prompt = [int(t) for t in rng.integers(0, cfg.n_vocab, prompt_len)]
+    om = jo.OracleModel.from_model(model)
+    cap = prompt_len + steps + 2 * (k + 2)
+    ref = om.session(cap, jo.MODE_Q8, threads)
+    gpu = engine.create_session(cap)
+    nrmse, cosine, agree, total = [], [], 0, 0
+    g_tok, g_lg = gpu.prefill_greedy(prompt, logits=True)
+    r_ids, r_lg = ref.forward(prompt, 1)
+    tok = int(r_ids[0])
+    for step in range(steps + 1):
+        nrmse.append(jo.nrmse(r_lg[0], g_lg))
+        cosine.append(jo.cosine(r_lg[0], g_lg))
+        agree += int(g_tok == tok)
+        total += 1
+        if step == steps:
+            break
+        g_tok, g_lg = gpu.decode_greedy(tok, logits=True)
+        r_ids, r_lg = ref.forward([tok], 1)
+        tok = int(r_ids[0])
+    # the oracle's greedy continuation from here, then rewind both sessions
+    cont = [tok]
+    for _ in range(k):
+        ids, _ = ref.forward([cont[-1]], 1)
+        cont.append(int(ids[0]))
+    ref.rollback(k)
+    acc_agree = 0
+    for a in range(k + 1):
+        draft = cont[1:1 + a] + [(cont[1 + i] + 1 + i) % cfg.n_vocab for i in range(a, k)]
+        rows = [cont[0]] + draft
+        g_ids, g_acc = gpu.verify(rows)
+        r_ids, _ = ref.forward(rows, len(rows))
+        r_acc = 0
+        while r_acc < k and int(r_ids[r_acc]) == rows[1 + r_acc]:
+            r_acc += 1
+        acc_agree += int(g_acc == r_acc)
+        gpu.rollback(len(rows))
+        ref.rollback(len(rows))
+    ref.close()
+    out = {
+        "reference": "CPU oracle (same weights, same int8 activation rule), teacher-forced on the oracle's tokens",
+        "tokens_compared": total,
+        "greedy_agreement": round(agree / total, 4),
+        "accepted_length_agreement": round(acc_agree / (k + 1), 4),
+        "verify_steps_compared": k + 1,
+        "logits_nrmse_max": float(f"{max(nrmse):.3g}"),
+        "logits_cosine_min": float(f"{min(cosine):.7f}"),
+        "tolerance": {"nrmse": PARITY_NRMSE, "cosine": PARITY_COSINE},
+        "within_tolerance": bool(max(nrmse) <= PARITY_NRMSE and min(cosine) >= PARITY_COSINE),
+        "reference_gates": {"nrmse": REFERENCE_NRMSE, "cosine": REFERENCE_COSINE},
+        "within_reference_gates": bool(max(nrmse) <= REFERENCE_NRMSE and min(cosine) >= REFERENCE_COSINE),
+    }
+    log(f"parity vs CPU oracle: greedy {agree}/{total}, accepted lengths {acc_agree}/{k + 1}, "
+        f"nrmse max {max(nrmse):.2e}, cosine min {min(cosine):.6f} ({time.perf_counter() - t0:.1f}s)")
+    return out
 
 
 def cpu_baseline(model, cfg, context, args):

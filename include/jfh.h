@@ -232,6 +232,15 @@ jfh_status jfh_engine_dequantize(jfh_engine * engine, const char * tensor, uint3
                                  float * out);
 jfh_status jfh_engine_matmul(jfh_engine * engine, const char * tensor, const float * x, uint32_t n_tok, float * y);
 
+/* Parity entry points for the F16 KV cache (no reference counterpart: the
+ * reference's cache lives in GGML tensors, qwen2_architecture.cpp:1056-1092).
+ * read_kv copies positions [0, n) of one layer out of a session, layout
+ * [kv_head][n][head_dim]; import_kv writes positions [0, n) of every layer,
+ * layout [layer][kv_head][n][head_dim], and leaves the session at position n
+ * as after a prefill of n tokens (a long context without running it). */
+jfh_status jfh_session_read_kv(const jfh_session * session, uint32_t layer, uint32_t n, uint16_t * k, uint16_t * v);
+jfh_status jfh_session_import_kv(jfh_session * session, uint32_t n, const uint16_t * k, const uint16_t * v);
+
 /* Device time of `iterations` back-to-back decode steps (ms, HIP events on the
  * engine stream) after `warmup` untimed ones; the session is rolled back after
  * each step, so every step runs at the same position. */

@@ -8,7 +8,8 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char, c_char_p, c_double, c_float, c_int32, c_size_t, c_uint8, c_uint32, c_uint64, c_void_p
+from ctypes import (POINTER, c_char, c_char_p, c_double, c_float, c_int32, c_size_t, c_uint8, c_uint16, c_uint32,
+                    c_uint64, c_void_p)
 
 PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
 LIBRARY_PATH = os.path.join(PACKAGE_DIR, "libjfh.so")
@@ -124,6 +125,8 @@ SIGNATURES = {
                                        POINTER(c_int32), POINTER(c_uint32)]),
     "jfh_engine_dequantize": (Status, [c_void_p, c_char_p, c_uint32, c_uint32, POINTER(c_float)]),
     "jfh_engine_matmul": (Status, [c_void_p, c_char_p, POINTER(c_float), c_uint32, POINTER(c_float)]),
+    "jfh_session_read_kv": (Status, [c_void_p, c_uint32, c_uint32, POINTER(c_uint16), POINTER(c_uint16)]),
+    "jfh_session_import_kv": (Status, [c_void_p, c_uint32, POINTER(c_uint16), POINTER(c_uint16)]),
     "jfh_session_time_steps": (Status, [c_void_p, POINTER(c_int32), c_uint32, c_uint32, c_uint32, c_uint32,
                                         POINTER(c_double)]),
     "jfh_prompt_lookup_propose": (Status, [POINTER(c_uint32), c_size_t, c_uint32, c_uint32, c_uint32,

@@ -461,6 +461,20 @@ jfh_status jfh_engine_matmul(jfh_engine* engine, const char* tensor, const float
     });
 }
 
+jfh_status jfh_session_read_kv(const jfh_session* session, uint32_t layer, uint32_t n, uint16_t* k, uint16_t* v) {
+    return guarded([&] {
+        require(session && k && v, "cache read arguments are required");
+        session->owner->engine->read_kv(*session->session, layer, n, k, v);
+    });
+}
+
+jfh_status jfh_session_import_kv(jfh_session* session, uint32_t n, const uint16_t* k, const uint16_t* v) {
+    return guarded([&] {
+        require(session && k && v, "cache import arguments are required");
+        session->owner->engine->import_kv(*session->session, n, k, v);
+    });
+}
+
 jfh_status jfh_session_time_steps(jfh_session* session, const int32_t* tokens, uint32_t n, uint32_t all_logits,
                                   uint32_t warmup, uint32_t iterations, double* ms_per_step) {
     return guarded([&] {

@@ -619,6 +619,38 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
     }
 }
 
+void Engine::read_kv(const Session& s, uint32_t layer, uint32_t n, uint16_t* k, uint16_t* v) {
+    std::lock_guard lock(mutex_);
+    const ModelParams& p = params_;
+    if (layer >= p.n_layer || n > s.position_) fail(Status::InvalidArgument, "cache rows are outside the session");
+    hip_check(hipStreamSynchronize(stream_), "synchronize before cache read");
+    const size_t hd = p.head_dim, rows = static_cast<size_t>(n) * hd;
+    for (uint32_t h = 0; h < p.n_head_kv; ++h) {
+        const size_t src = (static_cast<size_t>(layer) * p.n_head_kv + h) * s.capacity_ * hd;
+        hip_check(hipMemcpy(k + h * rows, s.k_ + src, rows * sizeof(uint16_t), hipMemcpyDeviceToHost), "read K cache");
+        hip_check(hipMemcpy(v + h * rows, s.v_ + src, rows * sizeof(uint16_t), hipMemcpyDeviceToHost), "read V cache");
+    }
+}
+
+void Engine::import_kv(Session& s, uint32_t n, const uint16_t* k, const uint16_t* v) {
+    std::lock_guard lock(mutex_);
+    const ModelParams& p = params_;
+    if (n == 0 || n > s.capacity_) fail(Status::InvalidArgument, "imported cache rows exceed the session capacity");
+    hip_check(hipStreamSynchronize(stream_), "synchronize before cache import");
+    const size_t hd = p.head_dim, rows = static_cast<size_t>(n) * hd;
+    for (uint32_t l = 0; l < p.n_layer; ++l) {
+        for (uint32_t h = 0; h < p.n_head_kv; ++h) {
+            const size_t idx = static_cast<size_t>(l) * p.n_head_kv + h;
+            hip_check(hipMemcpy(s.k_ + idx * s.capacity_ * hd, k + idx * rows, rows * sizeof(uint16_t),
+                                hipMemcpyHostToDevice), "import K cache");
+            hip_check(hipMemcpy(s.v_ + idx * s.capacity_ * hd, v + idx * rows, rows * sizeof(uint16_t),
+                                hipMemcpyHostToDevice), "import V cache");
+        }
+    }
+    s.position_ = n;
+    s.prefill_position_ = n;
+}
+
 std::vector<KernelStat> Engine::profile(const std::vector<SeqStep>& steps, uint32_t iterations) {
     std::vector<ProfEvent> events;
     {

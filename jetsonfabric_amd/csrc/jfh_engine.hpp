@@ -108,6 +108,13 @@ public:
     // launch; sessions are restored to their starting positions.
     std::vector<KernelStat> profile(const std::vector<SeqStep>& steps, uint32_t iterations);
 
+    // Parity entry points: K/V rows [0, n) of one layer out of a session
+    // ([kv_head][n][head_dim] f16), and of every layer ([layer][kv_head][n]
+    // [head_dim]) into one, which then stands at position n as after a
+    // prefill of n tokens.
+    void read_kv(const Session& s, uint32_t layer, uint32_t n, uint16_t* k, uint16_t* v);
+    void import_kv(Session& s, uint32_t n, const uint16_t* k, const uint16_t* v);
+
     uint32_t max_prefill_chunk() const { return prefill_chunk_; }
 
 private:

@@ -287,6 +287,25 @@ class NativeSession:
     def rollback(self, token_count: int) -> None:
         check(library().jfh_session_rollback(self._h, token_count))
 
+    def read_kv(self, layer: int, n: int):
+        """K and V cache rows [0, n) of one layer as f16 bits, [kv_head][n][head_dim]."""
+        c = self._engine._config
+        k = np.zeros((c.n_head_kv, n, c.head_dim), dtype=np.uint16)
+        v = np.zeros_like(k)
+        u16 = ctypes.POINTER(ctypes.c_uint16)
+        check(library().jfh_session_read_kv(self._h, layer, n, k.ctypes.data_as(u16), v.ctypes.data_as(u16)))
+        return k, v
+
+    def import_kv(self, k: np.ndarray, v: np.ndarray) -> None:
+        """Writes cache rows [0, n) of every layer ([layer][kv_head][n][head_dim] f16 bits); the
+        session then stands at position n as after a prefill of n tokens."""
+        k = np.ascontiguousarray(k, dtype=np.uint16)
+        v = np.ascontiguousarray(v, dtype=np.uint16)
+        if k.shape != v.shape or k.ndim != 4:
+            raise ValueError("k and v must be [layer][kv_head][n][head_dim]")
+        u16 = ctypes.POINTER(ctypes.c_uint16)
+        check(library().jfh_session_import_kv(self._h, k.shape[2], k.ctypes.data_as(u16), v.ctypes.data_as(u16)))
+
     def time_steps(self, tokens: Sequence[int], iterations: int, warmup: int = 2, all_logits: bool | None = None) -> float:
         """Mean device ms per step of `tokens` at the current position (rolled back after each step)."""
         ms = ctypes.c_double()
