@@ -77,7 +77,7 @@ def main() -> int:
 
     rng = np.random.default_rng(args.seed)
     prompt = [int(t) for t in rng.integers(0, cfg.n_vocab, context)]
-    capacity = context + args.warmup + args.steps + k + 8
+    capacity = context + args.warmup + args.steps + k + 8 + 64
     session = engine.create_session(capacity)
     t0 = time.perf_counter()
     tok = session.prefill_greedy(prompt)
@@ -142,6 +142,10 @@ def main() -> int:
         f"-> {achieved:.0f} GB/s")
     vprof = session.profile_step([cont[0]] + cont[1:1 + k], iterations=args.profile_iters)
     verify_bytes = sum(p["bytes"] for p in vprof)
+    log("verify profile (ms/step): " + ", ".join(f"{p['kernel']} {p['ms']:.3f}" for p in vprof[:8]))
+    chunk = [int(t) for t in rng.integers(0, cfg.n_vocab, 64)]
+    pprof = session.profile_step(chunk, iterations=1, all_logits=False)
+    log("prefill chunk (64 rows) profile (ms): " + ", ".join(f"{p['kernel']} {p['ms']:.3f}" for p in pprof[:8]))
 
     cpu = None
     parity = None

@@ -38,9 +38,10 @@ bool quantized(uint32_t type) { return type == kQ4_K || type == kQ6_K || type ==
 }  // namespace
 
 // ------------------------------------------------------------------ Session
-Session::Session(Engine* engine, uint32_t capacity) : engine_(engine), capacity_(capacity) {
+Session::Session(Engine* engine, uint32_t capacity)
+    : engine_(engine), capacity_(capacity), stride_((std::max<uint32_t>(capacity, 16) + 15) / 16 * 16) {
     const ModelParams& p = engine->params();
-    const size_t elems = static_cast<size_t>(p.n_layer) * p.n_head_kv * capacity * p.head_dim;
+    const size_t elems = static_cast<size_t>(p.n_layer) * p.n_head_kv * stride_ * p.head_dim;
     kv_bytes_ = 2 * elems * sizeof(uint16_t);
     hip_check(hipMalloc(&k_, elems * sizeof(uint16_t)), "allocate K cache");
     if (hipMalloc(&v_, elems * sizeof(uint16_t)) != hipSuccess) {
@@ -327,7 +328,8 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
     if (p.head_dim % 2 != 0 || p.head_dim > 128) fail(Status::InvalidArgument, "unsupported head dimension");
     if (p.n_embd % 4 != 0) fail(Status::InvalidArgument, "hidden size must be a multiple of 4");
     const uint32_t G = p.n_head / p.n_head_kv;
-    prefill_chunk_ = std::max<uint32_t>(1, std::min<uint32_t>(8, 64 / G));
+    const uint32_t attn_rows = static_cast<uint32_t>(gpu::attention_max_rows(static_cast<int32_t>(p.head_dim)));
+    prefill_chunk_ = std::max<uint32_t>(1, std::min<uint32_t>(gpu::kMaxRows, attn_rows / G));
 
     if (p.head_dim % 4 != 0) fail(Status::InvalidArgument, "head dimension must be a multiple of 4");
     if (p.n_ff % gpu::kGluGroup != 0) fail(Status::InvalidArgument, "feed-forward length must be a multiple of 8");
@@ -427,6 +429,9 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
     };
     if (quantized(layers_[0].o->mat.type) && Hq % 256 == 0) xq_attn_ = act8(Hq);
     if (quantized(layers_[0].down->mat.type) && F % 256 == 0) xq_ffn_ = act8(F);
+    if ((quantized(layers_[0].qkv->mat.type) || quantized(layers_[0].gate_up->mat.type)) && H % 256 == 0) {
+        xq_norm_ = act8(H);
+    }
     step_dev_ = static_cast<gpu::StepDev*>(device_alloc(sizeof(gpu::StepDev)));
     out_dev_ = static_cast<gpu::StepOut*>(device_alloc(sizeof(gpu::StepOut)));
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&step_host_), sizeof(gpu::StepDev), hipHostMallocDefault),
@@ -545,13 +550,37 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
     timed("k_embed", n * H * 4.0 + n * static_cast<double>(row_bytes(embd_->mat.type, H)), [&] {
         gpu::launch_embed(embd_->mat, step_dev_, h_, n_rows, H, best_, gpu::kMaxRows, s);
     });
+    // Steps with more rows than one 8-row group run Q4_K matrices on matrix
+    // cores with int8 rows quantized once per step (same codes as the decode
+    // prologue, same results per row).
+    const bool wide = n_rows > 8 && n_rows <= gpu::kWideRows;
+    auto wide_ok = [&](const gpu::DMat& m) { return wide && gpu::wide_matmul_supported(m.type); };
+    auto matmul = [&](gpu::GemvArgs& a, const char* role) {
+        if (wide_ok(a.mat) && a.xq.q != nullptr) {
+            timed(std::string("k_mm_wide_q4k:") + role, gemv_bytes(a), [&] { gpu::launch_gemv_wide(a, s); });
+        } else {
+            timed(gemv_label(a) + ":" + role, gemv_bytes(a), [&] { gpu::launch_gemv(a, s); });
+        }
+    };
+    // Normalized rows of multi-row steps are quantized once into xq_norm_
+    // (the same codes the matmul prologue would stage): a draft-verify group
+    // then stages int8 rows instead of normalizing them in every work-group.
+    auto normed = [&](gpu::GemvArgs& a, const float* gain) {
+        if (n_rows > 1 && quantized(a.mat.type) && xq_norm_.q) {
+            timed("k_quantize_norm", n * H * 9.1,
+                  [&] { gpu::launch_quantize_norm(h_, H, nullptr, gain, p.rms_eps, n_rows, xq_norm_, s); });
+            a.xq = xq_norm_;
+        } else {
+            a.x = {h_, H, nullptr, gain, p.rms_eps};
+        }
+    };
     for (uint32_t l = 0; l < p.n_layer; ++l) {
         const Layer& L = layers_[l];
         gpu::GemvArgs qkv;
         qkv.mat = L.qkv->mat;
         qkv.mode = gpu::kQKV;
         qkv.n_tok = n_rows;
-        qkv.x = {h_, H, nullptr, L.attn_norm, p.rms_eps};
+        normed(qkv, L.attn_norm);
         qkv.qkv.step = step_dev_;
         qkv.qkv.rope = rope_;
         qkv.qkv.q = q_;
@@ -559,7 +588,7 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         qkv.qkv.n_head = static_cast<int32_t>(p.n_head);
         qkv.qkv.n_head_kv = static_cast<int32_t>(p.n_head_kv);
         qkv.qkv.head_dim = static_cast<int32_t>(p.head_dim);
-        timed(gemv_label(qkv) + ":qkv", gemv_bytes(qkv), [&] { gpu::launch_gemv(qkv, s); });
+        matmul(qkv, "qkv");
         timed("k_attention", attn_kv_bytes_ + n * Hq * 4.0, [&] {
             gpu::launch_attention(q_, step_dev_, max_len, n_seq, static_cast<int32_t>(l), static_cast<int32_t>(p.n_head),
                                   static_cast<int32_t>(p.n_head_kv), static_cast<int32_t>(p.head_dim), splits_, partial_, s);
@@ -576,15 +605,15 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         else o.x = {attn_, Hq, nullptr, nullptr, 0.0F};
         o.y = h_;
         o.y_stride = H;
-        timed(gemv_label(o) + ":attn_output", gemv_bytes(o), [&] { gpu::launch_gemv(o, s); });
+        matmul(o, "attn_output");
         gpu::GemvArgs gu;
         gu.mat = L.gate_up->mat;
         gu.mode = gpu::kSwiGLU;
         gu.n_tok = n_rows;
-        gu.x = {h_, H, nullptr, L.ffn_norm, p.rms_eps};
+        normed(gu, L.ffn_norm);
         gu.y = ffn_;
         gu.y_stride = F;
-        timed(gemv_label(gu) + ":ffn_gate_up", gemv_bytes(gu), [&] { gpu::launch_gemv(gu, s); });
+        matmul(gu, "ffn_gate_up");
         gpu::GemvArgs dn;
         dn.mat = L.down->mat;
         dn.mode = gpu::kAdd;
@@ -600,7 +629,7 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         }
         dn.y = h_;
         dn.y_stride = H;
-        timed(gemv_label(dn) + ":ffn_down", gemv_bytes(dn), [&] { gpu::launch_gemv(dn, s); });
+        matmul(dn, "ffn_down");
     }
     if (n_out > 0) {
         gpu::GemvArgs head;
@@ -609,7 +638,15 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         head.n_tok = n_out;
         const int32_t* out_rows =
             reinterpret_cast<const int32_t*>(reinterpret_cast<const char*>(step_dev_) + offsetof(gpu::StepDev, out_row));
-        head.x = {h_, H, out_rows, output_norm_, p.rms_eps};
+        if (n_out > 1 && quantized(head.mat.type) && xq_norm_.q) {
+            // several logits rows (draft verify, batches): normalized and quantized once
+            timed("k_quantize_norm", n_out * H * 9.1, [&] {
+                gpu::launch_quantize_norm(h_, H, out_rows, output_norm_, p.rms_eps, n_out, xq_norm_, s);
+            });
+            head.xq = xq_norm_;
+        } else {
+            head.x = {h_, H, out_rows, output_norm_, p.rms_eps};
+        }
         head.y = logits_;
         head.y_stride = static_cast<int32_t>(p.n_vocab);
         head.best = best_;
@@ -624,11 +661,17 @@ void Engine::read_kv(const Session& s, uint32_t layer, uint32_t n, uint16_t* k, 
     const ModelParams& p = params_;
     if (layer >= p.n_layer || n > s.position_) fail(Status::InvalidArgument, "cache rows are outside the session");
     hip_check(hipStreamSynchronize(stream_), "synchronize before cache read");
-    const size_t hd = p.head_dim, rows = static_cast<size_t>(n) * hd;
+    const size_t hd = p.head_dim, rows = static_cast<size_t>(n) * hd, stride = s.stride_;
+    std::vector<uint16_t> vt(rows);
     for (uint32_t h = 0; h < p.n_head_kv; ++h) {
-        const size_t src = (static_cast<size_t>(layer) * p.n_head_kv + h) * s.capacity_ * hd;
-        hip_check(hipMemcpy(k + h * rows, s.k_ + src, rows * sizeof(uint16_t), hipMemcpyDeviceToHost), "read K cache");
-        hip_check(hipMemcpy(v + h * rows, s.v_ + src, rows * sizeof(uint16_t), hipMemcpyDeviceToHost), "read V cache");
+        const size_t base = (static_cast<size_t>(layer) * p.n_head_kv + h) * stride * hd;
+        hip_check(hipMemcpy(k + h * rows, s.k_ + base, rows * sizeof(uint16_t), hipMemcpyDeviceToHost), "read K cache");
+        // V^T [dim][stride] -> [position][dim]
+        hip_check(hipMemcpy2D(vt.data(), n * sizeof(uint16_t), s.v_ + base, stride * sizeof(uint16_t),
+                              n * sizeof(uint16_t), hd, hipMemcpyDeviceToHost), "read V cache");
+        for (size_t d = 0; d < hd; ++d) {
+            for (size_t i = 0; i < n; ++i) v[h * rows + i * hd + d] = vt[d * n + i];
+        }
     }
 }
 
@@ -637,14 +680,18 @@ void Engine::import_kv(Session& s, uint32_t n, const uint16_t* k, const uint16_t
     const ModelParams& p = params_;
     if (n == 0 || n > s.capacity_) fail(Status::InvalidArgument, "imported cache rows exceed the session capacity");
     hip_check(hipStreamSynchronize(stream_), "synchronize before cache import");
-    const size_t hd = p.head_dim, rows = static_cast<size_t>(n) * hd;
+    const size_t hd = p.head_dim, rows = static_cast<size_t>(n) * hd, stride = s.stride_;
+    std::vector<uint16_t> vt(rows);
     for (uint32_t l = 0; l < p.n_layer; ++l) {
         for (uint32_t h = 0; h < p.n_head_kv; ++h) {
             const size_t idx = static_cast<size_t>(l) * p.n_head_kv + h;
-            hip_check(hipMemcpy(s.k_ + idx * s.capacity_ * hd, k + idx * rows, rows * sizeof(uint16_t),
+            hip_check(hipMemcpy(s.k_ + idx * stride * hd, k + idx * rows, rows * sizeof(uint16_t),
                                 hipMemcpyHostToDevice), "import K cache");
-            hip_check(hipMemcpy(s.v_ + idx * s.capacity_ * hd, v + idx * rows, rows * sizeof(uint16_t),
-                                hipMemcpyHostToDevice), "import V cache");
+            for (size_t i = 0; i < n; ++i) {
+                for (size_t d = 0; d < hd; ++d) vt[d * n + i] = v[idx * rows + i * hd + d];
+            }
+            hip_check(hipMemcpy2D(s.v_ + idx * stride * hd, stride * sizeof(uint16_t), vt.data(), n * sizeof(uint16_t),
+                                  n * sizeof(uint16_t), hd, hipMemcpyHostToDevice), "import V cache");
         }
     }
     s.position_ = n;
@@ -725,11 +772,13 @@ void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int
         if (static_cast<uint64_t>(s->position_) + st.n > s->capacity_) {
             fail(Status::InvalidArgument, "native Qwen2 step is outside session capacity");
         }
-        if (st.n * G > 64) fail(Status::InvalidArgument, "too many rows for one sequence step");
+        if (st.n * G > static_cast<uint32_t>(gpu::attention_max_rows(static_cast<int32_t>(p.head_dim)))) {
+            fail(Status::InvalidArgument, "too many rows for one sequence step");
+        }
         if (rows + static_cast<int32_t>(st.n) > gpu::kMaxRows) fail(Status::InvalidArgument, "too many token rows in one step");
         sd.seqs[si].k = s->k_;
         sd.seqs[si].v = s->v_;
-        sd.seqs[si].capacity = static_cast<int32_t>(s->capacity_);
+        sd.seqs[si].capacity = static_cast<int32_t>(s->stride_);
         sd.seqs[si].row0 = rows;
         sd.seqs[si].len = static_cast<int32_t>(st.n);
         sd.seqs[si].pos0 = static_cast<int32_t>(s->position_);
@@ -874,6 +923,15 @@ void Engine::matmul(const std::string& name, const float* x_host, uint32_t n_tok
         fail(Status::OutOfMemory, "allocate matmul output");
     }
     std::vector<float> full(static_cast<size_t>(n_tok) * m.rows);
+    // more than one 8-row group of a wide-capable type: quantized once, then the matrix-core path (as in a step)
+    const bool wide = n_tok > 8 && gpu::wide_matmul_supported(m.type) && m.cols % 256 == 0;
+    gpu::Act8 xq;
+    uint8_t* xq_mem = nullptr;
+    auto release = [&] {
+        (void) hipFree(x);
+        (void) hipFree(y);
+        if (xq_mem) (void) hipFree(xq_mem);
+    };
     try {
         hip_check(hipMemcpyAsync(x, x_host, x_bytes, hipMemcpyHostToDevice, stream_), "upload activations");
         gpu::GemvArgs a;
@@ -881,19 +939,29 @@ void Engine::matmul(const std::string& name, const float* x_host, uint32_t n_tok
         a.mat.bias = nullptr;
         a.mode = gpu::kStore;
         a.n_tok = static_cast<int32_t>(n_tok);
-        a.x = {x, static_cast<int32_t>(m.cols), nullptr, nullptr, 0.0F};
         a.y = y;
         a.y_stride = static_cast<int32_t>(m.rows);
-        gpu::launch_gemv(a, stream_);
+        if (wide) {
+            const size_t K = m.cols, nq = n_tok * K, nd = n_tok * (K / 256), ns = n_tok * (K / 16);
+            hip_check(hipMalloc(&xq_mem, nq + nd * sizeof(float) + ns * sizeof(int16_t)), "allocate int8 rows");
+            xq.K = static_cast<int32_t>(K);
+            xq.q = reinterpret_cast<int8_t*>(xq_mem);
+            xq.d = reinterpret_cast<float*>(xq_mem + nq);
+            xq.s = reinterpret_cast<int16_t*>(xq_mem + nq + nd * sizeof(float));
+            gpu::launch_quantize(x, static_cast<int32_t>(K), static_cast<int32_t>(n_tok), xq, stream_);
+            a.xq = xq;
+            gpu::launch_gemv_wide(a, stream_);
+        } else {
+            a.x = {x, static_cast<int32_t>(m.cols), nullptr, nullptr, 0.0F};
+            gpu::launch_gemv(a, stream_);
+        }
         hip_check(hipMemcpyAsync(full.data(), y, y_bytes, hipMemcpyDeviceToHost, stream_), "download matmul");
         hip_check(hipStreamSynchronize(stream_), "matmul");
     } catch (...) {
-        (void) hipFree(x);
-        (void) hipFree(y);
+        release();
         throw;
     }
-    (void) hipFree(x);
-    (void) hipFree(y);
+    release();
     for (uint32_t t = 0; t < n_tok; ++t) {
         for (uint32_t r = 0; r < ref.rows; ++r) {
             y_host[static_cast<size_t>(t) * ref.rows + r] = full[static_cast<size_t>(t) * m.rows + device_row(ref, r)];

@@ -50,10 +50,11 @@ private:
 
     Engine* engine_;
     uint32_t capacity_;
+    uint32_t stride_;  // allocated positions per (layer, kv head): capacity rounded up to 16
     uint32_t position_ = 0;
     uint32_t prefill_position_ = 0;
-    uint16_t* k_ = nullptr;
-    uint16_t* v_ = nullptr;
+    uint16_t* k_ = nullptr;  // [layer][kv head][stride][head_dim]
+    uint16_t* v_ = nullptr;  // [layer][kv head][head_dim][stride] (transposed)
     uint64_t kv_bytes_ = 0;
 };
 
@@ -195,6 +196,8 @@ private:
     // (set when the consuming matrix is quantized)
     gpu::Act8 xq_attn_;
     gpu::Act8 xq_ffn_;
+    // normalized int8 rows of wide steps (the QKV and gate/up inputs)
+    gpu::Act8 xq_norm_;
 
     // captured step graphs keyed by (rows, seqs, outs, store_logits)
     std::map<uint64_t, hipGraphExec_t> graphs_;

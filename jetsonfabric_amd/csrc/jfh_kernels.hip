@@ -12,6 +12,7 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <stdexcept>
 #include <string>
@@ -453,6 +454,14 @@ __device__ __forceinline__ int mul24(int a, int b) { return __mul24(a, b); }
 template <uint32_t TYPE>
 struct Tile;
 
+// A Q4_K tile's share of one lane group (two sub-blocks) for one token:
+// acc + xd * (d * isum - dmin * msum), with the fused products as written.
+// The decode and prefill matmuls both use it, so they round alike.
+__device__ __forceinline__ float q4k_term(float acc, float xd, float d, float dmin, int isum, int msum) {
+    const float t = __builtin_fmaf(d, static_cast<float>(isum), -(dmin * static_cast<float>(msum)));
+    return __builtin_fmaf(xd, t, acc);
+}
+
 // Q4_K: header of row i | codes: the lane's 32 qs bytes (sub-blocks 2g, 2g+1).
 // The lane reads d|dmin and the 8 header bytes that hold its 24-bit scale
 // field (header byte 4 + 3g) starting at the enclosing word.
@@ -499,7 +508,7 @@ struct Tile<11> {
                 const int16_t* s = x.s + t * x.s_stride + 4 * g;
                 const int isum = mul24(sca, da) + mul24(scb, db);
                 const int msum = mul24(ma, s[0] + s[1]) + mul24(mb, s[2] + s[3]);
-                acc[t] += x.d[t * x.d_stride] * (d * static_cast<float>(isum) - dmin * static_cast<float>(msum));
+                acc[t] = q4k_term(acc[t], x.d[t * x.d_stride], d, dmin, isum, msum);
             }
         }
     }
@@ -640,6 +649,8 @@ struct Tile<9> {
     }
 };
 
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ unsigned long long pack_best(float v, uint32_t idx) {
     uint32_t u = __float_as_uint(v);
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -676,8 +687,9 @@ __device__ __forceinline__ void qkv_store(const GemvArgs& a, int t, int gr, floa
     } else {
         const int g = gr - Hq - kv;
         const int head = g / hd, dcol = g % hd;
-        const size_t row = ((static_cast<size_t>(o.layer) * o.n_head_kv + head) * sd.capacity + pos) * hd;
-        as_global(sd.v)[row + dcol] = f2h(va);
+        // V is stored transposed: [layer][kv head][dim][position]
+        const size_t at = ((static_cast<size_t>(o.layer) * o.n_head_kv + head) * hd + dcol) * sd.capacity + pos;
+        as_global(sd.v)[at] = f2h(va);
     }
 }
 #pragma clang fp contract(on)
@@ -966,6 +978,122 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
     gemv_epilogue<kMmThreads>(a, row0, nrows, sum, lv);
 }
 
+// ------------------------------------------------------------------ wide matmul on matrix cores
+// Q4_K x int8 rows for steps of up to kWideRows tokens (prefill chunks,
+// large batches). Work-group
+// = one 16-row group and every token; wave w takes the K tiles w, w + W, ...
+// as the decode matmul does. For each lane group g (values 64 g .. 64 g + 63
+// of a tile, sub-blocks 2 g and 2 g + 1) the integer dots of the 16 rows with
+// 16 tokens at a time come from v_mfma_i32_16x16x32_i8 with lane group g's
+// 8-byte code chunks as the only non-zero B operand, so every product stays
+// within one sub-block. The scale arithmetic per (tile, lane group, token,
+// row) is the decode matmul's (q4k_term), accumulated per wave and lane
+// group in the same tile order and summed over waves, then lane groups, in
+// the same order: every row equals that row computed alone, bit for bit.
+__global__ __launch_bounds__(kMmThreads) void k_mm_wide_q4k(GemvArgs a) {
+    constexpr int W = kMmWaves;
+    constexpr uint32_t TB = tile_bytes(11);
+    __shared__ float red[W][4][16][16];  // [wave][lane group][token][row] of one token tile
+    __shared__ float vals[kWideRows][16];
+    const int K = static_cast<int>(a.mat.cols), nb = K / 256, n_tok = a.n_tok;
+    const int rg = blockIdx.x;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+    const int i = lane & 15, G = lane >> 4;
+    const uint8_t* base = a.mat.data + static_cast<size_t>(rg) * nb * TB;
+    const Act8 xq = a.xq;
+    // one token tile (16 tokens) at a time: the row group's tiles are re-read
+    // from L2 for each, which keeps the accumulators in registers
+#pragma unroll 1
+    for (int tt = 0; tt < (n_tok + 15) / 16; ++tt) {
+        float acc[4][4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[g][j] = 0.0F;
+        }
+        // A operand rows: token 16 tt + i; D fragment tokens: 16 tt + 4 G + j
+        const int8_t* xa_row = xq.q + static_cast<size_t>(min(16 * tt + i, n_tok - 1)) * K + 64 * G;
+        int tok[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) tok[j] = min(16 * tt + 4 * G + j, n_tok - 1);
+        for (int b = wave; b < nb; b += W) {
+            const uint8_t* t = base + static_cast<size_t>(b) * TB;
+            const uint4 hdr = *reinterpret_cast<const uint4*>(t + 16 * i);
+            const uint4 w0 = *reinterpret_cast<const uint4*>(t + 256 + 16 * lane);
+            const uint4 w1 = *reinterpret_cast<const uint4*>(t + 1280 + 16 * lane);
+            long av[2][4];
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) av[p][c] = *reinterpret_cast<const long*>(xa_row + b * 256 + 32 * p + 8 * c);
+            }
+            float xd[4];
+            u32x4 sums[4][2];  // the 16 code sums (int16) of each D token's block
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                xd[j] = xq.d[static_cast<size_t>(tok[j]) * nb + b];
+                const u32x4* sp = reinterpret_cast<const u32x4*>(xq.s + static_cast<size_t>(tok[j]) * (K / 16) + b * 16);
+                sums[j][0] = sp[0];
+                sums[j][1] = sp[1];
+            }
+            const float d = h2f(hdr.x), dmin = h2f(hdr.x >> 16);
+            // row i's 24-bit fields sc 2g | sc 2g+1 | m 2g | m 2g+1 of the four lane groups
+            const uint32_t F[4] = {hdr.y & 0xFFFFFFu, (hdr.y >> 24) | ((hdr.z & 0xFFFFu) << 8),
+                                   (hdr.z >> 16) | ((hdr.w & 0xFFu) << 16), hdr.w >> 8};
+            const uint32_t pw[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t f = F[g];
+                const int sca = f & 63, scb = (f >> 6) & 63, ma = (f >> 12) & 63, mb = (f >> 18) & 63;
+                i32x4 da = {0, 0, 0, 0}, db = {0, 0, 0, 0};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    // lane group g's 8 codes of chunk c (low nibbles: sub-block 2g, high: 2g + 1); zero elsewhere
+                    const uint32_t l0 = pw[2 * c] & 0x0F0F0F0Fu, l1 = pw[2 * c + 1] & 0x0F0F0F0Fu;
+                    const uint32_t h0 = (pw[2 * c] >> 4) & 0x0F0F0F0Fu, h1 = (pw[2 * c + 1] >> 4) & 0x0F0F0F0Fu;
+                    const long bl = G == g ? static_cast<long>(static_cast<uint64_t>(l0) | (static_cast<uint64_t>(l1) << 32)) : 0L;
+                    const long bh = G == g ? static_cast<long>(static_cast<uint64_t>(h0) | (static_cast<uint64_t>(h1) << 32)) : 0L;
+                    da = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[0][c], bl, da, 0, 0, 0);
+                    db = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[1][c], bh, db, 0, 0, 0);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    // 16-value sums 4g .. 4g+3 of the token's block
+                    const uint32_t s01 = sums[j][g >> 1][2 * (g & 1)], s23 = sums[j][g >> 1][2 * (g & 1) + 1];
+                    const int s0 = static_cast<int16_t>(s01 & 0xFFFFu), s1 = static_cast<int16_t>(s01 >> 16);
+                    const int s2 = static_cast<int16_t>(s23 & 0xFFFFu), s3 = static_cast<int16_t>(s23 >> 16);
+                    const int isum = mul24(sca, da[j]) + mul24(scb, db[j]);
+                    const int msum = mul24(ma, s0 + s1) + mul24(mb, s2 + s3);
+                    acc[g][j] = q4k_term(acc[g][j], xd[j], d, dmin, isum, msum);
+                }
+            }
+        }
+        // sum over waves, then lane groups (the decode matmul's order)
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) red[wave][g][4 * G + j][i] = acc[g][j];
+        }
+        __syncthreads();
+        if (threadIdx.x < 256) {
+            const int tk = threadIdx.x >> 4, r = threadIdx.x & 15;
+            float v = 0.0F;
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) v += red[w][g][tk][r];
+            }
+            vals[16 * tt + tk][r] = v;
+        }
+    }
+    __syncthreads();
+    const int row0 = rg * 16;
+    const int nrows = min(16, static_cast<int>(a.mat.rows) - row0);
+    gemv_epilogue<kMmThreads>(a, row0, nrows, [&](int j, int t) { return vals[t][j]; }, &vals[0][0]);
+}
+
 // Float weights (F32/F16, small models): one wave per row, lanes over K,
 // float activations (RMS-normalized in the prologue when a gain is given).
 constexpr int kFloatThreads = 256;
@@ -1027,6 +1155,42 @@ __global__ __launch_bounds__(256) void k_quantize(const float* x, int32_t stride
                      out.s + static_cast<size_t>(row) * (out.K / 16) + b * 16);
 }
 
+// RMSNorm x gain + quantization of whole rows, one work-group per row: the
+// codes and scales the normalized-input matmul prologue stages (stage_f32
+// with a gain, then finish_norm), computed the same way (prefill steps).
+constexpr int kNormMaxBlocks = 128;
+#pragma clang fp contract(off)
+__global__ __launch_bounds__(256) void k_quantize_norm(const float* x, int32_t stride, const int32_t* gather,
+                                                       const float* gain, float eps, Act8 out) {
+    __shared__ float ssq[kNormMaxBlocks], db[kNormMaxBlocks];
+    __shared__ float rs;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int row = blockIdx.x, nb = out.K / 256;
+    const float* xr = x + static_cast<size_t>(gather ? gather[row] : row) * stride;
+    for (int b = wave; b < nb; b += 4) {
+        const f32x4 v4 = *reinterpret_cast<const f32x4*>(xr + b * 256 + 4 * lane);
+        const f32x4 g4 = *reinterpret_cast<const f32x4*>(gain + b * 256 + 4 * lane);
+        float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+        const float sq2 = wave_sum(vv[0] * vv[0] + vv[1] * vv[1] + vv[2] * vv[2] + vv[3] * vv[3]);
+        if (lane == 0) ssq[b] = sq2;
+        vv[0] = vv[0] * g4.x;
+        vv[1] = vv[1] * g4.y;
+        vv[2] = vv[2] * g4.z;
+        vv[3] = vv[3] * g4.w;
+        quant_block_wave(vv, lane, out.q + static_cast<size_t>(row) * out.K + b * 256, &db[b],
+                         out.s + static_cast<size_t>(row) * (out.K / 16) + b * 16);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float sum = 0.0F;
+        for (int b = 0; b < nb; ++b) sum += ssq[b];
+        rs = 1.0F / sqrtf(sum / static_cast<float>(out.K) + eps);
+    }
+    __syncthreads();
+    for (int b = threadIdx.x; b < nb; b += 256) out.d[static_cast<size_t>(row) * nb + b] = db[b] * rs;
+}
+#pragma clang fp contract(on)
+
 // ------------------------------------------------------------------ attention
 // Split-K causal GQA flash attention (qwen2_architecture.cpp:438-464, mask
 // 697-708) over the f16 caches. Work-group = (key split, kv head x query
@@ -1058,10 +1222,14 @@ __device__ __forceinline__ void attn_load_tile(global_ptr<const uint16_t> kc, gl
 #pragma unroll
         for (int c = 0; c < HD / 32; ++c) kr[c] = load_u4(krow + qq * (HD / 4) + 8 * c);
     }
+    // V is stored transposed ([dim][position]): the lane's two dims come from two rows
+    const int d0 = min(2 * lane, hd - 1), d1 = min(2 * lane + 1, hd - 1);
 #pragma unroll
     for (int u = 0; u < kAttnTile; ++u) {
         const int kj = min(t0 + u, capacity - 1);
-        vv[u] = 2 * lane < hd ? *(global_ptr<const uint32_t>) (vc + static_cast<size_t>(kj) * hd + 2 * lane) : 0u;
+        const uint32_t lo = vc[static_cast<size_t>(d0) * capacity + kj];
+        const uint32_t hi = vc[static_cast<size_t>(d1) * capacity + kj];
+        vv[u] = 2 * lane < hd ? (lo | (hi << 16)) : 0u;
     }
 }
 
@@ -1257,6 +1425,191 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
     }
 }
 
+// ------------------------------------------------------------------ attention on matrix cores
+// The same split-K causal GQA attention for head dims 64 and 128 on MFMA.
+// Work-group = (key split, kv head x group of 16 query rows, sequence); the
+// 16 query rows (G heads x tokens) are the N side of both products. Each wave
+// takes 16-key tiles:
+//   S^T[16 keys][16 rows] = K[16 keys][hd] . Q^T[hd][16 rows]     (16x16x32 f16)
+//   O^T[hd][16 rows]     += V^T[hd][16 keys] . P^T[16 keys][16 rows] (16x16x16 f16)
+// K is read as stored (position-major rows) and V from its transposed cache
+// ([dim][position]), so every operand is a contiguous per-lane load. The
+// queries (scaled by hd^-1/2) and the probabilities enter as f16 hi + lo
+// pairs, which keeps the products at about 22 bits. Lane l holds row l % 16
+// of the S^T and O^T fragments, so a row's online-softmax state lives in the
+// four lanes l % 16 + 16 j. Output: the split's (max, sum, output) partial,
+// as from k_attention.
+constexpr int kAttnRows = 16;
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <int HD>
+__device__ __forceinline__ void attn_mfma_load(global_ptr<const uint16_t> kc, global_ptr<const uint16_t> vt, int t0,
+                                               int capacity, int r, int grp, u32x4 (&kr)[HD / 32],
+                                               u32x2 (&vr)[HD / 16]) {
+    // capacity is a multiple of 16, so a clamped tile start keeps all 16 keys in bounds
+    const int tl = min(t0, capacity - kAttnRows);
+    global_ptr<const uint16_t> krow = kc + static_cast<size_t>(tl + r) * HD + 8 * grp;
+#pragma unroll
+    for (int s = 0; s < HD / 32; ++s) kr[s] = *(global_ptr<const u32x4>) (krow + 32 * s);
+#pragma unroll
+    for (int d = 0; d < HD / 16; ++d) {
+        vr[d] = *(global_ptr<const u32x2>) (vt + static_cast<size_t>(16 * d + r) * capacity + tl + 4 * grp);
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void k_attention_mfma(const float* __restrict__ q,
+                                                                 const StepDev* __restrict__ step, int32_t layer,
+                                                                 int32_t n_head, int32_t n_head_kv,
+                                                                 int32_t splits_max, int32_t qgroups,
+                                                                 float* __restrict__ partial) {
+    constexpr int W = kAttnThreads / kWave, KS = HD / 32, DB = HD / 16, R = kAttnRows;
+    __shared__ float Ms[W][R], Ls[W][R];
+    __shared__ float Os[W][HD][R];
+    const int seq = blockIdx.z;
+    if (seq >= step->n_seq) return;
+    const int32_t pos0 = step->seqs[seq].pos0, len = step->seqs[seq].len, row0 = step->seqs[seq].row0;
+    const int32_t capacity = step->seqs[seq].capacity;
+    const int G = n_head / n_head_kv, NQ = G * len, H = n_head * HD;
+    const int kvh = blockIdx.y / qgroups, qg = blockIdx.y % qgroups;
+    const int q_begin = qg * R;
+    if (q_begin >= NQ) return;
+    const int n_keys = pos0 + len;
+    const int L = attn_split_len(n_keys, splits_max);
+    const int n_splits = (n_keys + L - 1) / L;
+    const int split = blockIdx.x;
+    if (split >= n_splits) return;
+    const int k0 = split * L, k1 = min(n_keys, k0 + L);
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int r = lane & (R - 1), grp = lane >> 4;
+    const size_t head_base = static_cast<size_t>(layer) * n_head_kv + kvh;
+    global_ptr<const uint16_t> kc =
+        as_global(static_cast<const uint16_t*>(step->seqs[seq].k)) + head_base * capacity * HD;
+    global_ptr<const uint16_t> vt =
+        as_global(static_cast<const uint16_t*>(step->seqs[seq].v)) + head_base * HD * capacity;
+
+    // the wave's first tile is requested before the queries
+    int t0 = k0 + R * wave;
+    u32x4 kr[KS];
+    u32x2 vr[DB];
+    attn_mfma_load<HD>(kc, vt, t0, capacity, r, grp, kr, vr);
+
+    // B operand of S^T: the lane's row r, dims 32 s + 8 grp .. + 7, as f16 hi + lo
+    const int qi = min(q_begin + r, NQ - 1);
+    const bool row_ok = q_begin + r < NQ;
+    const int tr = qi / G, head = kvh * G + qi % G;
+    const int limit = pos0 + tr;  // last visible key of the row (causal)
+    const float* qrow = q + static_cast<size_t>(row0 + tr) * H + head * HD + 8 * grp;
+    const float scale = 1.0F / sqrtf(static_cast<float>(HD));
+    h8 qhi[KS], qlo[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        const float4 a = *reinterpret_cast<const float4*>(qrow + 32 * s);
+        const float4 b = *reinterpret_cast<const float4*>(qrow + 32 * s + 4);
+        const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float v = row_ok ? x[j] * scale : 0.0F;
+            qhi[s][j] = static_cast<_Float16>(v);
+            qlo[s][j] = static_cast<_Float16>(v - static_cast<float>(qhi[s][j]));
+        }
+    }
+
+    float m = -INFINITY, l = 0.0F;
+    f32x4 o[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) o[d] = f32x4{0.0F, 0.0F, 0.0F, 0.0F};
+    for (; t0 < k1; t0 += W * R) {
+        u32x4 krn[KS];
+        u32x2 vrn[DB];
+        attn_mfma_load<HD>(kc, vt, t0 + W * R, capacity, r, grp, krn, vrn);
+        f32x4 sc = {0.0F, 0.0F, 0.0F, 0.0F};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const h8 ka = __builtin_bit_cast(h8, kr[s]);
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qhi[s], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qlo[s], sc, 0, 0, 0);
+        }
+        // the lane's keys t0 + 4 grp + j for row r
+        float sv[4], tmax = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int key = t0 + 4 * grp + j;
+            const bool vis = row_ok && key < k1 && key <= limit;
+            sv[j] = vis ? sc[j] : -INFINITY;
+            tmax = fmaxf(tmax, sv[j]);
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float m_new = fmaxf(m, tmax);
+        float alpha = 1.0F, p[4] = {0.0F, 0.0F, 0.0F, 0.0F};
+        if (m_new != -INFINITY) {
+            alpha = m == -INFINITY ? 0.0F : expf(m - m_new);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) p[j] = sv[j] == -INFINITY ? 0.0F : expf(sv[j] - m_new);
+        }
+        l = l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+        m = m_new;
+        h4 phi, plo;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            phi[j] = static_cast<_Float16>(p[j]);
+            plo[j] = static_cast<_Float16>(p[j] - static_cast<float>(phi[j]));
+        }
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+            const h4 va = __builtin_bit_cast(h4, vr[d]);
+            o[d] *= alpha;
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, phi, o[d], 0, 0, 0);
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, plo, o[d], 0, 0, 0);
+        }
+#pragma unroll
+        for (int s = 0; s < KS; ++s) kr[s] = krn[s];
+#pragma unroll
+        for (int d = 0; d < DB; ++d) vr[d] = vrn[d];
+    }
+    // the row's sum over its four lanes, then the waves merged in LDS
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (grp == 0) {
+        Ms[wave][r] = m;
+        Ls[wave][r] = l;
+    }
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Os[wave][16 * d + 4 * grp + j][r] = o[d][j];
+    }
+    __syncthreads();
+    const int nq = min(R, NQ - q_begin);
+    for (int e = threadIdx.x; e < nq * HD; e += kAttnThreads) {
+        const int i = e / HD, dim = e - i * HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, Ms[w][i]);
+        float Lsum = 0.0F, acc = 0.0F;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                const float f = Ms[w][i] == -INFINITY ? 0.0F : expf(Ms[w][i] - M);
+                Lsum += f * Ls[w][i];
+                acc += f * Os[w][dim][i];
+            }
+        }
+        const int qrow_i = q_begin + i;
+        const int t = qrow_i / G, hh = kvh * G + qrow_i % G;
+        float* dst = partial + ((static_cast<size_t>(row0 + t) * n_head + hh) * splits_max + split) * (HD + 2);
+        if (dim == 0) {
+            dst[0] = M;
+            dst[1] = Lsum;
+        }
+        dst[2 + dim] = acc;
+    }
+}
+
 // Combines the split partials of every (row, head): one work-group per
 // (row, 256 output values); with xq set the 256 values are quantized into xq.
 __global__ __launch_bounds__(256) void k_attention_merge(const float* __restrict__ partial,
@@ -1375,6 +1728,7 @@ constexpr int kMmChunk = JFH_MM_CHUNK;
 constexpr int kMmPartBytes = 65536;
 constexpr int kMmTargetWgs = JFH_MM_TARGET_WGS;
 constexpr size_t kMmOnePassLds = 64 * 1024;  // largest one-pass staging of a row that is not normalized
+constexpr size_t kMmMaxLds = 160 * 1024;
 
 size_t mm_lds_bytes(int nt, int chunk, int rgw) {
     const size_t nbc = static_cast<size_t>(chunk) / 256;
@@ -1403,11 +1757,17 @@ MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds) {
     const bool normed = a.xq.q == nullptr && a.x.gain != nullptr;
     int chunk = K;
     if (!normed && K > kMmChunk && mm_lds_bytes(nt, K, rgw) > kMmOnePassLds) chunk = kMmChunk;
+    if (!normed && mm_lds_bytes(nt, chunk, rgw) > kMmMaxLds) {
+        // wide token groups: shorter passes, in whole rounds of the waves' tiles, until the staging fits
+        const int round = 256 * kMmWaves;
+        chunk = std::min(chunk, kMmChunk) / round * round;
+        while (chunk > round && mm_lds_bytes(nt, chunk, rgw) > kMmMaxLds) chunk -= round;
+    }
     MmGeom g;
     g.rgw = rgw;
     g.chunk = chunk;
     lds = mm_lds_bytes(nt, chunk, rgw);
-    if (lds > 160 * 1024) throw std::invalid_argument("matmul staging does not fit the LDS");
+    if (lds > kMmMaxLds) throw std::invalid_argument("matmul staging does not fit the LDS");
     return g;
 }
 
@@ -1512,11 +1872,41 @@ void launch_quantize(const float* x, int32_t stride, int32_t n_rows, const Act8&
     check(hipGetLastError(), "quantize launch");
 }
 
+void launch_quantize_norm(const float* x, int32_t stride, const int32_t* gather, const float* gain, float eps,
+                          int32_t n_rows, const Act8& out, hipStream_t stream) {
+    if (out.K % 256 != 0 || out.K / 256 > kNormMaxBlocks || stride % 4 != 0 || gain == nullptr) {
+        throw std::invalid_argument("normalized quantization needs rows of a multiple of 256 values and a gain");
+    }
+    launch(k_quantize_norm, dim3(n_rows), dim3(256), 0, stream, x, stride, gather, gain, eps, out);
+    check(hipGetLastError(), "normalized quantize launch");
+}
+
+bool wide_matmul_supported(uint32_t type) { return type == 11; }
+
+void launch_gemv_wide(const GemvArgs& a, hipStream_t stream) {
+    if (!wide_matmul_supported(a.mat.type) || a.xq.q == nullptr || a.xq.K != static_cast<int32_t>(a.mat.cols) ||
+        a.mat.cols % kActBlock != 0 || a.n_tok < 1 || a.n_tok > kWideRows) {
+        throw std::invalid_argument("wide matmul takes Q4_K weights and up to 64 pre-quantized token rows");
+    }
+    if (a.mode == kLogits || (a.mode == kSwiGLU && a.mat.rows % (2 * kGluGroup) != 0) ||
+        (a.mode == kQKV && a.mat.rows % 2 != 0)) {
+        throw std::invalid_argument("wide matmul mode or row layout not supported");
+    }
+    const int grid = (static_cast<int>(a.mat.rows) + 15) / 16;
+    launch(k_mm_wide_q4k, dim3(grid), dim3(kMmThreads), 0, stream, a);
+    check(hipGetLastError(), "wide matmul launch");
+}
+
 void launch_embed(const DMat& table, const StepDev* step, float* h, int32_t n_rows, int32_t H,
                   unsigned long long* best, int32_t n_best, hipStream_t stream) {
     dim3 grid((H + 255) / 256, n_rows);
     launch(k_embed, grid, dim3(256), 0, stream, table, step, h, H, best, n_best);
     check(hipGetLastError(), "embed launch");
+}
+
+int32_t attention_max_rows(int32_t head_dim) {
+    // the matrix-core kernel takes any number of 16-row groups; the generic one up to kMaxAttnQGroups groups of 8
+    return (head_dim == 128 || head_dim == 64) ? kMaxRows * 64 : kMaxAttnQGroups * kAttnQPW;
 }
 
 int32_t attention_splits(int32_t capacity) {
@@ -1532,21 +1922,25 @@ void launch_attention(const float* q, const StepDev* step, int32_t max_len, int3
                       int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t splits, float* partial,
                       hipStream_t stream) {
     const int G = n_head / n_head_kv;
-    const int qgroups = (G * max_len + kAttnQPW - 1) / kAttnQPW;
     if (head_dim > 2 * kWave || head_dim % 4 != 0) {
         throw std::invalid_argument("attention supports head dims that are multiples of 4 up to 128");
     }
-    if (qgroups > kMaxAttnQGroups) throw std::invalid_argument("attention step has too many query rows per kv head");
+    const bool mfma = head_dim == 128 || head_dim == 64;
+    const int group_rows = mfma ? kAttnRows : kAttnQPW;
+    const int qgroups = (G * max_len + group_rows - 1) / group_rows;
+    if (G * max_len > attention_max_rows(head_dim)) {
+        throw std::invalid_argument("attention step has too many query rows per kv head");
+    }
     dim3 grid(splits, n_head_kv * qgroups, n_seq), block(kAttnThreads);
     if (head_dim == 128) {
-        launch(k_attention<128>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
-                           qgroups, partial);
+        launch(k_attention_mfma<128>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, splits, qgroups,
+               partial);
     } else if (head_dim == 64) {
-        launch(k_attention<64>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
-                           qgroups, partial);
+        launch(k_attention_mfma<64>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, splits, qgroups,
+               partial);
     } else {
-        launch(k_attention<0>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits,
-                           qgroups, partial);
+        launch(k_attention<0>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits, qgroups,
+               partial);
     }
     check(hipGetLastError(), "attention launch");
 }

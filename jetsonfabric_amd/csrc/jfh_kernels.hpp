@@ -148,6 +148,20 @@ void launch_embed(const DMat& table, const StepDev* step, float* h, int32_t n_ro
 void launch_gemv(const GemvArgs& a, hipStream_t stream);
 // Quantizes n_rows float rows of K values (K % 256 == 0) into `out`.
 void launch_quantize(const float* x, int32_t stride, int32_t n_rows, const Act8& out, hipStream_t stream);
+// RMS-normalizes n_rows float rows (row gather[r] when gather is set),
+// multiplies them by `gain` and quantizes them into `out`: the codes and
+// scales the matmul's normalized-input prologue would stage.
+void launch_quantize_norm(const float* x, int32_t stride, const int32_t* gather, const float* gain, float eps,
+                          int32_t n_rows, const Act8& out, hipStream_t stream);
+// Token rows of one matrix-core matmul launch (steps with more rows than the
+// decode matmul's 8-row groups).
+constexpr int kWideRows = 64;
+// Whether launch_gemv_wide takes matrices of this type.
+bool wide_matmul_supported(uint32_t type);
+// Matmul of 9..kWideRows pre-quantized token rows (a.xq) on matrix cores;
+// every row's result equals launch_gemv's for that row alone. Modes kStore,
+// kAdd, kSwiGLU and kQKV.
+void launch_gemv_wide(const GemvArgs& a, hipStream_t stream);
 // Split-K causal GQA flash attention over the f16 caches of the step's
 // sequences. Every (row, head, split) writes its (max, sum, unnormalized
 // output) to `partial`; launch_attention_merge combines the splits.
@@ -159,6 +173,8 @@ void launch_attention(const float* q, const StepDev* step, int32_t max_len, int3
 void launch_attention_merge(const float* partial, const StepDev* step, int32_t n_rows, int32_t n_head,
                             int32_t head_dim, int32_t splits, float* out, const Act8& xq, hipStream_t stream);
 int32_t attention_splits(int32_t capacity);
+// Query rows (G heads x tokens) one sequence may bring to a step per kv head.
+int32_t attention_max_rows(int32_t head_dim);
 // Floats of the attention split scratch for `rows` token rows.
 size_t attention_partial_floats(int32_t rows, int32_t n_head, int32_t head_dim, int32_t splits);
 void launch_finish(const unsigned long long* best, const StepDev* step, int32_t n_out, StepOut* out,

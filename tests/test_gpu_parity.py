@@ -75,7 +75,7 @@ def test_dequantize_bit_exact(typed):
             assert np.array_equal(gpu[i].view(np.uint32), ref.view(np.uint32)), f"{name} row {r}"
 
 
-@pytest.mark.parametrize("n_tok", [1, 2, 3, 5, 8, 9])
+@pytest.mark.parametrize("n_tok", [1, 2, 3, 5, 8, 9, 16, 40, 64])
 def test_matmul_matches_oracle(typed, n_tok):
     t, model, engine = typed
     rng = np.random.default_rng(n_tok)
@@ -90,6 +90,21 @@ def test_matmul_matches_oracle(typed, n_tok):
         assert np.allclose(gpu, ref, rtol=1e-4, atol=2e-5 * scale), f"{name} max err {np.abs(gpu - ref).max():.3e}"
         exact = jo.matmul(t, info["data"], cols, rows, x, jo.MODE_EXACT)
         assert jo.nrmse(exact, gpu) < 1e-2
+
+
+@pytest.mark.parametrize("n_tok", [9, 33, 64])
+def test_wide_matmul_rows_equal_single_rows(typed, n_tok):
+    """Steps of more than 8 rows run Q4_K matrices on matrix cores; every row
+    must equal the same row computed alone (the decode path), bit for bit."""
+    t, model, engine = typed
+    rng = np.random.default_rng(100 + n_tok)
+    for name in ("blk.0.attn_q.weight", "blk.1.ffn_down.weight"):
+        cols, rows = model.tensor(name)["shape"]
+        x = rng.standard_normal((n_tok, cols)).astype(np.float32)
+        wide = engine.matmul(name, x, rows)
+        for r in range(n_tok):
+            single = engine.matmul(name, x[r:r + 1], rows)
+            assert np.array_equal(wide[r].view(np.uint32), single[0].view(np.uint32)), f"{name} row {r}"
 
 
 def test_tiny_fixture_known_answer():
@@ -119,6 +134,29 @@ def test_forward_matches_oracle(q4k):
         _, rl = ref.forward([tok], 1)
         assert_logits_match(rl[0], lg, nxt, f"decode step {step}")
         tok = nxt
+
+
+def test_chunked_prefill_matches_oracle_and_token_by_token(q4k):
+    """A 150-token prompt is prefilled in chunks of up to 64 rows (matrix-core
+    matmuls); its logits match the oracle's, and a session fed the same
+    prompt one token at a time reaches the same greedy continuation."""
+    model, engine, om = q4k
+    prompt = _prompt(150, SMALL.n_vocab, 12)
+    s = engine.create_session(200)
+    ref = om.session(200, jo.MODE_Q8)
+    tok, lg = s.prefill_greedy(prompt, logits=True)
+    _, rl = ref.forward(prompt, 1)
+    assert_logits_match(rl[0], lg, tok, "chunked prefill")
+    one = engine.create_session(200)
+    first = one.prefill_greedy(prompt[:1])
+    for t in prompt[1:]:
+        first = one.decode_greedy(t)
+    assert first == tok
+    a, b = [tok], [first]
+    for _ in range(6):
+        a.append(s.decode_greedy(a[-1]))
+        b.append(one.decode_greedy(b[-1]))
+    assert a == b
 
 
 @pytest.mark.parametrize("types", [(jf.Q4_K, jf.Q8_0, jf.Q8_0, True), (jf.Q2_K, jf.Q2_K, jf.Q6_K, False),
