@@ -492,7 +492,11 @@ std::string gemv_label(const gpu::GemvArgs& a) {
     const bool fl = t == kF32 || t == kF16;
     const int nt = a.n_tok > 8 ? 8 : a.n_tok;
     const int slot = nt <= 2 ? nt : nt <= 4 ? 4 : nt <= 6 ? 6 : 8;
-    return std::string(fl ? "k_gemv_f<" : "k_mm<") + (fl ? "" : std::to_string(t) + ",") + std::to_string(fl ? nt : slot) + ">";
+    if (fl) return "k_gemv_f<" + std::to_string(nt) + ">";
+    // template arguments of the launched kernel: type, token slots, input kind
+    // (0 int8 rows, 1 RMS-normalized float rows, 2 float rows)
+    const int in = a.xq.q ? 0 : a.x.gain ? 1 : 2;
+    return "k_mm<" + std::to_string(t) + "," + std::to_string(slot) + "," + std::to_string(in) + ">";
 }
 
 // Algorithmic HBM bytes of one matmul launch: encoded weights and bias, the

@@ -206,9 +206,24 @@ class OracleModel:
                          ctypes.cast(self._layers, POINTER(_Layer)))
 
     @classmethod
-    def from_model(cls, model) -> "OracleModel":
+    def from_model(cls, model, overrides: dict | None = None) -> "OracleModel":
+        """Oracle over a jetsonfabric_amd Model's host tensors; `overrides`
+        maps tensor names to float32 arrays of the same shape used instead
+        (kept alive by the returned object)."""
         names = set(model.tensor_names())
-        return cls(model.config, model.tensor, lambda n: n in names)
+        held = {k: np.ascontiguousarray(v, dtype=np.float32) for k, v in (overrides or {}).items()}
+
+        def tensor(name: str) -> dict:
+            v = model.tensor(name)
+            if name not in held:
+                return v
+            if v["type"] != F32 or held[name].size != int(np.prod(v["shape"])):
+                raise ValueError(f"override of {name} must be float32 of shape {v['shape']}")
+            return dict(v, data=held[name].ctypes.data)
+
+        om = cls(model.config, tensor, lambda n: n in names)
+        om._held = held
+        return om
 
     def session(self, capacity: int, mode: int = MODE_Q8, threads: int = 8) -> "OracleSession":
         return OracleSession(self, capacity, mode, threads)

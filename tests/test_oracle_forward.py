@@ -222,6 +222,24 @@ def test_capacity_and_vocabulary_errors():
         s.forward([300], 1)
 
 
+def test_tensor_overrides():
+    model = _q4k_model()
+    prompt = [5, 17, 99, 3, 250, 7]
+    gain = np.frombuffer(model.tensor_bytes("blk.0.attn_norm.weight"), dtype=np.float32).copy()
+    _, base = jo.OracleModel.from_model(model).session(16, jo.MODE_Q8, 1).forward(prompt, 1)
+    _, same = jo.OracleModel.from_model(model, {"blk.0.attn_norm.weight": gain}).session(16, jo.MODE_Q8, 1).forward(
+        prompt, 1)
+    assert np.array_equal(base, same)
+    gain[3] *= np.float32(1.5)
+    _, moved = jo.OracleModel.from_model(model, {"blk.0.attn_norm.weight": gain}).session(16, jo.MODE_Q8, 1).forward(
+        prompt, 1)
+    assert not np.array_equal(base, moved)
+    with pytest.raises(ValueError, match="float32 of shape"):
+        jo.OracleModel.from_model(model, {"blk.0.attn_norm.weight": gain[:10]})
+    with pytest.raises(ValueError, match="float32 of shape"):
+        jo.OracleModel.from_model(model, {"blk.0.attn_q.weight": np.zeros(256 * 256, np.float32)})
+
+
 def test_quantized_activation_mode_stays_close_to_exact():
     model = _q4k_model()
     om = jo.OracleModel.from_model(model)
