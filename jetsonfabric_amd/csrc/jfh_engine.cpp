@@ -491,7 +491,9 @@ std::string gemv_label(const gpu::GemvArgs& a) {
     const uint32_t t = a.mat.type;
     const bool fl = t == kF32 || t == kF16;
     const int nt = a.n_tok > 8 ? 8 : a.n_tok;
-    const int slot = nt <= 2 ? nt : nt <= 4 ? 4 : nt <= 6 ? 6 : 8;
+    // int8 Q4_K rows run in token quads (4 or 8 slots) from 3 tokens on
+    const bool quads = t == kQ4_K && a.xq.q != nullptr && nt >= 3;
+    const int slot = nt <= 2 ? nt : nt <= 4 ? 4 : nt <= 6 && !quads ? 6 : 8;
     if (fl) return "k_gemv_f<" + std::to_string(nt) + ">";
     // template arguments of the launched kernel: type, token slots, input kind
     // (0 int8 rows, 1 RMS-normalized float rows, 2 float rows)
@@ -927,8 +929,10 @@ void Engine::matmul(const std::string& name, const float* x_host, uint32_t n_tok
         fail(Status::OutOfMemory, "allocate matmul output");
     }
     std::vector<float> full(static_cast<size_t>(n_tok) * m.rows);
-    // more than one 8-row group of a wide-capable type: quantized once, then the matrix-core path (as in a step)
+    // Q4_K from 3 rows on: quantized once, then the matrix-core paths a step takes (token quads up to 8
+    // rows, the wide kernel beyond)
     const bool wide = n_tok > 8 && gpu::wide_matmul_supported(m.type) && m.cols % 256 == 0;
+    const bool quads = n_tok >= 3 && m.type == kQ4_K && m.cols % 256 == 0;
     gpu::Act8 xq;
     uint8_t* xq_mem = nullptr;
     auto release = [&] {
@@ -945,7 +949,7 @@ void Engine::matmul(const std::string& name, const float* x_host, uint32_t n_tok
         a.n_tok = static_cast<int32_t>(n_tok);
         a.y = y;
         a.y_stride = static_cast<int32_t>(m.rows);
-        if (wide) {
+        if (wide || quads) {
             const size_t K = m.cols, nq = n_tok * K, nd = n_tok * (K / 256), ns = n_tok * (K / 16);
             hip_check(hipMalloc(&xq_mem, nq + nd * sizeof(float) + ns * sizeof(int16_t)), "allocate int8 rows");
             xq.K = static_cast<int32_t>(K);
@@ -954,7 +958,8 @@ void Engine::matmul(const std::string& name, const float* x_host, uint32_t n_tok
             xq.s = reinterpret_cast<int16_t*>(xq_mem + nq + nd * sizeof(float));
             gpu::launch_quantize(x, static_cast<int32_t>(K), static_cast<int32_t>(n_tok), xq, stream_);
             a.xq = xq;
-            gpu::launch_gemv_wide(a, stream_);
+            if (wide) gpu::launch_gemv_wide(a, stream_);
+            else gpu::launch_gemv(a, stream_);
         } else {
             a.x = {x, static_cast<int32_t>(m.cols), nullptr, nullptr, 0.0F};
             gpu::launch_gemv(a, stream_);

@@ -16,6 +16,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <type_traits>
 
 namespace jfh::gpu {
 namespace {
@@ -35,6 +36,7 @@ __device__ __forceinline__ global_ptr<T> as_global(T* p) {
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint4 load_u4(global_ptr<const uint16_t> p) {
     const u32x4 v = *(global_ptr<const u32x4>) p;
@@ -496,19 +498,22 @@ struct Tile<11> {
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            if (t < nt) {
+            {
+                // token slots past nt repeat the last token (straight-line code keeps
+                // the load waits exact); their sums are never read
+                const int tc = min(t, nt - 1);
                 uint32_t xw[16];
-                load_x(x, t, xw);
+                load_x(x, tc, xw);
                 int da = 0, db = 0;
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     da = sdot4(lo[k], xw[k], da);
                     db = sdot4(hi[k], xw[8 + k], db);
                 }
-                const int16_t* s = x.s + t * x.s_stride + 4 * g;
+                const int16_t* s = x.s + tc * x.s_stride + 4 * g;
                 const int isum = mul24(sca, da) + mul24(scb, db);
                 const int msum = mul24(ma, s[0] + s[1]) + mul24(mb, s[2] + s[3]);
-                acc[t] = q4k_term(acc[t], x.d[t * x.d_stride], d, dmin, isum, msum);
+                acc[t] = q4k_term(acc[t], x.d[tc * x.d_stride], d, dmin, isum, msum);
             }
         }
     }
@@ -549,10 +554,13 @@ struct Tile<13> {
         for (int m = 0; m < 4; ++m) sc[m] = sext8(r.scw >> (8 * m));
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            if (t < nt) {
+            {
+                // token slots past nt repeat the last token (straight-line code keeps
+                // the load waits exact); their sums are never read
+                const int tc = min(t, nt - 1);
                 uint32_t xw[16];
-                load_x(x, t, xw);
-                const int16_t* s = x.s + t * x.s_stride + 4 * g;
+                load_x(x, tc, xw);
+                const int16_t* s = x.s + tc * x.s_stride + 4 * g;
                 int isum = 0;
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
@@ -561,7 +569,7 @@ struct Tile<13> {
                     for (int q = 0; q < 4; ++q) dm = sdot4(w[4 * m + q], xw[4 * m + q], dm);
                     isum += mul24(sc[m], dm - 32 * s[m]);
                 }
-                acc[t] += x.d[t * x.d_stride] * (d * static_cast<float>(isum));
+                acc[t] += x.d[tc * x.d_stride] * (d * static_cast<float>(isum));
             }
         }
     }
@@ -589,16 +597,19 @@ struct Tile<7> {
                                 r.c[2].x, r.c[2].y, r.c[2].z, r.c[2].w, r.c[3].x, r.c[3].y, r.c[3].z, r.c[3].w};
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            if (t < nt) {
+            {
+                // token slots past nt repeat the last token (straight-line code keeps
+                // the load waits exact); their sums are never read
+                const int tc = min(t, nt - 1);
                 uint32_t xw[16];
-                load_x(x, t, xw);
+                load_x(x, tc, xw);
                 int ia = 0, ib = 0;
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     ia = sdot4(w[k], xw[k], ia);
                     ib = sdot4(w[8 + k], xw[8 + k], ib);
                 }
-                acc[t] += x.d[t * x.d_stride] * (da * static_cast<float>(ia) + db * static_cast<float>(ib));
+                acc[t] += x.d[tc * x.d_stride] * (da * static_cast<float>(ia) + db * static_cast<float>(ib));
             }
         }
     }
@@ -630,10 +641,13 @@ struct Tile<9> {
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            if (t < nt) {
+            {
+                // token slots past nt repeat the last token (straight-line code keeps
+                // the load waits exact); their sums are never read
+                const int tc = min(t, nt - 1);
                 uint32_t xw[16];
-                load_x(x, t, xw);
-                const int16_t* s = x.s + t * x.s_stride + 4 * g;
+                load_x(x, tc, xw);
+                const int16_t* s = x.s + tc * x.s_stride + 4 * g;
                 int isum = 0, msum = 0;
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
@@ -643,13 +657,90 @@ struct Tile<9> {
                     isum += mul24(sc[m], dm);
                     msum += mul24(mn[m], s[m]);
                 }
-                acc[t] += x.d[t * x.d_stride] * (d * static_cast<float>(isum) - dmin * static_cast<float>(msum));
+                acc[t] += x.d[tc * x.d_stride] * (d * static_cast<float>(isum) - dmin * static_cast<float>(msum));
             }
         }
     }
 };
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Q4_K tiles x 4..8 int8 token rows on matrix cores, one token quad per
+// v_mfma_i32_16x16x32_i8: the A operand's 16 rows are (token t', lane group
+// G') pairs, 4 t' + G', and row 4 t' + G' carries token t''s activation codes
+// only in lane group G''s K slots (zero elsewhere), so D[4 t' + G'][i] is the
+// integer dot of weight row i's sub-block with token t' over lane group G''s
+// values alone — the same integer the decode dot computes for that lane
+// group. Four MFMAs (chunks of 8 values) per sub-block parity give the dots of
+// sub-blocks 2 G' (low nibbles) and 2 G' + 1 (high nibbles). Lane (row i,
+// lane group L) then holds token 4 q + L's dots for all four lane groups and
+// applies q4k_term per lane group in the decode order, keeping acc[4 q + G'].
+struct TileQ4Quad {
+    struct Regs {
+        uint4 w0, w1, hdr;
+    };
+    static __device__ __forceinline__ Regs load(const uint8_t* t, int lane) {
+        Regs r;
+        r.hdr = *reinterpret_cast<const uint4*>(t + 16 * (lane & 15));
+        r.w0 = *reinterpret_cast<const uint4*>(t + 256 + 16 * lane);
+        r.w1 = *reinterpret_cast<const uint4*>(t + 1280 + 16 * lane);
+        return r;
+    }
+    // acc[4 q + G']: running sum of (row lane % 16, token 4 q + lane / 16,
+    // lane group G'); zero: 64 zero bytes of LDS (the masked A slots).
+    template <int NT>
+    static __device__ __forceinline__ void dot(const Regs& r, int L, const XLds& x, int nt, float* acc,
+                                               const int8_t* zero) {
+        static_assert(NT % 4 == 0, "token quads");
+        constexpr int NQ = NT / 4;
+        const int i = threadIdx.x & 15;
+        const float d = h2f(r.hdr.x), dmin = h2f(r.hdr.x >> 16);
+        // row i's 24-bit fields sc 2g | sc 2g+1 | m 2g | m 2g+1 of the four lane groups
+        const uint32_t F[4] = {r.hdr.y & 0xFFFFFFu, (r.hdr.y >> 24) | ((r.hdr.z & 0xFFFFu) << 8),
+                               (r.hdr.z >> 16) | ((r.hdr.w & 0xFFu) << 16), r.hdr.w >> 8};
+        const uint32_t pw[8] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w, r.w1.x, r.w1.y, r.w1.z, r.w1.w};
+        long bl[4], bh[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t l0 = pw[2 * c] & 0x0F0F0F0Fu, l1 = pw[2 * c + 1] & 0x0F0F0F0Fu;
+            const uint32_t h0 = (pw[2 * c] >> 4) & 0x0F0F0F0Fu, h1 = (pw[2 * c + 1] >> 4) & 0x0F0F0F0Fu;
+            bl[c] = static_cast<long>(static_cast<uint64_t>(l0) | (static_cast<uint64_t>(l1) << 32));
+            bh[c] = static_cast<long>(static_cast<uint64_t>(h0) | (static_cast<uint64_t>(h1) << 32));
+        }
+        const bool own = (i & 3) == L;  // this lane's A slots carry codes
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            // token slots past nt repeat the last token; their sums are never read
+            const int ta = min(4 * q + (i >> 2), nt - 1);
+            const u32x4* src = reinterpret_cast<const u32x4*>(own ? x.q + ta * x.q_stride : zero);
+            const u32x4 c0 = src[0], c1 = src[1], c2 = src[2], c3 = src[3];
+            const u32x2 al[4] = {{c0.x, c0.y}, {c0.z, c0.w}, {c1.x, c1.y}, {c1.z, c1.w}};
+            const u32x2 ah[4] = {{c2.x, c2.y}, {c2.z, c2.w}, {c3.x, c3.y}, {c3.z, c3.w}};
+            i32x4 dl = {0, 0, 0, 0}, dh = {0, 0, 0, 0};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, al[c]), bl[c], dl, 0, 0, 0);
+                dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, ah[c]), bh[c], dh, 0, 0, 0);
+            }
+            const int tk = min(4 * q + L, nt - 1);
+            const float xd = x.d[tk * x.d_stride];
+            const u32x4* sp = reinterpret_cast<const u32x4*>(x.s + tk * x.s_stride);
+            const u32x4 s03 = sp[0], s47 = sp[1];  // the block's 16 code sums (int16 pairs)
+            const uint32_t sw[8] = {s03.x, s03.y, s03.z, s03.w, s47.x, s47.y, s47.z, s47.w};
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t f = F[g];
+                const int sca = f & 63, scb = (f >> 6) & 63, ma = (f >> 12) & 63, mb = (f >> 18) & 63;
+                const uint32_t s01 = sw[2 * g], s23 = sw[2 * g + 1];
+                const int s0 = static_cast<int16_t>(s01 & 0xFFFFu), s1 = static_cast<int16_t>(s01 >> 16);
+                const int s2 = static_cast<int16_t>(s23 & 0xFFFFu), s3 = static_cast<int16_t>(s23 >> 16);
+                const int isum = mul24(sca, dl[g]) + mul24(scb, dh[g]);
+                const int msum = mul24(ma, s0 + s1) + mul24(mb, s2 + s3);
+                acc[4 * q + g] = q4k_term(acc[4 * q + g], xd, d, dmin, isum, msum);
+            }
+        }
+    }
+};
 
 __device__ __forceinline__ unsigned long long pack_best(float v, uint32_t idx) {
     uint32_t u = __float_as_uint(v);
@@ -809,7 +900,9 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
     constexpr bool A8 = IN == kInAct8;
     constexpr bool GAIN = IN == kInNormed;
     constexpr int NB = GAIN ? kStageBatch : kStageBatchFloat;  // blocks per wave of a float staging batch
-    using T = Tile<TYPE>;
+    // int8 Q4_K rows in token quads run on matrix cores (TileQ4Quad)
+    constexpr bool QUAD = TYPE == 11 && A8 && NT % 4 == 0;
+    using T = std::conditional_t<QUAD, TileQ4Quad, Tile<TYPE>>;
     using Regs = typename T::Regs;
     constexpr int W = kMmWaves;
     constexpr uint32_t TB = tile_bytes(TYPE);
@@ -820,10 +913,17 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
     int8_t* sq = reinterpret_cast<int8_t*>(lds_raw);
     float* sd = reinterpret_cast<float*>(lds_raw + NT * chunk);
     int16_t* ss = reinterpret_cast<int16_t*>(sd + NT * nbc);
-    float* part = reinterpret_cast<float*>(ss + NT * (chunk / 16));  // [rgw][W][64 lanes][NT]
-    float* rs = part + rgw * W * 64 * NT;
+    // Row partials. One pass over K: each wave stores its finished row-group
+    // sums with the four lane groups already combined, [rgw][W][16 rows][NT].
+    // Several passes: every lane keeps running sums, [rgw][W][64 lanes][NT].
+    const bool single = nbc >= nb;
+    float* part = reinterpret_cast<float*>(ss + NT * (chunk / 16));
+    float* rs = part + (single ? rgw * W * 16 * NT : rgw * W * 64 * NT);
     float* ssq = rs + NT;       // [NT][nbc] block sums of squares (normed inputs)
     float* lv = ssq + NT * nbc;  // [rgw * 16 * NT]
+    // 64 zero bytes (16-byte aligned) for the masked operand slots of TileQ4Quad
+    int8_t* zero = reinterpret_cast<int8_t*>(lds_raw) +
+                   ((reinterpret_cast<uint8_t*>(lv + rgw * 16 * NT) - lds_raw + 15) & ~static_cast<ptrdiff_t>(15));
 
     const int n_rg = (static_cast<int>(a.mat.rows) + 15) / 16;
     const int rg0 = blockIdx.x * rgw;
@@ -891,7 +991,9 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
                                           : reinterpret_cast<const float*>(a.mat.data);
         y_pre = *src;
     }
-    for (int i = threadIdx.x; i < rgw * W * 64 * NT; i += kMmThreads) part[i] = 0.0F;
+    // zero partials (waves without tiles, when the row has fewer blocks than waves, add nothing)
+    for (int i = threadIdx.x; i < (single ? rgw * W * 16 * NT : rgw * W * 64 * NT); i += kMmThreads) part[i] = 0.0F;
+    if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(zero)[threadIdx.x] = 0u;
     if constexpr (A8) {
         stage_act8<kMmThreads>(a.xq, n_tok, 0, nbcur, sq, sd, ss, chunk, q0);
     } else {
@@ -905,6 +1007,7 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
             float acc[NT];
             int cm = 0;                                             // tile of the row group being computed
             float* slot = part + (wave * 64 + lane) * NT;          // the lane's running sums of that row group
+            float* done = part + (wave * 16 + (lane & 15)) * NT;   // its finished sums (one pass)
             const int8_t* xq0 = sq + wave * 256 + 64 * grp;         // its activation slice
             for (int n0 = 0; n0 < total; n0 += kMmDepth) {
 #pragma unroll
@@ -912,7 +1015,7 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
                     if (n0 + u < total) {
                         if (cm == 0) {
 #pragma unroll
-                            for (int t = 0; t < NT; ++t) acc[t] = slot[t];
+                            for (int t = 0; t < NT; ++t) acc[t] = single ? 0.0F : slot[t];
                         }
                         const int bl = wave + W * cm;
                         XLds x;
@@ -922,12 +1025,33 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
                         x.q_stride = chunk;
                         x.d_stride = nbc;
                         x.s_stride = chunk / 16;
-                        T::template dot<NT>(ring[u], grp, x, n_tok, acc);
+                        if constexpr (QUAD) T::template dot<NT>(ring[u], grp, x, n_tok, acc, zero);
+                        else T::template dot<NT>(ring[u], grp, x, n_tok, acc);
                         if (++cm == pr) {
                             cm = 0;
+                            if (single) {
+                                // (g0 + g1) + (g2 + g3) of the row's four lane-group sums
+                                if constexpr (QUAD) {
 #pragma unroll
-                            for (int t = 0; t < NT; ++t) slot[t] = acc[t];
-                            slot += W * 64 * NT;
+                                    for (int q = 0; q < NT / 4; ++q) {
+                                        done[4 * q + grp] =
+                                            (acc[4 * q] + acc[4 * q + 1]) + (acc[4 * q + 2] + acc[4 * q + 3]);
+                                    }
+                                } else {
+#pragma unroll
+                                    for (int t = 0; t < NT; ++t) {
+                                        float v = acc[t];
+                                        v += __shfl_xor(v, 16);
+                                        v += __shfl_xor(v, 32);
+                                        if (grp == 0) done[t] = v;
+                                    }
+                                }
+                                done += W * 16 * NT;
+                            } else {
+#pragma unroll
+                                for (int t = 0; t < NT; ++t) slot[t] = acc[t];
+                                slot += W * 64 * NT;
+                            }
                         }
                     }
                     load_next(ring[u]);
@@ -955,13 +1079,24 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
         }
     }
     __syncthreads();
+    // row sum: over waves in order of ((g0 + g1) + (g2 + g3)) per wave, on every layout
     auto sum = [&](int j, int t) {
         const int r = j >> 4, i = j & 15;
         float v = 0.0F;
+        if (single) {
+#pragma unroll
+            for (int w = 0; w < W; ++w) v += part[((r * W + w) * 16 + i) * NT + t];
+            return v;
+        }
 #pragma unroll
         for (int w = 0; w < W; ++w) {
+            float p[4];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) v += part[((r * W + w) * 64 + i + 16 * g) * NT + t];
+            for (int g = 0; g < 4; ++g) {
+                p[g] = QUAD ? part[((r * W + w) * 64 + i + 16 * (t & 3)) * NT + 4 * (t >> 2) + g]
+                            : part[((r * W + w) * 64 + i + 16 * g) * NT + t];
+            }
+            v += (p[0] + p[1]) + (p[2] + p[3]);
         }
         return v;
     };
@@ -1069,7 +1204,7 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide_q4k(GemvArgs a) {
                 }
             }
         }
-        // sum over waves, then lane groups (the decode matmul's order)
+        // sum over waves of ((g0 + g1) + (g2 + g3)) (the decode matmul's order)
         __syncthreads();
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -1081,10 +1216,7 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide_q4k(GemvArgs a) {
             const int tk = threadIdx.x >> 4, r = threadIdx.x & 15;
             float v = 0.0F;
 #pragma unroll
-            for (int w = 0; w < W; ++w) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) v += red[w][g][tk][r];
-            }
+            for (int w = 0; w < W; ++w) v += (red[w][0][tk][r] + red[w][1][tk][r]) + (red[w][2][tk][r] + red[w][3][tk][r]);
             vals[16 * tt + tk][r] = v;
         }
     }
@@ -1443,7 +1575,6 @@ constexpr int kAttnRows = 16;
 
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 template <int HD>
 __device__ __forceinline__ void attn_mfma_load(global_ptr<const uint16_t> kc, global_ptr<const uint16_t> vt, int t0,
@@ -1730,11 +1861,12 @@ constexpr int kMmTargetWgs = JFH_MM_TARGET_WGS;
 constexpr size_t kMmOnePassLds = 64 * 1024;  // largest one-pass staging of a row that is not normalized
 constexpr size_t kMmMaxLds = 160 * 1024;
 
-size_t mm_lds_bytes(int nt, int chunk, int rgw) {
+size_t mm_lds_bytes(int nt, int chunk, int rgw, int K) {
     const size_t nbc = static_cast<size_t>(chunk) / 256;
+    const size_t part_rows = chunk >= K ? 16 : 64;  // one pass: combined lane groups (see k_mm)
     return static_cast<size_t>(nt) * chunk + nt * nbc * 4 + static_cast<size_t>(nt) * chunk / 8 +
-           static_cast<size_t>(rgw) * kMmWaves * 64 * nt * 4 + static_cast<size_t>(nt) * 4 + nt * nbc * 4 +
-           static_cast<size_t>(rgw) * 16 * nt * 4;
+           static_cast<size_t>(rgw) * kMmWaves * part_rows * nt * 4 + static_cast<size_t>(nt) * 4 + nt * nbc * 4 +
+           static_cast<size_t>(rgw) * 16 * nt * 4 + 16 + 64;  // + the aligned zero bytes
 }
 
 MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds) {
@@ -1745,10 +1877,12 @@ MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds) {
     // with two work-groups would set the kernel's time); larger matrices: two
     // work-groups per CU.
     const int wgs = n_rg <= 2 * kMmTargetWgs ? kMmTargetWgs : 2 * kMmTargetWgs;
-    int rgw = (n_rg + wgs - 1) / wgs;
-    const int cap = kMmPartBytes / (kMmWaves * 64 * nt * 4);
-    if (rgw > cap) rgw = cap;
-    if (rgw < 1) rgw = 1;
+    const int want = (n_rg + wgs - 1) / wgs;
+    // row groups per work-group within kMmPartBytes of row partials
+    auto rgw_for = [&](int chunk) {
+        const int cap = kMmPartBytes / (kMmWaves * (chunk >= K ? 16 : 64) * nt * 4);
+        return std::max(1, std::min(want, cap));
+    };
     // The whole row is staged in one pass when it fits (a normalized input
     // always is: its block scales need the full row's rms), else in passes of
     // kMmChunk values. Wave w takes tiles w, w + W, ... of the row either way
@@ -1756,17 +1890,20 @@ MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds) {
     // any sum.
     const bool normed = a.xq.q == nullptr && a.x.gain != nullptr;
     int chunk = K;
-    if (!normed && K > kMmChunk && mm_lds_bytes(nt, K, rgw) > kMmOnePassLds) chunk = kMmChunk;
-    if (!normed && mm_lds_bytes(nt, chunk, rgw) > kMmMaxLds) {
+    int rgw = rgw_for(chunk);
+    if (!normed && K > kMmChunk && mm_lds_bytes(nt, K, rgw, K) > kMmOnePassLds) chunk = kMmChunk;
+    rgw = rgw_for(chunk);
+    if (!normed && mm_lds_bytes(nt, chunk, rgw, K) > kMmMaxLds) {
         // wide token groups: shorter passes, in whole rounds of the waves' tiles, until the staging fits
         const int round = 256 * kMmWaves;
         chunk = std::min(chunk, kMmChunk) / round * round;
-        while (chunk > round && mm_lds_bytes(nt, chunk, rgw) > kMmMaxLds) chunk -= round;
+        rgw = rgw_for(chunk);
+        while (chunk > round && mm_lds_bytes(nt, chunk, rgw, K) > kMmMaxLds) chunk -= round;
     }
     MmGeom g;
     g.rgw = rgw;
     g.chunk = chunk;
-    lds = mm_lds_bytes(nt, chunk, rgw);
+    lds = mm_lds_bytes(nt, chunk, rgw, K);
     if (lds > kMmMaxLds) throw std::invalid_argument("matmul staging does not fit the LDS");
     return g;
 }
@@ -1785,6 +1922,14 @@ void mm(const GemvArgs& a, hipStream_t stream) {
 
 template <uint32_t TYPE>
 void mm_nt(const GemvArgs& a, hipStream_t stream) {
+    if constexpr (TYPE == 11) {
+        // int8 Q4_K rows from 3 tokens on: token quads on matrix cores
+        if (a.xq.q != nullptr && a.n_tok >= 3) {
+            if (a.n_tok <= 4) mm<TYPE, 4>(a, stream);
+            else mm<TYPE, 8>(a, stream);
+            return;
+        }
+    }
     switch (a.n_tok) {
     case 1: mm<TYPE, 1>(a, stream); break;
     case 2: mm<TYPE, 2>(a, stream); break;
