@@ -910,17 +910,18 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
     const int K = static_cast<int>(a.mat.cols), nb = K / 256;
     const int chunk = geo.chunk, nbc = chunk / 256, rgw = geo.rgw;
     const int n_tok = a.n_tok;
+    // staging for the step's n_tok rows (token slots past them are never read)
     int8_t* sq = reinterpret_cast<int8_t*>(lds_raw);
-    float* sd = reinterpret_cast<float*>(lds_raw + NT * chunk);
-    int16_t* ss = reinterpret_cast<int16_t*>(sd + NT * nbc);
+    float* sd = reinterpret_cast<float*>(lds_raw + n_tok * chunk);
+    int16_t* ss = reinterpret_cast<int16_t*>(sd + ((n_tok * nbc + 3) & ~3));  // 16-byte aligned
     // Row partials. One pass over K: each wave stores its finished row-group
     // sums with the four lane groups already combined, [rgw][W][16 rows][NT].
     // Several passes: every lane keeps running sums, [rgw][W][64 lanes][NT].
     const bool single = nbc >= nb;
-    float* part = reinterpret_cast<float*>(ss + NT * (chunk / 16));
+    float* part = reinterpret_cast<float*>(ss + n_tok * (chunk / 16));
     float* rs = part + (single ? rgw * W * 16 * NT : rgw * W * 64 * NT);
-    float* ssq = rs + NT;       // [NT][nbc] block sums of squares (normed inputs)
-    float* lv = ssq + NT * nbc;  // [rgw * 16 * NT]
+    float* ssq = rs + NT;       // [n_tok][nbc] block sums of squares (normed inputs)
+    float* lv = ssq + n_tok * nbc;  // [rgw * 16 * NT]
     // 64 zero bytes (16-byte aligned) for the masked operand slots of TileQ4Quad
     int8_t* zero = reinterpret_cast<int8_t*>(lds_raw) +
                    ((reinterpret_cast<uint8_t*>(lv + rgw * 16 * NT) - lds_raw + 15) & ~static_cast<ptrdiff_t>(15));
@@ -1861,11 +1862,12 @@ constexpr int kMmTargetWgs = JFH_MM_TARGET_WGS;
 constexpr size_t kMmOnePassLds = 64 * 1024;  // largest one-pass staging of a row that is not normalized
 constexpr size_t kMmMaxLds = 160 * 1024;
 
-size_t mm_lds_bytes(int nt, int chunk, int rgw, int K) {
+// LDS of k_mm: staging of n rows, row partials and epilogue values of nt token slots
+size_t mm_lds_bytes(int nt, int n, int chunk, int rgw, int K) {
     const size_t nbc = static_cast<size_t>(chunk) / 256;
     const size_t part_rows = chunk >= K ? 16 : 64;  // one pass: combined lane groups (see k_mm)
-    return static_cast<size_t>(nt) * chunk + nt * nbc * 4 + static_cast<size_t>(nt) * chunk / 8 +
-           static_cast<size_t>(rgw) * kMmWaves * part_rows * nt * 4 + static_cast<size_t>(nt) * 4 + nt * nbc * 4 +
+    return static_cast<size_t>(n) * chunk + (n * nbc + 3) / 4 * 16 + static_cast<size_t>(n) * chunk / 8 +
+           static_cast<size_t>(rgw) * kMmWaves * part_rows * nt * 4 + static_cast<size_t>(nt) * 4 + n * nbc * 4 +
            static_cast<size_t>(rgw) * 16 * nt * 4 + 16 + 64;  // + the aligned zero bytes
 }
 
@@ -1889,21 +1891,24 @@ MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds) {
     // and adds them in increasing order, so the pass length does not change
     // any sum.
     const bool normed = a.xq.q == nullptr && a.x.gain != nullptr;
+    const int n = a.n_tok;
     int chunk = K;
     int rgw = rgw_for(chunk);
-    if (!normed && K > kMmChunk && mm_lds_bytes(nt, K, rgw, K) > kMmOnePassLds) chunk = kMmChunk;
+    // A grid of at most one work-group per CU may use the whole LDS for one pass.
+    const size_t one_pass = (n_rg + rgw - 1) / rgw <= kMmTargetWgs ? kMmMaxLds : kMmOnePassLds;
+    if (!normed && K > kMmChunk && mm_lds_bytes(nt, n, K, rgw, K) > one_pass) chunk = kMmChunk;
     rgw = rgw_for(chunk);
-    if (!normed && mm_lds_bytes(nt, chunk, rgw, K) > kMmMaxLds) {
+    if (!normed && mm_lds_bytes(nt, n, chunk, rgw, K) > kMmMaxLds) {
         // wide token groups: shorter passes, in whole rounds of the waves' tiles, until the staging fits
         const int round = 256 * kMmWaves;
         chunk = std::min(chunk, kMmChunk) / round * round;
         rgw = rgw_for(chunk);
-        while (chunk > round && mm_lds_bytes(nt, chunk, rgw, K) > kMmMaxLds) chunk -= round;
+        while (chunk > round && mm_lds_bytes(nt, n, chunk, rgw, K) > kMmMaxLds) chunk -= round;
     }
     MmGeom g;
     g.rgw = rgw;
     g.chunk = chunk;
-    lds = mm_lds_bytes(nt, chunk, rgw, K);
+    lds = mm_lds_bytes(nt, n, chunk, rgw, K);
     if (lds > kMmMaxLds) throw std::invalid_argument("matmul staging does not fit the LDS");
     return g;
 }
