@@ -917,7 +917,7 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
     // Row partials. One pass over K: each wave stores its finished row-group
     // sums with the four lane groups already combined, [rgw][W][16 rows][NT].
     // Several passes: every lane keeps running sums, [rgw][W][64 lanes][NT].
-    const bool single = nbc >= nb;
+    const bool single = NT <= 2 || nbc >= nb;  // one- and two-token groups always run one pass (mm_geom)
     float* part = reinterpret_cast<float*>(ss + n_tok * (chunk / 16));
     float* rs = part + (single ? rgw * W * 16 * NT : rgw * W * 64 * NT);
     float* ssq = rs + NT;       // [n_tok][nbc] block sums of squares (normed inputs)
@@ -994,7 +994,9 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
     }
     // zero partials (waves without tiles, when the row has fewer blocks than waves, add nothing)
     for (int i = threadIdx.x; i < (single ? rgw * W * 16 * NT : rgw * W * 64 * NT); i += kMmThreads) part[i] = 0.0F;
-    if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(zero)[threadIdx.x] = 0u;
+    if constexpr (QUAD) {
+        if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(zero)[threadIdx.x] = 0u;
+    }
     if constexpr (A8) {
         stage_act8<kMmThreads>(a.xq, n_tok, 0, nbcur, sq, sd, ss, chunk, q0);
     } else {
@@ -1905,6 +1907,7 @@ MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds) {
         rgw = rgw_for(chunk);
         while (chunk > round && mm_lds_bytes(nt, n, chunk, rgw, K) > kMmMaxLds) chunk -= round;
     }
+    if (nt <= 2 && chunk < K) throw std::invalid_argument("one- and two-token matmul rows must fit one pass");
     MmGeom g;
     g.rgw = rgw;
     g.chunk = chunk;
