@@ -491,8 +491,8 @@ std::string gemv_label(const gpu::GemvArgs& a) {
     const uint32_t t = a.mat.type;
     const bool fl = t == kF32 || t == kF16;
     const int nt = a.n_tok > 8 ? 8 : a.n_tok;
-    // int8 Q4_K rows run in token quads (4 or 8 slots) from 3 tokens on
-    const bool quads = t == kQ4_K && a.xq.q != nullptr && nt >= 3;
+    // int8 Q4_K / Q6_K rows run in token quads (4 or 8 slots) from 3 tokens on
+    const bool quads = (t == kQ4_K || t == kQ6_K) && a.xq.q != nullptr && nt >= 3;
     const int slot = nt <= 2 ? nt : nt <= 4 ? 4 : nt <= 6 && !quads ? 6 : 8;
     if (fl) return "k_gemv_f<" + std::to_string(nt) + ">";
     // template arguments of the launched kernel: type, token slots, input kind
@@ -932,7 +932,7 @@ void Engine::matmul(const std::string& name, const float* x_host, uint32_t n_tok
     // Q4_K from 3 rows on: quantized once, then the matrix-core paths a step takes (token quads up to 8
     // rows, the wide kernel beyond)
     const bool wide = n_tok > 8 && gpu::wide_matmul_supported(m.type) && m.cols % 256 == 0;
-    const bool quads = n_tok >= 3 && m.type == kQ4_K && m.cols % 256 == 0;
+    const bool quads = n_tok >= 3 && (m.type == kQ4_K || m.type == kQ6_K) && m.cols % 256 == 0;
     gpu::Act8 xq;
     uint8_t* xq_mem = nullptr;
     auto release = [&] {

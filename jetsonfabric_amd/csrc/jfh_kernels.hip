@@ -569,7 +569,7 @@ struct Tile<13> {
                     for (int q = 0; q < 4; ++q) dm = sdot4(w[4 * m + q], xw[4 * m + q], dm);
                     isum += mul24(sc[m], dm - 32 * s[m]);
                 }
-                acc[t] += x.d[tc * x.d_stride] * (d * static_cast<float>(isum));
+                acc[t] = __builtin_fmaf(x.d[tc * x.d_stride], d * static_cast<float>(isum), acc[t]);
             }
         }
     }
@@ -742,6 +742,81 @@ struct TileQ4Quad {
     }
 };
 
+// Q6_K tiles x 4..8 int8 token rows on matrix cores, with the operand layout
+// of TileQ4Quad: one MFMA per 8-value chunk, two chunks per 16-value
+// sub-block, so D holds sub-block dots of lane group G' per (token, row); the
+// scale and offset arithmetic per lane group is Tile<13>::dot's.
+struct TileQ6Quad {
+    struct Regs {
+        uint4 c0, c1, c2, sc;
+        uint32_t d;
+    };
+    static __device__ __forceinline__ Regs load(const uint8_t* t, int lane) {
+        Regs r;
+        r.c0 = *reinterpret_cast<const uint4*>(t + 288 + 16 * lane);
+        r.c1 = *reinterpret_cast<const uint4*>(t + 1312 + 16 * lane);
+        r.c2 = *reinterpret_cast<const uint4*>(t + 2336 + 16 * lane);
+        r.sc = *reinterpret_cast<const uint4*>(t + 32 + 16 * (lane & 15));
+        r.d = *reinterpret_cast<const uint16_t*>(t + 2 * (lane & 15));
+        return r;
+    }
+    template <int NT>
+    static __device__ __forceinline__ void dot(const Regs& r, int L, const XLds& x, int nt, float* acc,
+                                               const int8_t* zero) {
+        static_assert(NT % 4 == 0, "token quads");
+        constexpr int NQ = NT / 4;
+        const int i = threadIdx.x & 15;
+        const float d = h2f(r.d);
+        const uint32_t Lw[8] = {r.c0.x, r.c0.y, r.c0.z, r.c0.w, r.c1.x, r.c1.y, r.c1.z, r.c1.w};
+        const uint32_t Hb[4] = {r.c2.x, r.c2.y, r.c2.z, r.c2.w};
+        const uint32_t scw[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};  // row i's scales of lane groups 0..3
+        constexpr uint32_t M4 = 0x0F0F0F0Fu, M30 = 0x30303030u;
+        long b[8];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint32_t w0 = (Lw[2 * m] & M4) | ((Hb[m] << 4) & M30);
+            const uint32_t w1 = ((Lw[2 * m] >> 4) & M4) | ((Hb[m] << 2) & M30);
+            const uint32_t w2 = (Lw[2 * m + 1] & M4) | (Hb[m] & M30);
+            const uint32_t w3 = ((Lw[2 * m + 1] >> 4) & M4) | ((Hb[m] >> 2) & M30);
+            b[2 * m] = static_cast<long>(static_cast<uint64_t>(w0) | (static_cast<uint64_t>(w1) << 32));
+            b[2 * m + 1] = static_cast<long>(static_cast<uint64_t>(w2) | (static_cast<uint64_t>(w3) << 32));
+        }
+        const bool own = (i & 3) == L;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int ta = min(4 * q + (i >> 2), nt - 1);
+            const u32x4* src = reinterpret_cast<const u32x4*>(own ? x.q + ta * x.q_stride : zero);
+            const u32x4 c0 = src[0], c1 = src[1], c2 = src[2], c3 = src[3];
+            const u32x2 a[8] = {{c0.x, c0.y}, {c0.z, c0.w}, {c1.x, c1.y}, {c1.z, c1.w},
+                                {c2.x, c2.y}, {c2.z, c2.w}, {c3.x, c3.y}, {c3.z, c3.w}};
+            i32x4 D[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const i32x4 z = {0, 0, 0, 0};
+                D[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a[2 * m]), b[2 * m], z, 0, 0, 0);
+                D[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a[2 * m + 1]), b[2 * m + 1], D[m],
+                                                            0, 0, 0);
+            }
+            const int tk = min(4 * q + L, nt - 1);
+            const float xd = x.d[tk * x.d_stride];
+            const u32x4* sp = reinterpret_cast<const u32x4*>(x.s + tk * x.s_stride);
+            const u32x4 s03 = sp[0], s47 = sp[1];
+            const uint32_t sw[8] = {s03.x, s03.y, s03.z, s03.w, s47.x, s47.y, s47.z, s47.w};
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                int isum = 0;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const int j = 4 * g + m;  // sub-block of the block
+                    const int sj = static_cast<int16_t>((sw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+                    isum += mul24(sext8(scw[g] >> (8 * m)), D[m][g] - 32 * sj);
+                }
+                acc[4 * q + g] = __builtin_fmaf(xd, d * static_cast<float>(isum), acc[4 * q + g]);
+            }
+        }
+    }
+};
+
 __device__ __forceinline__ unsigned long long pack_best(float v, uint32_t idx) {
     uint32_t u = __float_as_uint(v);
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -900,9 +975,9 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
     constexpr bool A8 = IN == kInAct8;
     constexpr bool GAIN = IN == kInNormed;
     constexpr int NB = GAIN ? kStageBatch : kStageBatchFloat;  // blocks per wave of a float staging batch
-    // int8 Q4_K rows in token quads run on matrix cores (TileQ4Quad)
-    constexpr bool QUAD = TYPE == 11 && A8 && NT % 4 == 0;
-    using T = std::conditional_t<QUAD, TileQ4Quad, Tile<TYPE>>;
+    // int8 Q4_K / Q6_K rows in token quads run on matrix cores (TileQ4Quad, TileQ6Quad)
+    constexpr bool QUAD = (TYPE == 11 || TYPE == 13) && A8 && NT % 4 == 0;
+    using T = std::conditional_t<QUAD, std::conditional_t<TYPE == 11, TileQ4Quad, TileQ6Quad>, Tile<TYPE>>;
     using Regs = typename T::Regs;
     constexpr int W = kMmWaves;
     constexpr uint32_t TB = tile_bytes(TYPE);
@@ -1294,15 +1369,16 @@ __global__ __launch_bounds__(256) void k_quantize(const float* x, int32_t stride
 // codes and scales the normalized-input matmul prologue stages (stage_f32
 // with a gain, then finish_norm), computed the same way (prefill steps).
 constexpr int kNormMaxBlocks = 128;
+constexpr int kNormThreads = 1024;  // a wave per block for rows up to 4096 values
 #pragma clang fp contract(off)
-__global__ __launch_bounds__(256) void k_quantize_norm(const float* x, int32_t stride, const int32_t* gather,
+__global__ __launch_bounds__(kNormThreads) void k_quantize_norm(const float* x, int32_t stride, const int32_t* gather,
                                                        const float* gain, float eps, Act8 out) {
     __shared__ float ssq[kNormMaxBlocks], db[kNormMaxBlocks];
     __shared__ float rs;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int row = blockIdx.x, nb = out.K / 256;
     const float* xr = x + static_cast<size_t>(gather ? gather[row] : row) * stride;
-    for (int b = wave; b < nb; b += 4) {
+    for (int b = wave; b < nb; b += kNormThreads / kWave) {
         const f32x4 v4 = *reinterpret_cast<const f32x4*>(xr + b * 256 + 4 * lane);
         const f32x4 g4 = *reinterpret_cast<const f32x4*>(gain + b * 256 + 4 * lane);
         float vv[4] = {v4.x, v4.y, v4.z, v4.w};
@@ -1322,7 +1398,7 @@ __global__ __launch_bounds__(256) void k_quantize_norm(const float* x, int32_t s
         rs = 1.0F / sqrtf(sum / static_cast<float>(out.K) + eps);
     }
     __syncthreads();
-    for (int b = threadIdx.x; b < nb; b += 256) out.d[static_cast<size_t>(row) * nb + b] = db[b] * rs;
+    for (int b = threadIdx.x; b < nb; b += kNormThreads) out.d[static_cast<size_t>(row) * nb + b] = db[b] * rs;
 }
 #pragma clang fp contract(on)
 
@@ -1930,8 +2006,8 @@ void mm(const GemvArgs& a, hipStream_t stream) {
 
 template <uint32_t TYPE>
 void mm_nt(const GemvArgs& a, hipStream_t stream) {
-    if constexpr (TYPE == 11) {
-        // int8 Q4_K rows from 3 tokens on: token quads on matrix cores
+    if constexpr (TYPE == 11 || TYPE == 13) {
+        // int8 Q4_K / Q6_K rows from 3 tokens on: token quads on matrix cores
         if (a.xq.q != nullptr && a.n_tok >= 3) {
             if (a.n_tok <= 4) mm<TYPE, 4>(a, stream);
             else mm<TYPE, 8>(a, stream);
@@ -2030,7 +2106,7 @@ void launch_quantize_norm(const float* x, int32_t stride, const int32_t* gather,
     if (out.K % 256 != 0 || out.K / 256 > kNormMaxBlocks || stride % 4 != 0 || gain == nullptr) {
         throw std::invalid_argument("normalized quantization needs rows of a multiple of 256 values and a gain");
     }
-    launch(k_quantize_norm, dim3(n_rows), dim3(256), 0, stream, x, stride, gather, gain, eps, out);
+    launch(k_quantize_norm, dim3(n_rows), dim3(kNormThreads), 0, stream, x, stride, gather, gain, eps, out);
     check(hipGetLastError(), "normalized quantize launch");
 }
 
