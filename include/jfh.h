@@ -285,6 +285,24 @@ jfh_status jfh_generate(jfh_engine * engine, const int32_t * prompt, uint32_t n_
                         uint32_t draft_max, uint32_t max_ngram, uint32_t min_ngram, int32_t * out_tokens,
                         uint32_t * out_count, jfh_generation_stats * stats);
 
+/* Continuous-batching generation: n_requests GenerationRunner loops (as
+ * jfh_generate, one thread each) over one HIP stage executor wrapped in the
+ * ContinuousBatchingExecutor the reference worker installs when
+ * --decode-batch-size > 1 (runtime/engine/builtin_inference_engines.cpp:117-123;
+ * batching: runtime/pipeline_parallel/continuous_batching_executor.cpp:14-200):
+ * concurrent decode steps are coalesced, up to n_requests per step, waiting at
+ * most batch_wait_us for a batch to fill, into one multi-sequence forward.
+ * prompts holds the requests' prompts back to back (prompt_lengths[i] ids
+ * each); out_tokens receives max_tokens slots per request, out_counts and
+ * stats (optional) one entry per request. The runners' decode phases start
+ * together once every prefill is done; decode_wall_ms (optional) is the time
+ * from that start until the last runner finishes. n_requests 1..8. */
+jfh_status jfh_generate_concurrent(jfh_engine * engine, uint32_t n_requests, const int32_t * prompts,
+                                   const uint32_t * prompt_lengths, uint32_t max_tokens, uint32_t draft_max,
+                                   uint32_t max_ngram, uint32_t min_ngram, uint32_t batch_wait_us,
+                                   int32_t * out_tokens, uint32_t * out_counts, jfh_generation_stats * stats,
+                                   double * decode_wall_ms);
+
 #ifdef __cplusplus
 }
 #endif

@@ -133,6 +133,9 @@ SIGNATURES = {
                                            POINTER(c_uint32), POINTER(c_uint32)]),
     "jfh_generate": (Status, [c_void_p, POINTER(c_int32), c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
                               POINTER(c_int32), POINTER(c_uint32), POINTER(GenerationStats)]),
+    "jfh_generate_concurrent": (Status, [c_void_p, c_uint32, POINTER(c_int32), POINTER(c_uint32), c_uint32, c_uint32,
+                                         c_uint32, c_uint32, c_uint32, POINTER(c_int32), POINTER(c_uint32),
+                                         POINTER(GenerationStats), POINTER(c_double)]),
 }
 
 STATUS_NAMES = {0: "ok", 1: "invalid_argument", 2: "io_error", 3: "format_error", 4: "not_found",

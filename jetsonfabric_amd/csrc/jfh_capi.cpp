@@ -6,10 +6,16 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
+#include <chrono>
+#include <condition_variable>
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <new>
+#include <string>
+#include <thread>
 
 struct jfh_model {
     std::unique_ptr<jfh::HostModel> model;
@@ -579,6 +585,109 @@ jfh_status jfh_generate(jfh_engine* engine, const int32_t* prompt, uint32_t n_pr
             stats->time_to_first_token_ms = r.time_to_first_token_ms;
             stats->decode_ms = r.decode_ms;
         }
+    });
+}
+
+jfh_status jfh_generate_concurrent(jfh_engine* engine, uint32_t n_requests, const int32_t* prompts,
+                                   const uint32_t* prompt_lengths, uint32_t max_tokens, uint32_t draft_max,
+                                   uint32_t max_ngram, uint32_t min_ngram, uint32_t batch_wait_us,
+                                   int32_t* out_tokens, uint32_t* out_counts, jfh_generation_stats* stats,
+                                   double* decode_wall_ms) {
+    return guarded([&] {
+        require(engine && prompts && prompt_lengths && out_tokens && out_counts && max_tokens > 0,
+                "generation arguments are required");
+        require(n_requests >= 1 && n_requests <= 8, "requests must be 1..8");
+        require(draft_max <= 8, "draft length must be 0..8");
+        require(n_requests * (draft_max + 1) <= static_cast<uint32_t>(jfh::gpu::kMaxRows),
+                "the requests' verify rows must fit one step");
+        namespace rt = jfh::runtime;
+        const jfh::ModelParams& p = engine->engine->params();
+        std::vector<std::vector<int32_t>> req_prompts(n_requests);
+        uint64_t longest = 0;
+        for (uint32_t i = 0, o = 0; i < n_requests; o += prompt_lengths[i], ++i) {
+            require(prompt_lengths[i] > 0, "every request needs a prompt");
+            req_prompts[i].assign(prompts + o, prompts + o + prompt_lengths[i]);
+            longest = std::max<uint64_t>(longest, prompt_lengths[i]);
+        }
+        rt::adapters::HipStageConfig cfg;
+        cfg.engine = engine->engine;
+        cfg.tokenizer = std::make_shared<rt::tokenization::IdTokenizer>();
+        cfg.ctx_size = static_cast<int>(std::min<uint64_t>(p.n_ctx, longest + max_tokens));
+        cfg.position = {0, 1};
+        cfg.layers = {0, static_cast<int>(p.n_layer)};
+        cfg.speculative_max_tokens = static_cast<int>(draft_max);
+        std::unique_ptr<rt::inference::Executor> executor = std::make_unique<rt::adapters::HipStageExecutor>(cfg);
+        if (n_requests > 1) {
+            rt::pipeline_parallel::ContinuousBatchingConfig bc;
+            bc.max_batch_size = n_requests;
+            bc.max_wait = std::chrono::microseconds(batch_wait_us);
+            executor = std::make_unique<rt::pipeline_parallel::ContinuousBatchingExecutor>(std::move(executor), bc);
+        }
+        std::unique_ptr<rt::speculative::PromptLookupDraft> draft;
+        if (draft_max > 0) draft = std::make_unique<rt::speculative::PromptLookupDraft>(max_ngram, min_ngram);
+
+        // decode phases start together: the last runner to finish its prefill releases the others
+        using clock = std::chrono::steady_clock;
+        std::mutex gate_mutex;
+        std::condition_variable gate;
+        uint32_t waiting = n_requests;
+        clock::time_point decode_start;
+        auto arrive = [&] {
+            std::unique_lock lock(gate_mutex);
+            if (--waiting == 0) {
+                decode_start = clock::now();
+                gate.notify_all();
+            } else {
+                gate.wait(lock, [&] { return waiting == 0; });
+            }
+        };
+        std::vector<rt::GenerationResult> results(n_requests);
+        std::vector<clock::time_point> finished(n_requests);
+        std::vector<std::thread> runners;
+        for (uint32_t i = 0; i < n_requests; ++i) {
+            runners.emplace_back([&, i] {
+                bool arrived = false;
+                rt::GenerationRequest req;
+                req.session_id = "session-" + std::to_string(i);
+                req.request_id = "request-" + std::to_string(i);
+                req.prompt = req_prompts[i];
+                req.max_tokens = static_cast<int>(max_tokens);
+                req.layer_count = static_cast<int>(p.n_layer);
+                req.after_prefill = [&] {
+                    arrived = true;
+                    arrive();
+                };
+                try {
+                    results[i] = rt::run_generation(*executor, req, draft.get(), static_cast<int>(draft_max));
+                } catch (const std::exception& e) {
+                    results[i].ok = false;
+                    results[i].error_code = "generation_failed";
+                    results[i].error_message = e.what();
+                }
+                if (!arrived) arrive();  // a runner that failed before decoding must not hold the others
+                finished[i] = clock::now();
+            });
+        }
+        for (std::thread& t : runners) t.join();
+        clock::time_point last = decode_start;
+        for (uint32_t i = 0; i < n_requests; ++i) {
+            const rt::GenerationResult& r = results[i];
+            if (!r.ok) throw jfh::Error(jfh::Status::InvalidArgument, r.error_code + ": " + r.error_message);
+            for (size_t k = 0; k < r.sampled_tokens.size(); ++k) {
+                out_tokens[static_cast<size_t>(i) * max_tokens + k] = static_cast<int32_t>(r.sampled_tokens[k]);
+            }
+            out_counts[i] = static_cast<uint32_t>(r.sampled_tokens.size());
+            if (stats) {
+                stats[i].completion_tokens = static_cast<uint32_t>(r.completion_tokens);
+                stats[i].target_decode_passes = static_cast<uint32_t>(r.target_decode_passes);
+                stats[i].speculative_draft_tokens = static_cast<uint32_t>(r.speculative_draft_tokens);
+                stats[i].speculative_accepted_tokens = static_cast<uint32_t>(r.speculative_accepted_tokens);
+                stats[i].time_to_first_token_ms = r.time_to_first_token_ms;
+                stats[i].decode_ms = r.decode_ms;
+            }
+            last = std::max(last, finished[i]);
+        }
+        if (decode_wall_ms) *decode_wall_ms = std::chrono::duration<double, std::milli>(last - decode_start).count();
     });
 }
 

@@ -9,8 +9,13 @@
 namespace jfh {
 namespace {
 
-// Token rows up to which the down projection reads the float SwiGLU output.
-constexpr int32_t kFloatDownRows = 2;
+// Token rows up to which the down projection reads the float SwiGLU output
+// (from 2 rows on, quantizing them once costs less than in every work-group).
+constexpr int32_t kFloatDownRows = 1;
+// Token rows up to which matmuls normalize their input in the prologue (from
+// 3 rows on, the rows are normalized and quantized once, as the token-quad
+// matrix-core path takes int8 rows).
+constexpr int32_t kNormedPrologueRows = 2;
 
 void hip_check(hipError_t e, const char* what) {
     if (e != hipSuccess) throw Error(Status::DeviceError, std::string(what) + ": " + hipGetErrorString(e));
@@ -572,7 +577,7 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
     // (the same codes the matmul prologue would stage): a draft-verify group
     // then stages int8 rows instead of normalizing them in every work-group.
     auto normed = [&](gpu::GemvArgs& a, const float* gain) {
-        if (n_rows > 1 && quantized(a.mat.type) && xq_norm_.q) {
+        if (n_rows > kNormedPrologueRows && quantized(a.mat.type) && xq_norm_.q) {
             timed("k_quantize_norm", n * H * 9.1,
                   [&] { gpu::launch_quantize_norm(h_, H, nullptr, gain, p.rms_eps, n_rows, xq_norm_, s); });
             a.xq = xq_norm_;
@@ -644,7 +649,7 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         head.n_tok = n_out;
         const int32_t* out_rows =
             reinterpret_cast<const int32_t*>(reinterpret_cast<const char*>(step_dev_) + offsetof(gpu::StepDev, out_row));
-        if (n_out > 1 && quantized(head.mat.type) && xq_norm_.q) {
+        if (n_out > kNormedPrologueRows && quantized(head.mat.type) && xq_norm_.q) {
             // several logits rows (draft verify, batches): normalized and quantized once
             timed("k_quantize_norm", n_out * H * 9.1, [&] {
                 gpu::launch_quantize_norm(h_, H, out_rows, output_norm_, p.rms_eps, n_out, xq_norm_, s);

@@ -4,9 +4,13 @@
 
 #include <algorithm>
 #include <chrono>
+#include <condition_variable>
+#include <deque>
+#include <future>
 #include <limits>
 #include <map>
 #include <stdexcept>
+#include <thread>
 
 namespace jfh::runtime {
 
@@ -558,6 +562,7 @@ GenerationResult run_generation(const inference::Executor& executor, const Gener
         previous = token;
     };
     if (!eog) emit(first.tokens[0]);
+    if (request.after_prefill) request.after_prefill();
 
     const auto t1 = clock::now();
     while (result.completion_tokens < request.max_tokens && !eog) {
@@ -611,5 +616,141 @@ GenerationResult run_generation(const inference::Executor& executor, const Gener
     result.finish_reason = eog ? "stop" : "length";
     return result;
 }
+
+// ------------------------------------------------------------------ continuous batching
+namespace pipeline_parallel {
+
+struct ContinuousBatchingExecutor::Impl {
+    struct Pending {
+        inference::StageInput input;
+        std::promise<inference::ExecutionResult> done;
+    };
+
+    std::unique_ptr<inference::Executor> delegate;
+    ContinuousBatchingConfig config;
+    std::mutex delegate_mutex;
+    std::mutex queue_mutex;
+    std::condition_variable queued;
+    std::deque<std::shared_ptr<Pending>> queue;
+    bool stopping = false;
+    std::thread worker;
+
+    Impl(std::unique_ptr<inference::Executor> d, ContinuousBatchingConfig c) : delegate(std::move(d)), config(c) {
+        if (!delegate) throw std::invalid_argument("continuous batching requires a layer executor");
+        if (config.max_batch_size < 2) throw std::invalid_argument("continuous batching size must be at least two");
+        if (config.max_wait < std::chrono::microseconds::zero()) {
+            throw std::invalid_argument("continuous batching wait must not be negative");
+        }
+        worker = std::thread([this] { serve(); });
+    }
+
+    ~Impl() {
+        {
+            std::lock_guard lock(queue_mutex);
+            stopping = true;
+        }
+        queued.notify_all();
+        worker.join();
+    }
+
+    inference::ExecutionResult submit(const inference::StageInput& input) {
+        if (input.phase == inference::Phase::Prefill) {
+            // prefill is not held back behind decoders
+            std::lock_guard lock(delegate_mutex);
+            return delegate->execute(input);
+        }
+        auto pending = std::make_shared<Pending>();
+        pending->input = input;
+        std::future<inference::ExecutionResult> result = pending->done.get_future();
+        {
+            std::lock_guard lock(queue_mutex);
+            if (stopping) {
+                return inference::ExecutionResult::failure("continuous_batch_stopped",
+                                                           "continuous batching executor stopped before execution");
+            }
+            queue.push_back(std::move(pending));
+        }
+        queued.notify_all();
+        return result.get();
+    }
+
+    // Waits for a first queued step, then up to max_wait for the batch to
+    // fill; takes at most max_batch_size steps in arrival order.
+    std::vector<std::shared_ptr<Pending>> take_batch() {
+        std::unique_lock lock(queue_mutex);
+        queued.wait(lock, [this] { return stopping || !queue.empty(); });
+        if (stopping) return {};
+        queued.wait_until(lock, std::chrono::steady_clock::now() + config.max_wait,
+                          [this] { return stopping || queue.size() >= config.max_batch_size; });
+        if (stopping) return {};
+        std::vector<std::shared_ptr<Pending>> batch;
+        while (!queue.empty() && batch.size() < config.max_batch_size) {
+            batch.push_back(std::move(queue.front()));
+            queue.pop_front();
+        }
+        return batch;
+    }
+
+    void serve() {
+        for (;;) {
+            std::vector<std::shared_ptr<Pending>> batch = take_batch();
+            if (batch.empty()) break;
+            std::vector<inference::StageInput> inputs;
+            inputs.reserve(batch.size());
+            for (const auto& p : batch) inputs.push_back(p->input);
+            std::vector<inference::ExecutionResult> results;
+            try {
+                std::lock_guard lock(delegate_mutex);
+                results = delegate->execute_batch(inputs);
+            } catch (const std::exception& e) {
+                results.assign(inputs.size(), inference::ExecutionResult::failure("continuous_batch_failed", e.what()));
+            }
+            if (results.size() != batch.size()) {
+                results.assign(batch.size(), inference::ExecutionResult::failure(
+                                                 "continuous_batch_result_mismatch",
+                                                 "layer executor returned the wrong number of batch results"));
+            }
+            for (std::size_t i = 0; i < batch.size(); ++i) batch[i]->done.set_value(std::move(results[i]));
+        }
+        // whatever is still queued when the executor stops fails
+        std::deque<std::shared_ptr<Pending>> left;
+        {
+            std::lock_guard lock(queue_mutex);
+            left.swap(queue);
+        }
+        for (const auto& p : left) {
+            p->done.set_value(inference::ExecutionResult::failure(
+                "continuous_batch_stopped", "continuous batching executor stopped before execution"));
+        }
+    }
+};
+
+ContinuousBatchingExecutor::ContinuousBatchingExecutor(std::unique_ptr<inference::Executor> delegate,
+                                                       ContinuousBatchingConfig config)
+    : impl_(std::make_unique<Impl>(std::move(delegate), config)) {}
+
+ContinuousBatchingExecutor::~ContinuousBatchingExecutor() = default;
+
+inference::ExecutionResult ContinuousBatchingExecutor::execute(const inference::StageInput& input) const {
+    return impl_->submit(input);
+}
+
+std::vector<inference::ExecutionResult> ContinuousBatchingExecutor::execute_batch(
+    const std::vector<inference::StageInput>& inputs) const {
+    std::lock_guard lock(impl_->delegate_mutex);
+    return impl_->delegate->execute_batch(inputs);
+}
+
+void ContinuousBatchingExecutor::close_session(const std::string& session_id) const {
+    std::lock_guard lock(impl_->delegate_mutex);
+    impl_->delegate->close_session(session_id);
+}
+
+void ContinuousBatchingExecutor::rollback_session(const std::string& session_id, int token_count) const {
+    std::lock_guard lock(impl_->delegate_mutex);
+    impl_->delegate->rollback_session(session_id, token_count);
+}
+
+}  // namespace pipeline_parallel
 
 }  // namespace jfh::runtime

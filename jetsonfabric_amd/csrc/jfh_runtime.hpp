@@ -13,11 +13,16 @@
 //     (runtime/adapters/llama_cpp_stage_adapter.cpp:350-475, 895-937)
 //   run_generation -- GenerationRunner::run for one local stage
 //     (runtime/pipeline_parallel/generation_runner.cpp:398-566)
+//   pipeline_parallel::ContinuousBatchingExecutor -- coalesces concurrent
+//     decode steps into execute_batch calls
+//     (runtime/pipeline_parallel/continuous_batching_executor.{hpp,cpp})
 #pragma once
 
 #include "jfh_engine.hpp"
 
+#include <chrono>
 #include <cstdint>
+#include <functional>
 #include <memory>
 #include <mutex>
 #include <span>
@@ -207,6 +212,10 @@ struct GenerationRequest {
     std::vector<std::int32_t> prompt;
     int max_tokens = 16;
     int layer_count = 0;
+    // Called once after the prefill's token is read and before the first
+    // decode pass (no counterpart in the reference runner: it lets a caller
+    // start the decode phases of several runners together).
+    std::function<void()> after_prefill;
 };
 
 struct GenerationResult {
@@ -226,5 +235,37 @@ struct GenerationResult {
 // GenerationRunner::run restricted to one local stage that owns every layer.
 GenerationResult run_generation(const inference::Executor& executor, const GenerationRequest& request,
                                 const speculative::DraftStrategy* draft, int speculative_max_tokens);
+
+namespace pipeline_parallel {
+
+// continuous_batching_executor.hpp:11-14
+struct ContinuousBatchingConfig {
+    std::size_t max_batch_size = 1;
+    std::chrono::microseconds max_wait = std::chrono::microseconds(500);
+};
+
+// Coalesces concurrently arriving decode steps: a worker thread takes up to
+// max_batch_size queued decode inputs (waiting at most max_wait for the batch
+// to fill once one is queued) and runs them as one delegate execute_batch.
+// Prefill runs immediately on the caller's thread. Same contract and error
+// codes as the reference (continuous_batching_executor.cpp:14-200).
+class ContinuousBatchingExecutor final : public inference::Executor {
+public:
+    ContinuousBatchingExecutor(std::unique_ptr<inference::Executor> delegate, ContinuousBatchingConfig config);
+    ~ContinuousBatchingExecutor() override;
+    ContinuousBatchingExecutor(const ContinuousBatchingExecutor&) = delete;
+    ContinuousBatchingExecutor& operator=(const ContinuousBatchingExecutor&) = delete;
+
+    inference::ExecutionResult execute(const inference::StageInput& input) const override;
+    std::vector<inference::ExecutionResult> execute_batch(const std::vector<inference::StageInput>& inputs) const override;
+    void close_session(const std::string& session_id) const override;
+    void rollback_session(const std::string& session_id, int token_count) const override;
+
+private:
+    struct Impl;
+    std::unique_ptr<Impl> impl_;
+};
+
+}  // namespace pipeline_parallel
 
 }  // namespace jfh::runtime

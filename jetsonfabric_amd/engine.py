@@ -440,6 +440,34 @@ class NativeEngine:
         )
 
 
+    def generate_concurrent(self, prompts: Sequence[Sequence[int]], max_tokens: int, draft_max: int = 0,
+                            max_ngram: int = 4, min_ngram: int = 2, batch_wait_us: int = 500):
+        """Concurrent GenerationRunner loops over a continuous-batching executor
+        (continuous_batching_executor.cpp:14-200); returns (results per prompt,
+        decode wall ms from the common decode start to the last finish)."""
+        n = len(prompts)
+        flat = [t for p in prompts for t in p]
+        lengths = (ctypes.c_uint32 * n)(*[len(p) for p in prompts])
+        out = (ctypes.c_int32 * (n * max_tokens))()
+        counts = (ctypes.c_uint32 * n)()
+        stats = (_capi.GenerationStats * n)()
+        wall = ctypes.c_double()
+        check(library().jfh_generate_concurrent(self._h, n, _i32(flat), lengths, max_tokens, draft_max, max_ngram,
+                                                min_ngram, batch_wait_us, out, counts, stats, ctypes.byref(wall)))
+        results = []
+        for i in range(n):
+            st = stats[i]
+            results.append(GenerationResult(
+                sampled_tokens=[int(x) for x in out[i * max_tokens:i * max_tokens + counts[i]]],
+                time_to_first_token_ms=st.time_to_first_token_ms,
+                decode_ms=st.decode_ms,
+                target_decode_passes=int(st.target_decode_passes),
+                speculative_draft_tokens=int(st.speculative_draft_tokens),
+                speculative_accepted_tokens=int(st.speculative_accepted_tokens),
+            ))
+        return results, wall.value
+
+
 def prompt_lookup_propose(history: Sequence[int], max_tokens: int, max_ngram: int = 4, min_ngram: int = 2) -> list[int]:
     """PromptLookupDraft::propose through the C ABI (prompt_lookup_draft.cpp:15-44)."""
     hist = (ctypes.c_uint32 * max(1, len(history)))(*history)

@@ -1,14 +1,19 @@
 // Host-side tests of the speculative runtime (no GPU): prompt-lookup
 // drafting, the greedy acceptance / rollback loop over a scripted executor,
-// and the stage payload helpers. Mirrors the reference's own cases in
-// runtime/speculative/prompt_lookup_draft_test.cpp:15-36 and
-// runtime/pipeline_parallel/generation_runner_test.cpp:108-190, 355-430.
+// the continuous-batching executor, and the stage payload helpers. Mirrors
+// the reference's own cases in
+// runtime/speculative/prompt_lookup_draft_test.cpp:15-36,
+// runtime/pipeline_parallel/generation_runner_test.cpp:108-190, 355-430 and
+// runtime/pipeline_parallel/continuous_batching_executor_test.cpp.
 #include "jfh_runtime.hpp"
 
+#include <chrono>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
 using namespace jfh::runtime;
@@ -171,6 +176,116 @@ void test_payloads() {
     expect(!inference::validate_stage_input(in).empty(), "missing session id rejected");
 }
 
+// Answers decode rows with row + 1 and records the batches it is handed.
+class BatchRecorder final : public inference::Executor {
+public:
+    mutable std::mutex mutex;
+    mutable std::vector<std::size_t> batches;
+    mutable int prefills = 0, closes = 0, rollbacks = 0;
+    bool fail_batches = false;
+
+    inference::ExecutionResult execute(const inference::StageInput& in) const override {
+        inference::StageOutput out;
+        const std::vector<std::int32_t> rows = inference::decode_token_ids(in.payload);
+        if (in.phase == inference::Phase::Prefill) {
+            ++prefills;
+            out.payload = inference::sampled_token_payload(7);
+        } else {
+            out.payload = inference::sampled_token_payload(rows.at(0) + 1);
+        }
+        return inference::ExecutionResult::success(out);
+    }
+    std::vector<inference::ExecutionResult> execute_batch(
+        const std::vector<inference::StageInput>& inputs) const override {
+        {
+            std::lock_guard lock(mutex);
+            batches.push_back(inputs.size());
+        }
+        if (fail_batches) throw std::runtime_error("injected batch failure");
+        std::vector<inference::ExecutionResult> out;
+        for (const auto& in : inputs) out.push_back(execute(in));
+        return out;
+    }
+    void close_session(const std::string&) const override { ++closes; }
+    void rollback_session(const std::string&, int) const override { ++rollbacks; }
+};
+
+inference::StageInput step_input(inference::Phase phase, const std::string& session, std::int32_t token) {
+    inference::StageInput in;
+    in.session_id = session;
+    in.request_id = "r-" + session;
+    in.model_id = "m";
+    in.phase = phase;
+    in.decode_step = phase == inference::Phase::Prefill ? 0 : 1;
+    in.position = {0, 1};
+    in.layers = {0, 1};
+    const std::int32_t t[1] = {token};
+    in.payload = inference::tokens_payload(std::span<const std::int32_t>(t, 1));
+    in.max_tokens = 4;
+    return in;
+}
+
+void test_continuous_batching() {
+    using pipeline_parallel::ContinuousBatchingConfig;
+    using pipeline_parallel::ContinuousBatchingExecutor;
+    using std::chrono::microseconds;
+    // two concurrent decode steps run as one batch
+    {
+        auto rec = std::make_unique<BatchRecorder>();
+        const BatchRecorder* r = rec.get();
+        ContinuousBatchingExecutor ex(std::move(rec), ContinuousBatchingConfig{2, microseconds(2000000)});
+        inference::ExecutionResult a, b;
+        std::thread ta([&] { a = ex.execute(step_input(inference::Phase::Decode, "a", 10)); });
+        std::thread tb([&] { b = ex.execute(step_input(inference::Phase::Decode, "b", 20)); });
+        ta.join();
+        tb.join();
+        expect(a.ok && b.ok, "batched decode results are ok");
+        expect(inference::decode_token_ids(a.output.payload) == std::vector<std::int32_t>{11}, "first result is its own");
+        expect(inference::decode_token_ids(b.output.payload) == std::vector<std::int32_t>{21}, "second result is its own");
+        expect(r->batches == std::vector<std::size_t>{2}, "two concurrent steps form one batch of two");
+        // prefill is immediate and bypasses the batcher; rollback and close pass through
+        const inference::ExecutionResult p = ex.execute(step_input(inference::Phase::Prefill, "c", 1));
+        expect(p.ok && r->prefills == 1 && r->batches.size() == 1, "prefill runs immediately");
+        ex.rollback_session("a", 1);
+        ex.close_session("a");
+        expect(r->rollbacks == 1 && r->closes == 1, "rollback and close reach the delegate");
+    }
+    // a lone step runs as a batch of one after the wait
+    {
+        auto rec = std::make_unique<BatchRecorder>();
+        const BatchRecorder* r = rec.get();
+        ContinuousBatchingExecutor ex(std::move(rec), ContinuousBatchingConfig{2, microseconds(3000)});
+        const auto t0 = std::chrono::steady_clock::now();
+        const inference::ExecutionResult a = ex.execute(step_input(inference::Phase::Decode, "a", 5));
+        const double waited = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+        expect(a.ok && r->batches == std::vector<std::size_t>{1}, "a lone step runs alone");
+        expect(waited >= 3000.0, "a lone step waits for the batch to fill");
+    }
+    // delegate failures reach every step of the batch
+    {
+        auto rec = std::make_unique<BatchRecorder>();
+        rec->fail_batches = true;
+        ContinuousBatchingExecutor ex(std::move(rec), ContinuousBatchingConfig{2, microseconds(0)});
+        const inference::ExecutionResult a = ex.execute(step_input(inference::Phase::Decode, "a", 5));
+        expect(!a.ok && a.error.code == "continuous_batch_failed", "batch failure is reported per step");
+    }
+    // configuration errors
+    bool threw = false;
+    try {
+        ContinuousBatchingExecutor ex(std::make_unique<BatchRecorder>(), ContinuousBatchingConfig{1, microseconds(0)});
+    } catch (const std::invalid_argument&) {
+        threw = true;
+    }
+    expect(threw, "batch size one is rejected");
+    threw = false;
+    try {
+        ContinuousBatchingExecutor ex(nullptr, ContinuousBatchingConfig{2, microseconds(0)});
+    } catch (const std::invalid_argument&) {
+        threw = true;
+    }
+    expect(threw, "a missing delegate is rejected");
+}
+
 }  // namespace
 
 int main() {
@@ -179,6 +294,7 @@ int main() {
     test_recovery_pass_after_rejection();
     test_rollback_failure_emits_nothing_rejected();
     test_payloads();
+    test_continuous_batching();
     if (failures) {
         std::printf("%d runtime check(s) failed\n", failures);
         return 1;

@@ -256,6 +256,28 @@ def test_speculative_generation_is_greedy_invariant(q4k):
     assert stats["speculative_accepted_tokens"] == spec.speculative_accepted_tokens
 
 
+@pytest.mark.parametrize("draft", [0, 4])
+def test_concurrent_generation_equals_each_alone(q4k, draft):
+    """Continuous batching of 3 runners (decode steps coalesced into one
+    multi-sequence forward) produces every request's tokens and speculation
+    counters exactly as that request generated alone."""
+    model, engine, _ = q4k
+    prompts = []
+    for i in range(3):
+        seg = _prompt(12 + 2 * i, SMALL.n_vocab, 40 + i)
+        prompts.append(seg + seg + seg[: 5 + i])  # repetitive: prompt lookup finds drafts
+    results, wall_ms = engine.generate_concurrent(prompts, 20, draft_max=draft, max_ngram=3, min_ngram=3,
+                                                  batch_wait_us=2000)
+    assert wall_ms > 0.0
+    for prompt, got in zip(prompts, results):
+        alone = engine.generate(prompt, 20, draft_max=draft, max_ngram=3, min_ngram=3)
+        assert got.sampled_tokens == alone.sampled_tokens
+        assert got.target_decode_passes == alone.target_decode_passes
+        assert got.speculative_accepted_tokens == alone.speculative_accepted_tokens
+    if draft:
+        assert sum(r.speculative_accepted_tokens for r in results) > 0
+
+
 def test_invalid_inputs_raise(q4k):
     model, engine, _ = q4k
     s = engine.create_session(8)
