@@ -1732,10 +1732,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_mfma(const float* __
     f32x4 o[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) o[d] = f32x4{0.0F, 0.0F, 0.0F, 0.0F};
-    for (; t0 < k1; t0 += W * R) {
-        u32x4 krn[KS];
-        u32x2 vrn[DB];
-        attn_mfma_load<HD>(kc, vt, t0 + W * R, capacity, r, grp, krn, vrn);
+    // one 16-key tile of the wave at t0 from kr / vr
+    auto tile = [&](int t0) {
         f32x4 sc = {0.0F, 0.0F, 0.0F, 0.0F};
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
@@ -1776,11 +1774,19 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_mfma(const float* __
             o[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, phi, o[d], 0, 0, 0);
             o[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, plo, o[d], 0, 0, 0);
         }
+    };
+    // a wave with several tiles keeps the next one in flight; its last tile requests nothing more
+    for (; t0 + W * R < k1; t0 += W * R) {
+        u32x4 krn[KS];
+        u32x2 vrn[DB];
+        attn_mfma_load<HD>(kc, vt, t0 + W * R, capacity, r, grp, krn, vrn);
+        tile(t0);
 #pragma unroll
         for (int s = 0; s < KS; ++s) kr[s] = krn[s];
 #pragma unroll
         for (int d = 0; d < DB; ++d) vr[d] = vrn[d];
     }
+    if (t0 < k1) tile(t0);
     // the row's sum over its four lanes, then the waves merged in LDS
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
