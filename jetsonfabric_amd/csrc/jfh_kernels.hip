@@ -1087,53 +1087,62 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
             float* slot = part + (wave * 64 + lane) * NT;          // the lane's running sums of that row group
             float* done = part + (wave * 16 + (lane & 15)) * NT;   // its finished sums (one pass)
             const int8_t* xq0 = sq + wave * 256 + 64 * grp;         // its activation slice
-            for (int n0 = 0; n0 < total; n0 += kMmDepth) {
+            // one item of the wave's stream (its tile cm of the current row group) from slot u of the ring
+            auto consume = [&](const Regs& tile_regs) {
+                if (cm == 0) {
 #pragma unroll
-                for (int u = 0; u < kMmDepth; ++u) {
-                    if (n0 + u < total) {
-                        if (cm == 0) {
+                    for (int t = 0; t < NT; ++t) acc[t] = single ? 0.0F : slot[t];
+                }
+                const int bl = wave + W * cm;
+                XLds x;
+                x.q = xq0 + W * 256 * cm;
+                x.d = sd + bl;
+                x.s = ss + bl * 16;
+                x.q_stride = chunk;
+                x.d_stride = nbc;
+                x.s_stride = chunk / 16;
+                if constexpr (QUAD) T::template dot<NT>(tile_regs, grp, x, n_tok, acc, zero);
+                else T::template dot<NT>(tile_regs, grp, x, n_tok, acc);
+                if (++cm == pr) {
+                    cm = 0;
+                    if (single) {
+                        // (g0 + g1) + (g2 + g3) of the row's four lane-group sums
+                        if constexpr (QUAD) {
 #pragma unroll
-                            for (int t = 0; t < NT; ++t) acc[t] = single ? 0.0F : slot[t];
-                        }
-                        const int bl = wave + W * cm;
-                        XLds x;
-                        x.q = xq0 + W * 256 * cm;
-                        x.d = sd + bl;
-                        x.s = ss + bl * 16;
-                        x.q_stride = chunk;
-                        x.d_stride = nbc;
-                        x.s_stride = chunk / 16;
-                        if constexpr (QUAD) T::template dot<NT>(ring[u], grp, x, n_tok, acc, zero);
-                        else T::template dot<NT>(ring[u], grp, x, n_tok, acc);
-                        if (++cm == pr) {
-                            cm = 0;
-                            if (single) {
-                                // (g0 + g1) + (g2 + g3) of the row's four lane-group sums
-                                if constexpr (QUAD) {
+                            for (int q = 0; q < NT / 4; ++q) {
+                                done[4 * q + grp] =
+                                    (acc[4 * q] + acc[4 * q + 1]) + (acc[4 * q + 2] + acc[4 * q + 3]);
+                            }
+                        } else {
 #pragma unroll
-                                    for (int q = 0; q < NT / 4; ++q) {
-                                        done[4 * q + grp] =
-                                            (acc[4 * q] + acc[4 * q + 1]) + (acc[4 * q + 2] + acc[4 * q + 3]);
-                                    }
-                                } else {
-#pragma unroll
-                                    for (int t = 0; t < NT; ++t) {
-                                        float v = acc[t];
-                                        v += __shfl_xor(v, 16);
-                                        v += __shfl_xor(v, 32);
-                                        if (grp == 0) done[t] = v;
-                                    }
-                                }
-                                done += W * 16 * NT;
-                            } else {
-#pragma unroll
-                                for (int t = 0; t < NT; ++t) slot[t] = acc[t];
-                                slot += W * 64 * NT;
+                            for (int t = 0; t < NT; ++t) {
+                                float v = acc[t];
+                                v += __shfl_xor(v, 16);
+                                v += __shfl_xor(v, 32);
+                                if (grp == 0) done[t] = v;
                             }
                         }
+                        done += W * 16 * NT;
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < NT; ++t) slot[t] = acc[t];
+                        slot += W * 64 * NT;
                     }
+                }
+            };
+            // Items whose ring slot is refilled with a later item; the last
+            // kMmDepth items are consumed without further loads.
+            int n0 = 0;
+            for (; n0 + kMmDepth < total; n0 += kMmDepth) {
+#pragma unroll
+                for (int u = 0; u < kMmDepth; ++u) {
+                    consume(ring[u]);
                     load_next(ring[u]);
                 }
+            }
+#pragma unroll
+            for (int u = 0; u < kMmDepth; ++u) {
+                if (n0 + u < total) consume(ring[u]);
             }
         }
         c0b += nbc;
