@@ -496,9 +496,10 @@ std::string gemv_label(const gpu::GemvArgs& a) {
     const uint32_t t = a.mat.type;
     const bool fl = t == kF32 || t == kF16;
     const int nt = a.n_tok > 8 ? 8 : a.n_tok;
-    // int8 Q4_K / Q6_K rows run in token quads (4 or 8 slots) from 3 tokens on
-    const bool quads = (t == kQ4_K || t == kQ6_K) && a.xq.q != nullptr && nt >= 3;
-    const int slot = nt <= 2 ? nt : nt <= 4 ? 4 : nt <= 6 && !quads ? 6 : 8;
+    // int8 or normalized Q4_K / Q6_K rows run in token quads (4 or 8 slots)
+    const bool quads = (t == kQ4_K || t == kQ6_K) && (a.xq.q != nullptr || a.x.gain != nullptr) &&
+                       nt >= gpu::kQuadMinRows;
+    const int slot = quads ? (nt <= 4 ? 4 : 8) : nt <= 2 ? nt : nt <= 4 ? 4 : nt <= 6 ? 6 : 8;
     if (fl) return "k_gemv_f<" + std::to_string(nt) + ">";
     // template arguments of the launched kernel: type, token slots, input kind
     // (0 int8 rows, 1 RMS-normalized float rows, 2 float rows)

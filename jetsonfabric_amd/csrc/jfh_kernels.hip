@@ -975,8 +975,8 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
     constexpr bool A8 = IN == kInAct8;
     constexpr bool GAIN = IN == kInNormed;
     constexpr int NB = GAIN ? kStageBatch : kStageBatchFloat;  // blocks per wave of a float staging batch
-    // int8 Q4_K / Q6_K rows in token quads run on matrix cores (TileQ4Quad, TileQ6Quad)
-    constexpr bool QUAD = (TYPE == 11 || TYPE == 13) && A8 && NT % 4 == 0;
+    // int8 or normalized Q4_K / Q6_K rows in token quads run on matrix cores (TileQ4Quad, TileQ6Quad)
+    constexpr bool QUAD = (TYPE == 11 || TYPE == 13) && (A8 || GAIN) && NT % 4 == 0;
     using T = std::conditional_t<QUAD, std::conditional_t<TYPE == 11, TileQ4Quad, TileQ6Quad>, Tile<TYPE>>;
     using Regs = typename T::Regs;
     constexpr int W = kMmWaves;
@@ -2022,8 +2022,8 @@ void mm(const GemvArgs& a, hipStream_t stream) {
 template <uint32_t TYPE>
 void mm_nt(const GemvArgs& a, hipStream_t stream) {
     if constexpr (TYPE == 11 || TYPE == 13) {
-        // int8 Q4_K / Q6_K rows from 3 tokens on: token quads on matrix cores
-        if (a.xq.q != nullptr && a.n_tok >= 3) {
+        // int8 or normalized Q4_K / Q6_K rows from kQuadMinRows tokens on: token quads on matrix cores
+        if ((a.xq.q != nullptr || a.x.gain != nullptr) && a.n_tok >= kQuadMinRows) {
             if (a.n_tok <= 4) mm<TYPE, 4>(a, stream);
             else mm<TYPE, 8>(a, stream);
             return;

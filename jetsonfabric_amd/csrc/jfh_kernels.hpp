@@ -9,7 +9,13 @@
 
 namespace jfh::gpu {
 
-constexpr int kMaxRows = 64;        // token rows of one step (sum over sequences)
+constexpr int kMaxRows = 64;
+// Q4_K / Q6_K token groups of at least this many rows (int8 or RMS-normalized
+// input) run as token quads on matrix cores.
+#ifndef JFH_QUAD_MIN_ROWS
+#define JFH_QUAD_MIN_ROWS 2
+#endif
+constexpr int kQuadMinRows = JFH_QUAD_MIN_ROWS;        // token rows of one step (sum over sequences)
 constexpr int kMaxSeq = 16;         // sequences of one batched step
 constexpr int kActBlock = 256;      // activation quantization block (values)
 constexpr int kTileRows = 16;       // rows of one weight tile
