@@ -496,9 +496,8 @@ std::string gemv_label(const gpu::GemvArgs& a) {
     const uint32_t t = a.mat.type;
     const bool fl = t == kF32 || t == kF16;
     const int nt = a.n_tok > 8 ? 8 : a.n_tok;
-    // int8 or normalized Q4_K / Q6_K rows run in token quads (4 or 8 slots)
-    const bool quads = (t == kQ4_K || t == kQ6_K) && (a.xq.q != nullptr || a.x.gain != nullptr) &&
-                       nt >= gpu::kQuadMinRows;
+    // int8 or normalized rows of the quantized formats run in token quads (4 or 8 slots)
+    const bool quads = quantized(t) && (a.xq.q != nullptr || a.x.gain != nullptr) && nt >= gpu::kQuadMinRows;
     const int slot = quads ? (nt <= 4 ? 4 : 8) : nt <= 2 ? nt : nt <= 4 ? 4 : nt <= 6 ? 6 : 8;
     if (fl) return "k_gemv_f<" + std::to_string(nt) + ">";
     // template arguments of the launched kernel: type, token slots, input kind
@@ -935,10 +934,10 @@ void Engine::matmul(const std::string& name, const float* x_host, uint32_t n_tok
         fail(Status::OutOfMemory, "allocate matmul output");
     }
     std::vector<float> full(static_cast<size_t>(n_tok) * m.rows);
-    // Q4_K from 3 rows on: quantized once, then the matrix-core paths a step takes (token quads up to 8
-    // rows, the wide kernel beyond)
+    // quantized formats from 3 rows on: quantized once, then the matrix-core paths a step takes (token
+    // quads up to 8 rows, the wide kernel beyond, where the format has one)
     const bool wide = n_tok > 8 && gpu::wide_matmul_supported(m.type) && m.cols % 256 == 0;
-    const bool quads = n_tok >= 3 && (m.type == kQ4_K || m.type == kQ6_K) && m.cols % 256 == 0;
+    const bool quads = n_tok >= 3 && quantized(m.type) && m.cols % 256 == 0;
     gpu::Act8 xq;
     uint8_t* xq_mem = nullptr;
     auto release = [&] {

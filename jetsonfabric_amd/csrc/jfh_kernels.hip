@@ -464,6 +464,12 @@ __device__ __forceinline__ float q4k_term(float acc, float xd, float d, float dm
     return __builtin_fmaf(xd, t, acc);
 }
 
+// A Q8_0 tile's share of one lane group (two GGML blocks) for one token:
+// acc + xd * (da * ia + db * ib), with the fused products as written.
+__device__ __forceinline__ float q8_term(float acc, float xd, float da, float db, int ia, int ib) {
+    return __builtin_fmaf(xd, __builtin_fmaf(da, static_cast<float>(ia), db * static_cast<float>(ib)), acc);
+}
+
 // Q4_K: header of row i | codes: the lane's 32 qs bytes (sub-blocks 2g, 2g+1).
 // The lane reads d|dmin and the 8 header bytes that hold its 24-bit scale
 // field (header byte 4 + 3g) starting at the enclosing word.
@@ -609,7 +615,7 @@ struct Tile<7> {
                     ia = sdot4(w[k], xw[k], ia);
                     ib = sdot4(w[8 + k], xw[8 + k], ib);
                 }
-                acc[t] += x.d[tc * x.d_stride] * (da * static_cast<float>(ia) + db * static_cast<float>(ib));
+                acc[t] = q8_term(acc[t], x.d[tc * x.d_stride], da, db, ia, ib);
             }
         }
     }
@@ -657,7 +663,7 @@ struct Tile<9> {
                     isum += mul24(sc[m], dm);
                     msum += mul24(mn[m], s[m]);
                 }
-                acc[t] += x.d[tc * x.d_stride] * (d * static_cast<float>(isum) - dmin * static_cast<float>(msum));
+                acc[t] = q4k_term(acc[t], x.d[tc * x.d_stride], d, dmin, isum, msum);
             }
         }
     }
@@ -817,6 +823,160 @@ struct TileQ6Quad {
     }
 };
 
+// Q8_0 tiles x 4..8 int8 token rows on matrix cores, with the operand layout
+// of TileQ4Quad: the lane group's 64 codes are eight 8-value chunks, chunks
+// 0..3 (GGML block 2 G') accumulate into D0 and chunks 4..7 (block 2 G' + 1)
+// into D1; the float step per lane group is Tile<7>::dot's.
+struct TileQ8Quad {
+    struct Regs {
+        uint4 c[4];
+        uint4 sc;  // row i's eight block scales (f16)
+    };
+    static __device__ __forceinline__ Regs load(const uint8_t* t, int lane) {
+        Regs r;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) r.c[u] = *reinterpret_cast<const uint4*>(t + 256 + 1024 * u + 16 * lane);
+        r.sc = *reinterpret_cast<const uint4*>(t + 16 * (lane & 15));
+        return r;
+    }
+    template <int NT>
+    static __device__ __forceinline__ void dot(const Regs& r, int L, const XLds& x, int nt, float* acc,
+                                               const int8_t* zero) {
+        static_assert(NT % 4 == 0, "token quads");
+        constexpr int NQ = NT / 4;
+        const int i = threadIdx.x & 15;
+        const uint32_t scw[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};  // (da, db) of lane groups 0..3
+        long b[8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            b[2 * u] = static_cast<long>(static_cast<uint64_t>(r.c[u].x) | (static_cast<uint64_t>(r.c[u].y) << 32));
+            b[2 * u + 1] =
+                static_cast<long>(static_cast<uint64_t>(r.c[u].z) | (static_cast<uint64_t>(r.c[u].w) << 32));
+        }
+        const bool own = (i & 3) == L;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int ta = min(4 * q + (i >> 2), nt - 1);
+            const u32x4* src = reinterpret_cast<const u32x4*>(own ? x.q + ta * x.q_stride : zero);
+            const u32x4 c0 = src[0], c1 = src[1], c2 = src[2], c3 = src[3];
+            const u32x2 a[8] = {{c0.x, c0.y}, {c0.z, c0.w}, {c1.x, c1.y}, {c1.z, c1.w},
+                                {c2.x, c2.y}, {c2.z, c2.w}, {c3.x, c3.y}, {c3.z, c3.w}};
+            i32x4 D0 = {0, 0, 0, 0}, D1 = {0, 0, 0, 0};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                D0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a[c]), b[c], D0, 0, 0, 0);
+                D1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a[4 + c]), b[4 + c], D1, 0, 0, 0);
+            }
+            const int tk = min(4 * q + L, nt - 1);
+            const float xd = x.d[tk * x.d_stride];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float da = h2f(scw[g]), db = h2f(scw[g] >> 16);
+                acc[4 * q + g] = q8_term(acc[4 * q + g], xd, da, db, D0[g], D1[g]);
+            }
+        }
+    }
+};
+
+// Q2_K tiles x 4..8 int8 token rows on matrix cores, with the operand layout
+// of TileQ4Quad: chunk c (values 8 c .. 8 c + 7 of the lane group) is the
+// 2-bit fields 4 (c % 2) and 4 (c % 2) + 2 of code word c / 2, two chunks per
+// 16-value sub-block, so D[m] holds sub-block m's dot of lane group G' per
+// (token, row); the scale and minimum arithmetic per lane group is
+// Tile<9>::dot's.
+struct TileQ2Quad {
+    struct Regs {
+        uint4 c, sc;
+        uint32_t dd;
+    };
+    static __device__ __forceinline__ Regs load(const uint8_t* t, int lane) {
+        Regs r;
+        r.c = *reinterpret_cast<const uint4*>(t + 320 + 16 * lane);
+        r.sc = *reinterpret_cast<const uint4*>(t + 64 + 16 * (lane & 15));
+        r.dd = *reinterpret_cast<const uint32_t*>(t + 4 * (lane & 15));
+        return r;
+    }
+    template <int NT>
+    static __device__ __forceinline__ void dot(const Regs& r, int L, const XLds& x, int nt, float* acc,
+                                               const int8_t* zero) {
+        static_assert(NT % 4 == 0, "token quads");
+        constexpr int NQ = NT / 4;
+        const int i = threadIdx.x & 15;
+        const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
+        const uint32_t Q[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
+        const uint32_t scw[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};  // row i's scale bytes of lane groups 0..3
+        constexpr uint32_t M2 = 0x03030303u;
+        long b[8];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t lo = (Q[m] >> (4 * h)) & M2, hi = (Q[m] >> (4 * h + 2)) & M2;
+                b[2 * m + h] = static_cast<long>(static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32));
+            }
+        }
+        const bool own = (i & 3) == L;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int ta = min(4 * q + (i >> 2), nt - 1);
+            const u32x4* src = reinterpret_cast<const u32x4*>(own ? x.q + ta * x.q_stride : zero);
+            const u32x4 c0 = src[0], c1 = src[1], c2 = src[2], c3 = src[3];
+            const u32x2 a[8] = {{c0.x, c0.y}, {c0.z, c0.w}, {c1.x, c1.y}, {c1.z, c1.w},
+                                {c2.x, c2.y}, {c2.z, c2.w}, {c3.x, c3.y}, {c3.z, c3.w}};
+            i32x4 D[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const i32x4 z = {0, 0, 0, 0};
+                D[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a[2 * m]), b[2 * m], z, 0, 0, 0);
+                D[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a[2 * m + 1]), b[2 * m + 1], D[m],
+                                                            0, 0, 0);
+            }
+            const int tk = min(4 * q + L, nt - 1);
+            const float xd = x.d[tk * x.d_stride];
+            const u32x4* sp = reinterpret_cast<const u32x4*>(x.s + tk * x.s_stride);
+            const u32x4 s03 = sp[0], s47 = sp[1];
+            const uint32_t sw[8] = {s03.x, s03.y, s03.z, s03.w, s47.x, s47.y, s47.z, s47.w};
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                int isum = 0, msum = 0;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const int j = 4 * g + m;  // sub-block of the block
+                    const int sj = static_cast<int16_t>((sw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+                    const uint32_t byte = scw[g] >> (8 * m);
+                    isum += mul24(static_cast<int>(byte & 0xF), D[m][g]);
+                    msum += mul24(static_cast<int>((byte >> 4) & 0xF), sj);
+                }
+                acc[4 * q + g] = q4k_term(acc[4 * q + g], xd, d, dmin, isum, msum);
+            }
+        }
+    }
+};
+
+// The token-quad tile of a weight format (void: none).
+template <uint32_t TYPE>
+struct QuadTile {
+    using type = void;
+};
+template <>
+struct QuadTile<7> {
+    using type = TileQ8Quad;
+};
+template <>
+struct QuadTile<9> {
+    using type = TileQ2Quad;
+};
+template <>
+struct QuadTile<11> {
+    using type = TileQ4Quad;
+};
+template <>
+struct QuadTile<13> {
+    using type = TileQ6Quad;
+};
+template <uint32_t TYPE>
+constexpr bool kHasQuads = !std::is_void_v<typename QuadTile<TYPE>::type>;
+
 __device__ __forceinline__ unsigned long long pack_best(float v, uint32_t idx) {
     uint32_t u = __float_as_uint(v);
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -975,9 +1135,9 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
     constexpr bool A8 = IN == kInAct8;
     constexpr bool GAIN = IN == kInNormed;
     constexpr int NB = GAIN ? kStageBatch : kStageBatchFloat;  // blocks per wave of a float staging batch
-    // int8 or normalized Q4_K / Q6_K rows in token quads run on matrix cores (TileQ4Quad, TileQ6Quad)
-    constexpr bool QUAD = (TYPE == 11 || TYPE == 13) && (A8 || GAIN) && NT % 4 == 0;
-    using T = std::conditional_t<QUAD, std::conditional_t<TYPE == 11, TileQ4Quad, TileQ6Quad>, Tile<TYPE>>;
+    // int8 or normalized rows of a format with a token-quad tile, in token quads, run on matrix cores
+    constexpr bool QUAD = kHasQuads<TYPE> && (A8 || GAIN) && NT % 4 == 0;
+    using T = std::conditional_t<QUAD, typename QuadTile<TYPE>::type, Tile<TYPE>>;
     using Regs = typename T::Regs;
     constexpr int W = kMmWaves;
     constexpr uint32_t TB = tile_bytes(TYPE);
@@ -2021,8 +2181,8 @@ void mm(const GemvArgs& a, hipStream_t stream) {
 
 template <uint32_t TYPE>
 void mm_nt(const GemvArgs& a, hipStream_t stream) {
-    if constexpr (TYPE == 11 || TYPE == 13) {
-        // int8 or normalized Q4_K / Q6_K rows from kQuadMinRows tokens on: token quads on matrix cores
+    if constexpr (kHasQuads<TYPE>) {
+        // int8 or normalized rows from kQuadMinRows tokens on: token quads on matrix cores
         if ((a.xq.q != nullptr || a.x.gain != nullptr) && a.n_tok >= kQuadMinRows) {
             if (a.n_tok <= 4) mm<TYPE, 4>(a, stream);
             else mm<TYPE, 8>(a, stream);

@@ -10,8 +10,9 @@
 namespace jfh::gpu {
 
 constexpr int kMaxRows = 64;
-// Q4_K / Q6_K token groups of at least this many rows (int8 or RMS-normalized
-// input) run as token quads on matrix cores.
+// Token groups of at least this many rows (int8 or RMS-normalized input) of
+// the quantized formats (Q4_K, Q6_K, Q8_0, Q2_K) run as token quads on matrix
+// cores.
 #ifndef JFH_QUAD_MIN_ROWS
 #define JFH_QUAD_MIN_ROWS 2
 #endif

@@ -94,9 +94,9 @@ def test_matmul_matches_oracle(typed, n_tok):
 
 @pytest.mark.parametrize("n_tok", [3, 4, 5, 8, 9, 33, 64])
 def test_wide_matmul_rows_equal_single_rows(typed, n_tok):
-    """Steps of 3 or more int8 rows run Q4_K matrices on matrix cores (token
-    quads up to 8 rows, the wide kernel beyond); every row must equal the same
-    row computed alone (the decode path), bit for bit."""
+    """Steps of 3 or more int8 rows run every quantized format on matrix cores
+    (token quads up to 8 rows; for Q4_K the wide kernel beyond); every row must
+    equal the same row computed alone (the decode path), bit for bit."""
     t, model, engine = typed
     rng = np.random.default_rng(100 + n_tok)
     for name in ("blk.0.attn_q.weight", "blk.1.ffn_down.weight"):
