@@ -9,13 +9,13 @@
 namespace jfh {
 namespace {
 
-// Token rows up to which the down projection reads the float SwiGLU output
-// (from 2 rows on, quantizing them once costs less than in every work-group).
-constexpr int32_t kFloatDownRows = 1;
 // Token rows up to which matmuls normalize their input in the prologue (from
 // 3 rows on, the rows are normalized and quantized once, as the token-quad
 // matrix-core path takes int8 rows).
-constexpr int32_t kNormedPrologueRows = 2;
+#ifndef JFH_NORMED_PROLOGUE_ROWS
+#define JFH_NORMED_PROLOGUE_ROWS 2
+#endif
+constexpr int32_t kNormedPrologueRows = JFH_NORMED_PROLOGUE_ROWS;
 
 void hip_check(hipError_t e, const char* what) {
     if (e != hipSuccess) throw Error(Status::DeviceError, std::string(what) + ": " + hipGetErrorString(e));
@@ -625,15 +625,19 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         gu.y = ffn_;
         gu.y_stride = F;
         matmul(gu, "ffn_gate_up");
+        // The down projection reads the SwiGLU rows quantized once by
+        // k_quantize: the codes its float prologue would stage, where every
+        // work-group would quantize the whole row again (slower, also for a
+        // single row).
+        const bool int8_down = xq_ffn_.q && quantized(L.down->mat.type);
+        if (int8_down) {
+            timed("k_quantize", n * F * 5.1, [&] { gpu::launch_quantize(ffn_, F, n_rows, xq_ffn_, s); });
+        }
         gpu::GemvArgs dn;
         dn.mat = L.down->mat;
         dn.mode = gpu::kAdd;
         dn.n_tok = n_rows;
-        // Decode steps stage the float SwiGLU rows directly (the matmul
-        // quantizes them in its prologue); larger steps quantize them once.
-        // Both use the same block quantization, so the codes are identical.
-        if (xq_ffn_.q && quantized(dn.mat.type) && n_rows > kFloatDownRows) {
-            timed("k_quantize", n * F * 5.1, [&] { gpu::launch_quantize(ffn_, F, n_rows, xq_ffn_, s); });
+        if (int8_down) {
             dn.xq = xq_ffn_;
         } else {
             dn.x = {ffn_, F, nullptr, nullptr, 0.0F};
