@@ -99,6 +99,10 @@ typedef struct jfh_engine_info {
     uint64_t weight_bytes;
     uint32_t prefill_chunk;
     char device_name[128];
+    /* resident layer range [layer_start, layer_end) of the model's n_layer
+     * (ModelInfo::resident_layer_start/end, native_inference.hpp:30-40) */
+    uint32_t layer_start;
+    uint32_t layer_end;
 } jfh_engine_info;
 
 /* ---------------------------------------------------------------- formats */
@@ -213,6 +217,33 @@ jfh_status jfh_session_decode(jfh_session * session, int32_t token, int32_t * ou
  * logits may be NULL, else n * n_vocab floats. */
 jfh_status jfh_session_verify(jfh_session * session, const int32_t * tokens, uint32_t n, int32_t * out_tokens,
                               uint32_t * out_accepted, float * logits);
+
+/* Pipeline stages. An engine created from a model opened with a layer range
+ * runs only those layers (LayerRange, model_architecture.hpp:15-21): the
+ * first stage (layer_start 0) takes token ids, later stages take the
+ * previous stage's activations, f32 [n][n_embd] (the residual stream after
+ * its last layer); the last stage (layer_end n_layer) writes the greedy id of
+ * the last row to out_token, earlier stages write every row's activations to
+ * out_activations. Pass NULL for the unused input and output.
+ * NativeSession::prefill_stage_tokens / prefill_stage_activations
+ * (native_inference.hpp:112-113; qwen2_architecture.cpp:909-926, 977-1002). */
+jfh_status jfh_session_stage_prefill(jfh_session * session, const int32_t * tokens, const float * activations,
+                                     uint32_t n, int32_t * out_token, float * out_activations);
+/* One row: NativeSession::decode_stage_token / decode_stage_activation
+ * (native_inference.hpp:114-115; qwen2_architecture.cpp:928-947, 1004-1027).
+ * token points to the first stage's input id (NULL on later stages). */
+jfh_status jfh_session_stage_decode(jfh_session * session, const int32_t * token, const float * activation,
+                                    int32_t * out_token, float * out_activation);
+
+/* Activation codecs between pipeline stages (ActivationCodec, created by
+ * name from the default factory: runtime/activation/activation_codec.hpp:9-18,
+ * activation_codec_factory.cpp:24-46, builtin_activation_codecs.cpp:112-209).
+ * "f32" carries the values unchanged, "f16" as little-endian IEEE binary16
+ * (round to nearest even; NaNs quieted). encode writes n values' wire bytes
+ * (out_size must be n * 2 or n * 4); decode reads size bytes into size / 2 or
+ * size / 4 floats. */
+jfh_status jfh_activation_encode(const char * codec, const float * values, size_t n, void * out, size_t out_size);
+jfh_status jfh_activation_decode(const char * codec, const void * data, size_t size, float * values, size_t n);
 
 /* NativeSession::rollback (native_inference.hpp:116; qwen2_architecture.cpp:818-823). */
 jfh_status jfh_session_rollback(jfh_session * session, uint32_t n);

@@ -59,7 +59,8 @@ class EngineOptions(ctypes.Structure):
 
 
 class EngineInfo(ctypes.Structure):
-    _fields_ = [("weight_bytes", c_uint64), ("prefill_chunk", c_uint32), ("device_name", c_char * 128)]
+    _fields_ = [("weight_bytes", c_uint64), ("prefill_chunk", c_uint32), ("device_name", c_char * 128),
+                ("layer_start", c_uint32), ("layer_end", c_uint32)]
 
 
 class GenerationStats(ctypes.Structure):
@@ -121,6 +122,12 @@ SIGNATURES = {
     "jfh_session_verify": (Status, [c_void_p, POINTER(c_int32), c_uint32, POINTER(c_int32), POINTER(c_uint32),
                                     POINTER(c_float)]),
     "jfh_session_rollback": (Status, [c_void_p, c_uint32]),
+    "jfh_activation_encode": (Status, [c_char_p, POINTER(c_float), c_size_t, c_void_p, c_size_t]),
+    "jfh_activation_decode": (Status, [c_char_p, c_void_p, c_size_t, POINTER(c_float), c_size_t]),
+    "jfh_session_stage_prefill": (Status, [c_void_p, POINTER(c_int32), POINTER(c_float), c_uint32, POINTER(c_int32),
+                                           POINTER(c_float)]),
+    "jfh_session_stage_decode": (Status, [c_void_p, POINTER(c_int32), POINTER(c_float), POINTER(c_int32),
+                                          POINTER(c_float)]),
     "jfh_engine_step_batch": (Status, [c_void_p, POINTER(c_void_p), c_uint32, POINTER(c_int32), POINTER(c_uint32),
                                        POINTER(c_int32), POINTER(c_uint32)]),
     "jfh_engine_dequantize": (Status, [c_void_p, c_char_p, c_uint32, c_uint32, POINTER(c_float)]),

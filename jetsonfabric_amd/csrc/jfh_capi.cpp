@@ -358,6 +358,8 @@ jfh_status jfh_engine_get_info(const jfh_engine* engine, jfh_engine_info* out) {
         out->weight_bytes = engine->engine->weight_bytes();
         out->prefill_chunk = engine->engine->max_prefill_chunk();
         std::snprintf(out->device_name, sizeof(out->device_name), "%s", engine->engine->device_name().c_str());
+        out->layer_start = engine->engine->layer_start();
+        out->layer_end = engine->engine->layer_end();
     });
 }
 
@@ -417,6 +419,63 @@ jfh_status jfh_session_verify(jfh_session* session, const int32_t* tokens, uint3
         int32_t accepted = 0;
         session->owner->engine->forward({st}, out_tokens, &accepted, logits);
         if (out_accepted) *out_accepted = static_cast<uint32_t>(accepted);
+    });
+}
+
+jfh_status jfh_session_stage_prefill(jfh_session* session, const int32_t* tokens, const float* activations,
+                                     uint32_t n, int32_t* out_token, float* out_activations) {
+    return guarded([&] {
+        require(session, "session is required");
+        jfh::Engine& e = *session->owner->engine;
+        require(!e.last_stage() || out_token, "the final stage writes a token");
+        const int32_t token = e.stage_prefill(*session->session, tokens, activations, n, out_activations);
+        if (out_token) *out_token = token;
+    });
+}
+
+jfh_status jfh_session_stage_decode(jfh_session* session, const int32_t* token, const float* activation,
+                                    int32_t* out_token, float* out_activation) {
+    return guarded([&] {
+        require(session, "session is required");
+        jfh::Engine& e = *session->owner->engine;
+        require(!e.last_stage() || out_token, "the final stage writes a token");
+        const int32_t t = e.stage_decode(*session->session, token, activation, out_activation);
+        if (out_token) *out_token = t;
+    });
+}
+
+namespace {
+
+jfh::runtime::inference::Payload activation_payload(const std::string& dtype, const void* data, size_t size) {
+    jfh::runtime::inference::Payload p;
+    p.kind = jfh::runtime::inference::PayloadKind::Activation;
+    p.tensor.dtype = dtype;
+    p.tensor.byte_order = "little";
+    p.tensor.layout = "row_major";
+    const auto* b = static_cast<const uint8_t*>(data);
+    p.bytes.assign(b, b + size);
+    return p;
+}
+
+}  // namespace
+
+jfh_status jfh_activation_encode(const char* codec, const float* values, size_t n, void* out, size_t out_size) {
+    return guarded([&] {
+        require(codec && (values || n == 0) && (out || out_size == 0), "codec, values and output are required");
+        auto c = jfh::runtime::activation::make_default_activation_codec_factory()->create_codec(codec);
+        const auto wire = c->encode(activation_payload("f32", values, n * sizeof(float)));
+        require(wire.bytes.size() == out_size, "activation output size does not match the encoding");
+        if (out_size) std::memcpy(out, wire.bytes.data(), out_size);
+    });
+}
+
+jfh_status jfh_activation_decode(const char* codec, const void* data, size_t size, float* values, size_t n) {
+    return guarded([&] {
+        require(codec && (data || size == 0) && (values || n == 0), "codec, data and output are required");
+        auto c = jfh::runtime::activation::make_default_activation_codec_factory()->create_codec(codec);
+        const auto f32 = c->decode(activation_payload(codec, data, size));
+        require(f32.bytes.size() == n * sizeof(float), "activation output size does not match the encoding");
+        if (n) std::memcpy(values, f32.bytes.data(), n * sizeof(float));
     });
 }
 

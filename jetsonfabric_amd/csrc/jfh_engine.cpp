@@ -46,7 +46,7 @@ bool quantized(uint32_t type) { return type == kQ4_K || type == kQ6_K || type ==
 Session::Session(Engine* engine, uint32_t capacity)
     : engine_(engine), capacity_(capacity), stride_((std::max<uint32_t>(capacity, 16) + 15) / 16 * 16) {
     const ModelParams& p = engine->params();
-    const size_t elems = static_cast<size_t>(p.n_layer) * p.n_head_kv * stride_ * p.head_dim;
+    const size_t elems = static_cast<size_t>(engine->resident_layers()) * p.n_head_kv * stride_ * p.head_dim;
     kv_bytes_ = 2 * elems * sizeof(uint16_t);
     hip_check(hipMalloc(&k_, elems * sizeof(uint16_t)), "allocate K cache");
     if (hipMalloc(&v_, elems * sizeof(uint16_t)) != hipSuccess) {
@@ -326,8 +326,12 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
     }
     hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "create stream");
 
-    if (model.layer_start() != 0 || model.layer_end() != params_.n_layer) {
-        fail(Status::InvalidArgument, "the HIP engine holds every model layer on one device");
+    // a pipeline stage holds the model's layer range [layer_start, layer_end)
+    // (engine.c:181-196): the first stage the embedding, the last the head
+    layer_start_ = model.layer_start();
+    layer_end_ = model.layer_end();
+    if (layer_start_ >= layer_end_ || layer_end_ > params_.n_layer) {
+        fail(Status::InvalidArgument, "native Qwen2 layer range is invalid");
     }
     const ModelParams& p = params_;
     if (p.head_dim % 2 != 0 || p.head_dim > 128) fail(Status::InvalidArgument, "unsupported head dimension");
@@ -338,9 +342,9 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
 
     if (p.head_dim % 4 != 0) fail(Status::InvalidArgument, "head dimension must be a multiple of 4");
     if (p.n_ff % gpu::kGluGroup != 0) fail(Status::InvalidArgument, "feed-forward length must be a multiple of 8");
-    embd_ = &upload_single(model.require("token_embd.weight"));
-    output_norm_ = upload_f32(model.require("output_norm.weight"));
-    {
+    if (first_stage()) embd_ = &upload_single(model.require("token_embd.weight"));
+    if (last_stage()) {
+        output_norm_ = upload_f32(model.require("output_norm.weight"));
         const TensorView& out = model.require("output.weight");
         std::vector<float> bias;
         if (const TensorView* b = model.find("output.bias")) {
@@ -356,7 +360,7 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
         add_ref(out, *output_, 0, 0);
     }
     const uint32_t Hq = p.n_head * p.head_dim, KV = p.n_head_kv * p.head_dim;
-    for (uint32_t l = 0; l < p.n_layer; ++l) {
+    for (uint32_t l = layer_start_; l < layer_end_; ++l) {
         const std::string pre = "blk." + std::to_string(l) + ".";
         Layer L{};
         L.attn_norm = upload_f32(model.require(pre + "attn_norm.weight"));
@@ -412,7 +416,7 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
         }
         layers_.push_back(L);
     }
-    if (quantized(output_->mat.type) && output_->mat.cols % gpu::kActBlock != 0) {
+    if (output_ && quantized(output_->mat.type) && output_->mat.cols % gpu::kActBlock != 0) {
         fail(Status::FormatError, "quantized matrices need row lengths that are multiples of 256");
     }
 
@@ -422,8 +426,10 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
     q_ = static_cast<float*>(device_alloc(R * Hq * sizeof(float)));
     attn_ = static_cast<float*>(device_alloc(R * Hq * sizeof(float)));
     ffn_ = static_cast<float*>(device_alloc(R * F * sizeof(float)));
-    logits_ = static_cast<float*>(device_alloc(R * static_cast<size_t>(p.n_vocab) * sizeof(float)));
+    if (last_stage()) logits_ = static_cast<float*>(device_alloc(R * static_cast<size_t>(p.n_vocab) * sizeof(float)));
     best_ = static_cast<unsigned long long*>(device_alloc(R * sizeof(unsigned long long)));
+    // argmax slots start cleared; k_embed and k_finish clear them for every step
+    hip_check(hipMemset(best_, 0, R * sizeof(unsigned long long)), "clear argmax slots");
     auto act8 = [&](int32_t K) {
         gpu::Act8 a;
         a.K = K;
@@ -558,9 +564,12 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
     const int32_t Hq = static_cast<int32_t>(p.n_head * p.head_dim);
     const double n = n_rows;
     hipStream_t s = stream_;
-    timed("k_embed", n * H * 4.0 + n * static_cast<double>(row_bytes(embd_->mat.type, H)), [&] {
-        gpu::launch_embed(embd_->mat, step_dev_, h_, n_rows, H, best_, gpu::kMaxRows, s);
-    });
+    // the first stage embeds token ids; later stages find their input rows in h_
+    if (first_stage()) {
+        timed("k_embed", n * H * 4.0 + n * static_cast<double>(row_bytes(embd_->mat.type, H)), [&] {
+            gpu::launch_embed(embd_->mat, step_dev_, h_, n_rows, H, best_, gpu::kMaxRows, s);
+        });
+    }
     // Steps with more rows than one 8-row group run Q4_K matrices on matrix
     // cores with int8 rows quantized once per step (same codes as the decode
     // prologue, same results per row).
@@ -585,7 +594,8 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
             a.x = {h_, H, nullptr, gain, p.rms_eps};
         }
     };
-    for (uint32_t l = 0; l < p.n_layer; ++l) {
+    // l: the resident layer (its slot in the sessions' caches)
+    for (uint32_t l = 0; l < layers_.size(); ++l) {
         const Layer& L = layers_[l];
         gpu::GemvArgs qkv;
         qkv.mat = L.qkv->mat;
@@ -674,7 +684,10 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
 void Engine::read_kv(const Session& s, uint32_t layer, uint32_t n, uint16_t* k, uint16_t* v) {
     std::lock_guard lock(mutex_);
     const ModelParams& p = params_;
-    if (layer >= p.n_layer || n > s.position_) fail(Status::InvalidArgument, "cache rows are outside the session");
+    if (layer < layer_start_ || layer >= layer_end_ || n > s.position_) {
+        fail(Status::InvalidArgument, "cache rows are outside the session");
+    }
+    layer -= layer_start_;  // the resident layer
     hip_check(hipStreamSynchronize(stream_), "synchronize before cache read");
     const size_t hd = p.head_dim, rows = static_cast<size_t>(n) * hd, stride = s.stride_;
     std::vector<uint16_t> vt(rows);
@@ -697,7 +710,7 @@ void Engine::import_kv(Session& s, uint32_t n, const uint16_t* k, const uint16_t
     hip_check(hipStreamSynchronize(stream_), "synchronize before cache import");
     const size_t hd = p.head_dim, rows = static_cast<size_t>(n) * hd, stride = s.stride_;
     std::vector<uint16_t> vt(rows);
-    for (uint32_t l = 0; l < p.n_layer; ++l) {
+    for (uint32_t l = 0; l < resident_layers(); ++l) {
         for (uint32_t h = 0; h < p.n_head_kv; ++h) {
             const size_t idx = static_cast<size_t>(l) * p.n_head_kv + h;
             hip_check(hipMemcpy(s.k_ + idx * stride * hd, k + idx * rows, rows * sizeof(uint16_t),
@@ -767,9 +780,17 @@ std::vector<KernelStat> Engine::profile(const std::vector<SeqStep>& steps, uint3
     return out;
 }
 
-void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int32_t* accepted, float* logits) {
+void Engine::require_full_model() const {
+    if (!first_stage() || !last_stage()) {
+        fail(Status::InvalidArgument, "full-model native inference requires every model layer");
+    }
+}
+
+void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int32_t* accepted, float* logits,
+                     float* act_out) {
     std::lock_guard lock(mutex_);
     const ModelParams& p = params_;
+    if (!last_stage() && act_out == nullptr) fail(Status::InvalidArgument, "a non-final stage needs an activation output");
     if (steps.empty() || steps.size() > static_cast<size_t>(gpu::kMaxSeq)) {
         fail(Status::InvalidArgument, "a step needs 1.." + std::to_string(gpu::kMaxSeq) + " sequences");
     }
@@ -783,7 +804,14 @@ void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int
         for (size_t sj = 0; sj < si; ++sj) {
             if (steps[sj].session == s) fail(Status::InvalidArgument, "a session appears twice in one step");
         }
-        if (st.n == 0 || st.tokens == nullptr) fail(Status::InvalidArgument, "a sequence step needs at least one token");
+        if (st.n == 0 || (st.tokens == nullptr) == (st.activations == nullptr)) {
+            fail(Status::InvalidArgument, "a sequence step needs token ids or activation rows");
+        }
+        // token ids only enter the first stage, logits only leave the last
+        if ((st.tokens != nullptr && !first_stage()) || (st.logits != 0 && !last_stage())) require_full_model();
+        if (st.activations != nullptr && first_stage()) {
+            fail(Status::InvalidArgument, "the first native stage does not accept activations");
+        }
         if (static_cast<uint64_t>(s->position_) + st.n > s->capacity_) {
             fail(Status::InvalidArgument, "native Qwen2 step is outside session capacity");
         }
@@ -798,8 +826,8 @@ void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int
         sd.seqs[si].len = static_cast<int32_t>(st.n);
         sd.seqs[si].pos0 = static_cast<int32_t>(s->position_);
         for (uint32_t i = 0; i < st.n; ++i) {
-            const int32_t tok = st.tokens[i];
-            if (tok < 0 || static_cast<uint32_t>(tok) >= p.n_vocab) {
+            const int32_t tok = st.tokens ? st.tokens[i] : 0;
+            if (st.tokens && (tok < 0 || static_cast<uint32_t>(tok) >= p.n_vocab)) {
                 fail(Status::InvalidArgument, "native token ID is outside model vocabulary");
             }
             sd.token[rows + i] = tok;
@@ -813,7 +841,7 @@ void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int
         } else if (st.logits == 2) {
             for (uint32_t i = 0; i < st.n; ++i) {
                 sd.out_row[outs] = rows + static_cast<int32_t>(i);
-                sd.draft[outs] = i + 1 < st.n ? st.tokens[i + 1] : -1;
+                sd.draft[outs] = i + 1 < st.n && st.tokens ? st.tokens[i + 1] : -1;
                 ++outs;
             }
         }
@@ -829,6 +857,14 @@ void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int
     sd.n_out = outs;
     const bool store = logits != nullptr && outs > 0;
     hip_check(hipMemcpyAsync(step_dev_, step_host_, sizeof(gpu::StepDev), hipMemcpyHostToDevice, stream_), "upload step");
+    // input rows of a later stage: the previous stage's residual stream
+    for (size_t si = 0; si < steps.size(); ++si) {
+        if (steps[si].activations == nullptr) continue;
+        hip_check(hipMemcpyAsync(h_ + static_cast<size_t>(sd.seqs[si].row0) * p.n_embd, steps[si].activations,
+                                 static_cast<size_t>(steps[si].n) * p.n_embd * sizeof(float), hipMemcpyHostToDevice,
+                                 stream_),
+                  "upload stage activations");
+    }
     if (options_.use_graphs) {
         const uint64_t key = (static_cast<uint64_t>(rows) << 40) | (static_cast<uint64_t>(max_len) << 32) |
                              (static_cast<uint64_t>(steps.size()) << 16) | (static_cast<uint64_t>(outs) << 1) |
@@ -864,6 +900,11 @@ void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int
                       "download logits");
         }
     }
+    if (!last_stage()) {
+        hip_check(hipMemcpyAsync(act_out, h_, static_cast<size_t>(rows) * p.n_embd * sizeof(float),
+                                 hipMemcpyDeviceToHost, stream_),
+                  "download stage activations");
+    }
     hip_check(hipStreamSynchronize(stream_), "step");
     for (int32_t i = 0; i < outs; ++i) {
         if (out_tokens) out_tokens[i] = out_host_->token[i];
@@ -878,6 +919,7 @@ void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int
 }
 
 int32_t Engine::prefill(Session& s, const int32_t* tokens, uint32_t n, float* logits) {
+    require_full_model();
     if (s.position_ != 0 || n == 0 || n > s.capacity_) {
         fail(Status::InvalidArgument, "native Qwen2 prefill is outside session capacity");
     }
@@ -895,6 +937,62 @@ int32_t Engine::prefill(Session& s, const int32_t* tokens, uint32_t n, float* lo
     }
     s.prefill_position_ = n;
     return token;
+}
+
+int32_t Engine::stage_prefill(Session& s, const int32_t* tokens, const float* activations, uint32_t n,
+                              float* act_out) {
+    if (first_stage() && activations != nullptr) {
+        fail(Status::InvalidArgument, "the first native stage does not accept activations");
+    }
+    if (!first_stage() && tokens != nullptr) fail(Status::InvalidArgument, "only the first native stage accepts tokens");
+    if (first_stage() && tokens == nullptr) fail(Status::InvalidArgument, "the first native stage requires token input");
+    if (!first_stage() && (activations == nullptr || n == 0)) {
+        fail(Status::InvalidArgument, "native stage activation shape is invalid");
+    }
+    if (!last_stage() && act_out == nullptr) fail(Status::InvalidArgument, "a non-final stage needs an activation output");
+    if (s.position_ != 0 || n == 0 || n > s.capacity_) {
+        fail(Status::InvalidArgument, "native Qwen2 prefill is outside session capacity");
+    }
+    const size_t H = params_.n_embd;
+    int32_t token = -1;
+    for (uint32_t done = 0; done < n;) {
+        const uint32_t len = std::min(prefill_chunk_, n - done);
+        const bool last = done + len == n;
+        SeqStep st;
+        st.session = &s;
+        st.tokens = tokens ? tokens + done : nullptr;
+        st.activations = activations ? activations + done * H : nullptr;
+        st.n = len;
+        st.logits = last && last_stage() ? 1 : 0;
+        forward({st}, st.logits ? &token : nullptr, nullptr, nullptr, act_out ? act_out + done * H : nullptr);
+        done += len;
+    }
+    s.prefill_position_ = n;
+    return token;
+}
+
+int32_t Engine::stage_decode(Session& s, const int32_t* token, const float* activation, float* act_out) {
+    if (first_stage() && activation != nullptr) {
+        fail(Status::InvalidArgument, "the first native stage does not accept decode activations");
+    }
+    if (!first_stage() && token != nullptr) {
+        fail(Status::InvalidArgument, "only the first native stage accepts decode tokens");
+    }
+    if (first_stage() && token == nullptr) fail(Status::InvalidArgument, "the first native stage requires token input");
+    if (!first_stage() && activation == nullptr) fail(Status::InvalidArgument, "native stage activation shape is invalid");
+    if (!last_stage() && act_out == nullptr) fail(Status::InvalidArgument, "a non-final stage needs an activation output");
+    if (s.position_ == 0 || s.position_ >= s.capacity_) {
+        fail(Status::InvalidArgument, "native Qwen2 decode is outside session capacity");
+    }
+    SeqStep st;
+    st.session = &s;
+    st.tokens = token;
+    st.activations = activation;
+    st.n = 1;
+    st.logits = last_stage() ? 1 : 0;
+    int32_t out = -1;
+    forward({st}, st.logits ? &out : nullptr, nullptr, nullptr, act_out);
+    return out;
 }
 
 void Engine::dequantize(const std::string& name, uint32_t row0, uint32_t n_rows, float* out_host) {

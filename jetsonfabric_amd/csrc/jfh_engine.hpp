@@ -3,7 +3,8 @@
 //
 // Replaces the reference's Qwen2Architecture/Qwen2Session/ForwardGraph
 // (runtime/engines/native/src/qwen2_architecture.cpp:120-1212) and
-// TensorStore (tensor_store.cpp:57-196) for one GPU holding every layer.
+// TensorStore (tensor_store.cpp:57-196) for one GPU holding a model's layers
+// or one pipeline stage's layer range (LayerRange, model_architecture.hpp:15-21).
 #pragma once
 
 #include "jfh_kernels.hpp"
@@ -53,15 +54,16 @@ private:
     uint32_t stride_;  // allocated positions per (layer, kv head): capacity rounded up to 16
     uint32_t position_ = 0;
     uint32_t prefill_position_ = 0;
-    uint16_t* k_ = nullptr;  // [layer][kv head][stride][head_dim]
-    uint16_t* v_ = nullptr;  // [layer][kv head][head_dim][stride] (transposed)
+    uint16_t* k_ = nullptr;  // [resident layer][kv head][stride][head_dim]
+    uint16_t* v_ = nullptr;  // [resident layer][kv head][head_dim][stride] (transposed)
     uint64_t kv_bytes_ = 0;
 };
 
 // One sequence's share of a batched step.
 struct SeqStep {
     Session* session = nullptr;
-    const int32_t* tokens = nullptr;
+    const int32_t* tokens = nullptr;     // first stage: token ids, or
+    const float* activations = nullptr;  // later stages: f32 [n][n_embd] input rows
     uint32_t n = 0;
     // 0: no logits, 1: last row, 2: every row (draft verify)
     int logits = 1;
@@ -85,6 +87,15 @@ public:
 
     const ModelParams& params() const { return params_; }
     uint64_t weight_bytes() const { return weight_bytes_; }
+    // The resident layer range [layer_start, layer_end): the first stage
+    // embeds token ids, the last one holds the output head.
+    uint32_t layer_start() const { return layer_start_; }
+    uint32_t layer_end() const { return layer_end_; }
+    uint32_t resident_layers() const { return layer_end_ - layer_start_; }
+    bool first_stage() const { return layer_start_ == 0; }
+    bool last_stage() const { return layer_end_ == params_.n_layer; }
+    // Fails unless this engine holds every layer (full-model entry points).
+    void require_full_model() const;
     hipStream_t stream() const { return stream_; }
     const std::string& device_name() const { return device_name_; }
 
@@ -93,12 +104,24 @@ public:
     // Runs token rows for several sessions in one pass. Positions advance by
     // each sequence's row count. out_tokens receives one greedy id per logits
     // row (sequence order); accepted (optional) one accepted-draft count per
-    // sequence; logits (optional) n_logits_rows x vocab floats.
-    void forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int32_t* accepted, float* logits);
+    // sequence; logits (optional) n_logits_rows x vocab floats. A stage
+    // that is not the last one computes no logits: act_out receives the
+    // residual-stream rows after its last layer, f32 [rows][n_embd].
+    void forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int32_t* accepted, float* logits,
+                 float* act_out = nullptr);
 
     // Prefill of arbitrary length: runs the prompt in chunks and returns the
     // greedy token of the last row (and its logits if requested).
     int32_t prefill(Session& s, const int32_t* tokens, uint32_t n, float* logits);
+
+    // One pipeline stage's prefill (n rows at position 0) or decode (one row)
+    // (Qwen2Session::prefill_stage_* / decode_stage_*,
+    // qwen2_architecture.cpp:909-947, 977-1027): token ids into the first
+    // stage, activations into the others; the last stage returns the greedy
+    // id of the last row, the others write every row's activations to
+    // act_out and return -1.
+    int32_t stage_prefill(Session& s, const int32_t* tokens, const float* activations, uint32_t n, float* act_out);
+    int32_t stage_decode(Session& s, const int32_t* token, const float* activation, float* act_out);
 
     // Parity entry points: dequantize rows of a device tensor; multiply a
     // device matrix with host activations through the same kernels.
@@ -171,8 +194,9 @@ private:
     std::map<std::string, TensorRef> refs_;
     std::vector<void*> allocations_;
     std::vector<Layer> layers_;
-    const DeviceTensor* embd_ = nullptr;
-    const DeviceTensor* output_ = nullptr;
+    uint32_t layer_start_ = 0, layer_end_ = 0;
+    const DeviceTensor* embd_ = nullptr;    // first stage only
+    const DeviceTensor* output_ = nullptr;  // last stage only
     const float* output_norm_ = nullptr;
     uint64_t weight_bytes_ = 0;
     uint32_t prefill_chunk_ = 8;

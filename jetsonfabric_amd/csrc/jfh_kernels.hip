@@ -2055,12 +2055,16 @@ __global__ __launch_bounds__(256) void k_attention_merge(const float* __restrict
 // Greedy ids of the logits rows (first maximum, qwen2_architecture.cpp:594) and,
 // per sequence, the accepted draft prefix: rows are compared in order with the
 // next input token until the first mismatch (generation_runner.cpp:512-517).
-__global__ void k_finish(const unsigned long long* best, const StepDev* step, int32_t n_out, StepOut* out) {
+// The argmax slots are cleared for the next step (stages without an
+// embedding kernel rely on it).
+__global__ void k_finish(unsigned long long* best, const StepDev* step, int32_t n_out, StepOut* out) {
     __shared__ int32_t tok[kMaxRows];
     for (int i = threadIdx.x; i < n_out; i += blockDim.x) {
-        const uint32_t low = static_cast<uint32_t>(best[i] & 0xFFFFFFFFull);
-        tok[i] = best[i] == 0ull ? -1 : static_cast<int32_t>(0xFFFFFFFFu - low);
+        const unsigned long long b = best[i];
+        const uint32_t low = static_cast<uint32_t>(b & 0xFFFFFFFFull);
+        tok[i] = b == 0ull ? -1 : static_cast<int32_t>(0xFFFFFFFFu - low);
         out->token[i] = tok[i];
+        best[i] = 0ull;
     }
     __syncthreads();
     for (int s = threadIdx.x; s < step->n_seq; s += blockDim.x) {
@@ -2358,7 +2362,7 @@ void launch_attention_merge(const float* partial, const StepDev* step, int32_t n
     check(hipGetLastError(), "attention merge launch");
 }
 
-void launch_finish(const unsigned long long* best, const StepDev* step, int32_t n_out, StepOut* out,
+void launch_finish(unsigned long long* best, const StepDev* step, int32_t n_out, StepOut* out,
                    hipStream_t stream) {
     launch(k_finish, dim3(1), dim3(64), 0, stream, best, step, n_out, out);
     check(hipGetLastError(), "finish launch");

@@ -184,7 +184,7 @@ int32_t attention_splits(int32_t capacity);
 int32_t attention_max_rows(int32_t head_dim);
 // Floats of the attention split scratch for `rows` token rows.
 size_t attention_partial_floats(int32_t rows, int32_t n_head, int32_t head_dim, int32_t splits);
-void launch_finish(const unsigned long long* best, const StepDev* step, int32_t n_out, StepOut* out,
+void launch_finish(unsigned long long* best, const StepDev* step, int32_t n_out, StepOut* out,
                    hipStream_t stream);
 void launch_dequant_rows(const DMat& m, int32_t row0, int32_t n_rows, float* out, hipStream_t stream);
 // Host evaluation of the device tile decoder: value k (< 256) of row (< 16) of one tile.

@@ -369,11 +369,14 @@ void HostModel::finalize() {
     };
     const bool first = layer_start_ == 0, last = layer_end_ == p.n_layer;
     if (layer_start_ >= layer_end_ || layer_end_ > p.n_layer) fail(Status::InvalidArgument, "native Qwen2 layer range is invalid");
-    // vocabulary from the embedding or the output head (TensorStore::vocabulary_size)
+    // vocabulary from the embedding or the output head (TensorStore::vocabulary_size,
+    // tensor_store.cpp:211-220); a middle stage holds neither and has none
     const TensorView* vocab_src = find(first ? "token_embd.weight" : "output.weight");
     if (!vocab_src) vocab_src = find("output.weight");
-    if (!vocab_src || vocab_src->rank != 2) fail(Status::FormatError, "native Qwen2 vocabulary tensor is missing");
-    params_.n_vocab = uint32_t(vocab_src->shape[1]);
+    if ((first || last) && (!vocab_src || vocab_src->rank != 2)) {
+        fail(Status::FormatError, "native Qwen2 vocabulary tensor is missing");
+    }
+    params_.n_vocab = vocab_src && vocab_src->rank == 2 ? uint32_t(vocab_src->shape[1]) : 0;
     const uint64_t V = params_.n_vocab;
     if (first) shape("token_embd.weight", {H, V});
     if (last) {

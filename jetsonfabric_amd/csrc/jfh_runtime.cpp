@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <chrono>
 #include <condition_variable>
+#include <cstring>
 #include <deque>
 #include <future>
 #include <limits>
@@ -212,6 +213,156 @@ std::vector<std::uint32_t> PromptLookupDraft::propose(const std::vector<std::uin
 
 }  // namespace speculative
 
+// ------------------------------------------------------------------ activation codecs
+namespace activation {
+
+std::uint16_t f32_to_f16(float value) {
+    std::uint32_t x = 0;
+    std::memcpy(&x, &value, sizeof(x));
+    const std::uint16_t sign = static_cast<std::uint16_t>((x >> 16) & 0x8000U);
+    const std::uint32_t ax = x & 0x7FFFFFFFU;
+    if (ax > 0x7F800000U) return static_cast<std::uint16_t>(sign | 0x7E00U | ((ax >> 13) & 0x3FFU));  // NaN
+    if (ax >= 0x477FF000U) return static_cast<std::uint16_t>(sign | 0x7C00U);  // rounds past 65504: infinity
+    if (ax >= 0x38800000U) {
+        // normal: rebias the exponent (127 -> 15), round the 13 dropped bits
+        // to nearest even; a carry out of the mantissa bumps the exponent
+        std::uint32_t m = ax - 0x38000000U;
+        m += 0x0FFFU + ((m >> 13) & 1U);
+        return static_cast<std::uint16_t>(sign | (m >> 13));
+    }
+    if (ax < 0x33000000U) return sign;  // below half the smallest subnormal (2^-25)
+    // subnormal: value / 2^-24 rounded to nearest even (may reach 0x400, the smallest normal)
+    const std::uint32_t e = ax >> 23, mant = (ax & 0x7FFFFFU) | 0x800000U;
+    const std::uint32_t shift = 126U - e;  // 14 .. 24
+    std::uint32_t q = mant >> shift;
+    const std::uint32_t rest = mant & ((1U << shift) - 1U), half = 1U << (shift - 1U);
+    if (rest > half || (rest == half && (q & 1U) != 0U)) ++q;
+    return static_cast<std::uint16_t>(sign | q);
+}
+
+float f16_to_f32(std::uint16_t value) {
+    const std::uint32_t sign = static_cast<std::uint32_t>(value & 0x8000U) << 16;
+    const std::uint32_t e = (value >> 10) & 0x1FU, m = value & 0x3FFU;
+    std::uint32_t bits = 0;
+    if (e == 0x1FU) {
+        bits = sign | 0x7F800000U | (m << 13);
+    } else if (e != 0U) {
+        bits = sign | ((e + 112U) << 23) | (m << 13);
+    } else {
+        const float sub = static_cast<float>(m) * 0x1p-24F;  // exact: m < 2^10
+        std::memcpy(&bits, &sub, sizeof(bits));
+        bits |= sign;
+    }
+    float out = 0.0F;
+    std::memcpy(&out, &bits, sizeof(out));
+    return out;
+}
+
+namespace {
+
+constexpr const char* kF32 = "f32";
+constexpr const char* kF16 = "f16";
+
+void require_activation(const inference::Payload& p, const char* dtype) {
+    if (p.kind != inference::PayloadKind::Activation) {
+        throw std::invalid_argument("activation codec requires an activation payload");
+    }
+    if (p.tensor.dtype != dtype) {
+        throw std::invalid_argument(std::string("activation codec expected ") + dtype + " input, got " + p.tensor.dtype);
+    }
+}
+
+class F32Codec final : public ActivationCodec {
+public:
+    const std::string& name() const noexcept override {
+        static const std::string n = kF32;
+        return n;
+    }
+    inference::Payload encode(inference::Payload p) const override {
+        require_activation(p, kF32);
+        return p;
+    }
+    inference::Payload decode(inference::Payload p) const override {
+        require_activation(p, kF32);
+        return p;
+    }
+};
+
+// little-endian f32 words <-> little-endian f16 words
+class F16Codec final : public ActivationCodec {
+public:
+    const std::string& name() const noexcept override {
+        static const std::string n = kF16;
+        return n;
+    }
+    inference::Payload encode(inference::Payload p) const override {
+        require_activation(p, kF32);
+        if (p.bytes.size() % 4 != 0) throw std::invalid_argument("f32 activation byte length must be divisible by four");
+        std::vector<std::uint8_t> out(p.bytes.size() / 2);
+        for (std::size_t i = 0; i < out.size() / 2; ++i) {
+            const std::uint8_t* b = p.bytes.data() + 4 * i;
+            const std::uint32_t w = static_cast<std::uint32_t>(b[0]) | (static_cast<std::uint32_t>(b[1]) << 8) |
+                                    (static_cast<std::uint32_t>(b[2]) << 16) | (static_cast<std::uint32_t>(b[3]) << 24);
+            float f = 0.0F;
+            std::memcpy(&f, &w, sizeof(f));
+            const std::uint16_t h = f32_to_f16(f);
+            out[2 * i] = static_cast<std::uint8_t>(h & 0xFFU);
+            out[2 * i + 1] = static_cast<std::uint8_t>(h >> 8);
+        }
+        p.tensor.dtype = kF16;
+        p.bytes = std::move(out);
+        return p;
+    }
+    inference::Payload decode(inference::Payload p) const override {
+        require_activation(p, kF16);
+        if (p.bytes.size() % 2 != 0) throw std::invalid_argument("f16 activation byte length must be divisible by two");
+        std::vector<std::uint8_t> out(p.bytes.size() * 2);
+        for (std::size_t i = 0; i < p.bytes.size() / 2; ++i) {
+            const std::uint16_t h =
+                static_cast<std::uint16_t>(p.bytes[2 * i] | (static_cast<std::uint16_t>(p.bytes[2 * i + 1]) << 8));
+            const float f = f16_to_f32(h);
+            std::uint32_t w = 0;
+            std::memcpy(&w, &f, sizeof(w));
+            for (int k = 0; k < 4; ++k) out[4 * i + k] = static_cast<std::uint8_t>((w >> (8 * k)) & 0xFFU);
+        }
+        p.tensor.dtype = kF32;
+        p.bytes = std::move(out);
+        return p;
+    }
+};
+
+}  // namespace
+
+void ActivationCodecFactory::register_codec(std::string name, Builder builder) {
+    if (name.empty()) throw std::invalid_argument("activation codec name must not be empty");
+    if (!builder) throw std::invalid_argument("activation codec builder must not be empty");
+    if (!builders_.emplace(std::move(name), std::move(builder)).second) {
+        throw std::invalid_argument("activation codec is already registered");
+    }
+}
+
+bool ActivationCodecFactory::supports(const std::string& name) const { return builders_.count(name) != 0; }
+
+std::shared_ptr<const ActivationCodec> ActivationCodecFactory::create_codec(const std::string& name) const {
+    auto it = builders_.find(name);
+    if (it == builders_.end()) throw std::invalid_argument("unsupported activation encoding: " + name);
+    std::shared_ptr<const ActivationCodec> codec = it->second();
+    if (!codec) throw std::runtime_error("activation codec builder returned null: " + name);
+    if (codec->name() != name) {
+        throw std::runtime_error("activation codec registered as " + name + " returned strategy " + codec->name());
+    }
+    return codec;
+}
+
+std::shared_ptr<const ActivationCodecFactory> make_default_activation_codec_factory() {
+    auto f = std::make_shared<ActivationCodecFactory>();
+    f->register_codec(kF32, [] { return std::make_shared<F32Codec>(); });
+    f->register_codec(kF16, [] { return std::make_shared<F16Codec>(); });
+    return f;
+}
+
+}  // namespace activation
+
 // ------------------------------------------------------------------ adapter
 namespace adapters {
 
@@ -231,11 +382,17 @@ public:
     explicit Impl(HipStageConfig c) : config(std::move(c)) {
         if (!config.engine || !config.tokenizer) throw std::invalid_argument("native executor requires engine and tokenizer");
         if (config.ctx_size <= 0) throw std::invalid_argument("native executor context size must be positive");
+        // native_stage_executor.cpp:84-104: a stage runs exactly the engine's resident layers
         const int layers = static_cast<int>(config.engine->params().n_layer);
-        if (config.position.count != 1 || config.position.index != 0 || config.layers.start != 0 ||
-            config.layers.end != layers) {
-            // One GPU holds every layer: the stage is both first and last.
+        const inference::StagePosition& pos = config.position;
+        if (pos.count <= 0 || pos.index < 0 || pos.index >= pos.count || config.layers.start < 0 ||
+            config.layers.end <= config.layers.start || config.layers.end > layers ||
+            (pos.is_first() && config.layers.start != 0) || (pos.is_last() && config.layers.end != layers)) {
             throw std::invalid_argument("native serving stage assignment is invalid");
+        }
+        if (config.layers.start != static_cast<int>(config.engine->layer_start()) ||
+            config.layers.end != static_cast<int>(config.engine->layer_end())) {
+            throw std::invalid_argument("native stage exceeds its resident layer range");
         }
         if (static_cast<std::uint32_t>(config.ctx_size) > config.engine->params().n_ctx) {
             throw std::invalid_argument("native context size exceeds model context");
@@ -279,7 +436,7 @@ public:
         std::vector<std::vector<std::int32_t>> batch_tokens;
         for (std::size_t i = 0; i < inputs.size(); ++i) {
             const StageInput& in = inputs[i];
-            bool batchable = in.phase == Phase::Decode && inference::validate_stage_input(in).empty() &&
+            bool batchable = whole_model() && in.phase == Phase::Decode && inference::validate_stage_input(in).empty() &&
                              assignment_matches(in) && batch.size() < static_cast<std::size_t>(gpu::kMaxSeq);
             std::vector<std::int32_t> tokens;
             if (batchable) {
@@ -412,10 +569,102 @@ private:
         return out;
     }
 
+    bool whole_model() const { return config.position.is_first() && config.position.is_last(); }
+
+    // native_stage_executor.cpp:16-47: f32 [rows, n_embd] activation payloads
+    std::vector<float> input_activation(const StageInput& in) const {
+        const std::int64_t H = config.engine->params().n_embd;
+        const inference::Payload& p = in.payload;
+        if (p.kind != PayloadKind::Activation || p.tensor.dtype != "f32" || p.tensor.shape.size() != 2 ||
+            p.tensor.shape[0] <= 0 || p.tensor.shape[1] != H) {
+            throw std::invalid_argument("native activation must be f32[sequence_length, hidden_size]");
+        }
+        const std::size_t rows = static_cast<std::size_t>(p.tensor.shape[0]);
+        if (rows > std::numeric_limits<std::size_t>::max() / static_cast<std::size_t>(H) / sizeof(float)) {
+            throw std::invalid_argument("native activation shape exceeds addressable memory");
+        }
+        if (p.bytes.size() != rows * static_cast<std::size_t>(H) * sizeof(float)) {
+            throw std::invalid_argument("native activation byte count does not match its shape");
+        }
+        std::vector<float> rows_f32(rows * static_cast<std::size_t>(H));
+        std::memcpy(rows_f32.data(), p.bytes.data(), p.bytes.size());
+        return rows_f32;
+    }
+
+    StageOutput activation_output(const std::vector<float>& rows) const {
+        const std::int64_t H = config.engine->params().n_embd;
+        StageOutput out;
+        out.payload.kind = PayloadKind::Activation;
+        out.payload.tensor.dtype = "f32";
+        out.payload.tensor.shape = {static_cast<std::int64_t>(rows.size()) / H, H};
+        out.payload.tensor.byte_order = "little";
+        out.payload.tensor.layout = "row_major";
+        out.payload.bytes.resize(rows.size() * sizeof(float));
+        std::memcpy(out.payload.bytes.data(), rows.data(), out.payload.bytes.size());
+        out.execution_batch_size = 1;
+        return out;
+    }
+
+    // A stage of a pipeline (not the whole model): prefill_stage_* / decode_stage_*
+    // (native_stage_executor.cpp:226-320)
+    ExecutionResult stage_prefill(const StageInput& in) {
+        std::vector<std::int32_t> tokens;
+        std::vector<float> act;
+        std::size_t count = 0;
+        if (config.position.is_first()) {
+            tokens = input_tokens(in);
+            count = tokens.size();
+        } else {
+            act = input_activation(in);
+            count = act.size() / config.engine->params().n_embd;
+        }
+        const std::size_t capacity = session_capacity(count, in.max_tokens);
+        std::unique_ptr<Session> session = config.engine->create_session(static_cast<std::uint32_t>(capacity));
+        std::vector<float> out_rows(config.position.is_last() ? 0 : count * config.engine->params().n_embd);
+        const std::int32_t token = config.engine->stage_prefill(
+            *session, tokens.empty() ? nullptr : tokens.data(), act.empty() ? nullptr : act.data(),
+            static_cast<std::uint32_t>(count), out_rows.empty() ? nullptr : out_rows.data());
+        StageOutput out = config.position.is_last() ? token_output(token) : activation_output(out_rows);
+        if (config.position.is_first()) {
+            out.prompt_tokens = static_cast<int>(tokens.size());
+            for (const std::int32_t t : tokens) {
+                if (t < 0) throw std::invalid_argument("native tokenizer returned a negative token");
+                out.prompt_token_ids.push_back(static_cast<std::uint32_t>(t));
+            }
+        }
+        sessions.emplace(in.session_id, SessionState{std::move(session), 1});
+        return ExecutionResult::success(std::move(out));
+    }
+
+    ExecutionResult stage_decode(const StageInput& in, SessionState& state) {
+        std::vector<std::int32_t> tokens;
+        std::vector<float> act;
+        if (config.position.is_first()) {
+            tokens = input_tokens(in);
+            if (tokens.size() != 1U) {
+                return ExecutionResult::invalid_input("native_multi_token_verification_unsupported",
+                                                      "native serving currently accepts one decode token per pass");
+            }
+        } else {
+            act = input_activation(in);
+            if (act.size() != config.engine->params().n_embd) {
+                return ExecutionResult::invalid_input("native_multi_token_verification_unsupported",
+                                                      "native decode activation must contain one token row");
+            }
+        }
+        std::vector<float> out_rows(config.position.is_last() ? 0 : config.engine->params().n_embd);
+        const std::int32_t token =
+            config.engine->stage_decode(*state.session, tokens.empty() ? nullptr : tokens.data(),
+                                        act.empty() ? nullptr : act.data(), out_rows.empty() ? nullptr : out_rows.data());
+        ++state.expected_decode_step;
+        return ExecutionResult::success(config.position.is_last() ? token_output(token) : activation_output(out_rows));
+    }
+
     ExecutionResult prefill(const StageInput& in) {
         if (sessions.count(in.session_id)) {
             return ExecutionResult::invalid_input("duplicate_stage_session", "prefill session already exists on this native stage");
         }
+        if (!whole_model()) return stage_prefill(in);
         const std::vector<std::int32_t> tokens = input_tokens(in);
         if (tokens.empty()) throw std::invalid_argument("native Qwen2 prefill is outside session capacity");
         const std::size_t capacity = session_capacity(tokens.size(), in.max_tokens);
@@ -441,6 +690,7 @@ private:
         if (in.decode_step != state.expected_decode_step) {
             return ExecutionResult::invalid_input("unexpected_decode_step", "native decode step does not match session state");
         }
+        if (!whole_model()) return stage_decode(in, state);
         const std::vector<std::int32_t> tokens = input_tokens(in);
         if (tokens.empty() || tokens.size() > static_cast<std::size_t>(config.speculative_max_tokens + 1)) {
             return ExecutionResult::invalid_input("invalid_verification_width",

@@ -16,6 +16,10 @@
 //   pipeline_parallel::ContinuousBatchingExecutor -- coalesces concurrent
 //     decode steps into execute_batch calls
 //     (runtime/pipeline_parallel/continuous_batching_executor.{hpp,cpp})
+//   activation::{ActivationCodec, ActivationCodecFactory} -- the f32 / f16
+//     codecs of activations between pipeline stages
+//     (runtime/activation/activation_codec.hpp:9-18,
+//     activation_codec_factory.cpp:8-46, builtin_activation_codecs.cpp)
 #pragma once
 
 #include "jfh_engine.hpp"
@@ -175,6 +179,41 @@ private:
 };
 
 }  // namespace speculative
+
+namespace activation {
+
+// IEEE 754 binary16 conversions: f32 -> f16 rounds to nearest, ties to even
+// (overflow to infinity, gradual underflow to subnormals and signed zero);
+// NaNs stay NaNs with the quiet bit set and the top ten payload bits kept.
+// f16 -> f32 is exact.
+std::uint16_t f32_to_f16(float value);
+float f16_to_f32(std::uint16_t value);
+
+// Converts activation payloads between the engine's f32 rows and the
+// representation carried between pipeline stages.
+class ActivationCodec {
+public:
+    virtual ~ActivationCodec() = default;
+    virtual const std::string& name() const noexcept = 0;
+    virtual inference::Payload encode(inference::Payload payload) const = 0;
+    virtual inference::Payload decode(inference::Payload payload) const = 0;
+};
+
+class ActivationCodecFactory {
+public:
+    using Builder = std::function<std::shared_ptr<const ActivationCodec>()>;
+    void register_codec(std::string name, Builder builder);
+    bool supports(const std::string& name) const;
+    std::shared_ptr<const ActivationCodec> create_codec(const std::string& name) const;
+
+private:
+    std::unordered_map<std::string, Builder> builders_;
+};
+
+// "f32" (identity) and "f16" (half the wire bytes).
+std::shared_ptr<const ActivationCodecFactory> make_default_activation_codec_factory();
+
+}  // namespace activation
 
 namespace adapters {
 

@@ -61,6 +61,27 @@ def type_layout(type_id: int) -> tuple[int, int]:
     return e.value, b.value
 
 
+def activation_encode(values: np.ndarray, codec: str = "f16") -> bytes:
+    """Wire bytes of f32 activations under an activation codec ("f32" or "f16";
+    builtin_activation_codecs.cpp:112-209)."""
+    v = np.ascontiguousarray(values, dtype=np.float32).ravel()
+    width = {"f32": 4, "f16": 2}.get(codec, 2)
+    out = ctypes.create_string_buffer(v.size * width)
+    check(library().jfh_activation_encode(codec.encode(), v.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), v.size,
+                                          out, v.size * width))
+    return out.raw
+
+
+def activation_decode(data: bytes, codec: str = "f16") -> np.ndarray:
+    """f32 values of an activation codec's wire bytes."""
+    width = {"f32": 4, "f16": 2}.get(codec, 2)
+    n = len(data) // width
+    out = np.zeros(n, dtype=np.float32)
+    check(library().jfh_activation_decode(codec.encode(), data, len(data),
+                                          out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), n))
+    return out
+
+
 def sha256(data: bytes) -> bytes:
     out = (ctypes.c_uint8 * 32)()
     buf = ctypes.create_string_buffer(bytes(data), len(data))
@@ -284,6 +305,39 @@ class NativeSession:
         ids = [int(x) for x in out]
         return (ids, int(acc.value), buf) if logits else (ids, int(acc.value))
 
+    def _stage_io(self, activations, n: int):
+        e = self._engine
+        f32 = ctypes.POINTER(ctypes.c_float)
+        src = None
+        if activations is not None:
+            act = np.ascontiguousarray(activations, dtype=np.float32)
+            if act.ndim != 2 or act.shape[1] != e._config.n_embd or act.shape[0] != n:
+                raise ValueError(f"stage activations must be f32[{n}, {e._config.n_embd}]")
+            src = act
+        out = None if e.last_stage else np.zeros((n, e._config.n_embd), dtype=np.float32)
+        return (src, src.ctypes.data_as(f32) if src is not None else None, out,
+                out.ctypes.data_as(f32) if out is not None else None)
+
+    def prefill_stage(self, tokens: Sequence[int] | None = None, activations: np.ndarray | None = None):
+        """Pipeline-stage prefill (NativeSession::prefill_stage_tokens / _activations): token ids
+        into the first stage, f32[n, n_embd] activations into later ones. Returns the greedy id of
+        the last row on the last stage, else the stage's output activations f32[n, n_embd]."""
+        n = len(tokens) if tokens is not None else (len(activations) if activations is not None else 0)
+        src, src_p, out, out_p = self._stage_io(activations, n)
+        tok = ctypes.c_int32(-1)
+        check(library().jfh_session_stage_prefill(self._h, _i32(tokens) if tokens is not None else None, src_p, n,
+                                                  ctypes.byref(tok), out_p))
+        return tok.value if out is None else out
+
+    def decode_stage(self, token: int | None = None, activation: np.ndarray | None = None):
+        """One pipeline-stage decode row (NativeSession::decode_stage_token / _activation)."""
+        src, src_p, out, out_p = self._stage_io(activation, 1)
+        tok = ctypes.c_int32(-1)
+        tin = ctypes.c_int32(token) if token is not None else None
+        check(library().jfh_session_stage_decode(self._h, ctypes.byref(tin) if tin is not None else None, src_p,
+                                                 ctypes.byref(tok), out_p))
+        return tok.value if out is None else out
+
     def rollback(self, token_count: int) -> None:
         check(library().jfh_session_rollback(self._h, token_count))
 
@@ -348,6 +402,11 @@ class NativeEngine:
         self.weight_bytes = int(info.weight_bytes)
         self.prefill_chunk = int(info.prefill_chunk)
         self.device_name = info.device_name.decode()
+        # resident layer range of a pipeline stage (the whole model by default)
+        self.layer_start = int(info.layer_start)
+        self.layer_end = int(info.layer_end)
+        self.first_stage = self.layer_start == 0
+        self.last_stage = self.layer_end == self._config.n_layer
 
     def close(self) -> None:
         if self._h:

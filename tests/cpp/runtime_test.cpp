@@ -1,15 +1,18 @@
 // Host-side tests of the speculative runtime (no GPU): prompt-lookup
 // drafting, the greedy acceptance / rollback loop over a scripted executor,
-// the continuous-batching executor, and the stage payload helpers. Mirrors
+// the continuous-batching executor, the stage payload helpers and the
+// activation codecs. Mirrors
 // the reference's own cases in
 // runtime/speculative/prompt_lookup_draft_test.cpp:15-36,
 // runtime/pipeline_parallel/generation_runner_test.cpp:108-190, 355-430 and
-// runtime/pipeline_parallel/continuous_batching_executor_test.cpp.
+// runtime/pipeline_parallel/continuous_batching_executor_test.cpp and
+// runtime/activation/activation_codec_test.cpp.
 #include "jfh_runtime.hpp"
 
 #include <chrono>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -288,8 +291,82 @@ void test_continuous_batching() {
 
 }  // namespace
 
+// activation_codec_test.cpp:60-99: factory registration and codec guards
+void test_activation_codecs() {
+    auto factory = activation::make_default_activation_codec_factory();
+    expect(factory->supports("f32") && factory->supports("f16") && !factory->supports("missing"),
+           "default factory registers f32 and f16 only");
+    bool rejected = false;
+    try {
+        (void) factory->create_codec("missing");
+    } catch (const std::invalid_argument&) {
+        rejected = true;
+    }
+    expect(rejected, "unknown encoding is rejected");
+    struct Misnamed final : activation::ActivationCodec {
+        const std::string& name() const noexcept override {
+            static const std::string n = "other";
+            return n;
+        }
+        inference::Payload encode(inference::Payload p) const override { return p; }
+        inference::Payload decode(inference::Payload p) const override { return p; }
+    };
+    activation::ActivationCodecFactory custom;
+    custom.register_codec("registered", [] { return std::make_shared<Misnamed>(); });
+    bool misnamed = false;
+    try {
+        (void) custom.create_codec("registered");
+    } catch (const std::runtime_error&) {
+        misnamed = true;
+    }
+    expect(misnamed, "a codec whose name differs from its registration is rejected");
+    bool duplicate = false;
+    try {
+        custom.register_codec("registered", [] { return std::make_shared<Misnamed>(); });
+    } catch (const std::invalid_argument&) {
+        duplicate = true;
+    }
+    expect(duplicate, "a name registers once");
+
+    const auto f16 = factory->create_codec("f16");
+    inference::Payload p;
+    p.kind = inference::PayloadKind::Activation;
+    p.tensor.dtype = "f32";
+    p.tensor.shape = {1, 3};
+    for (const float v : {1.0F, -0.5F, 3.0e5F}) {
+        std::uint8_t b[4];
+        std::memcpy(b, &v, 4);
+        p.bytes.insert(p.bytes.end(), b, b + 4);
+    }
+    const inference::Payload wire = f16->encode(p);
+    expect(wire.tensor.dtype == "f16" && wire.bytes.size() == 6, "f16 wire payload is half the bytes");
+    expect(wire.bytes[0] == 0x00 && wire.bytes[1] == 0x3C && wire.bytes[2] == 0x00 && wire.bytes[3] == 0xB8 &&
+               wire.bytes[4] == 0x00 && wire.bytes[5] == 0x7C,
+           "1, -0.5 and an overflowing value encode as 0x3C00, 0xB800, +inf");
+    const inference::Payload back = f16->decode(wire);
+    expect(back.tensor.dtype == "f32" && back.bytes.size() == 12, "decode restores f32 rows");
+    bool wrong_dtype = false;
+    try {
+        (void) f16->decode(p);
+    } catch (const std::invalid_argument&) {
+        wrong_dtype = true;
+    }
+    expect(wrong_dtype, "f16 decode rejects an f32 payload");
+    inference::Payload tokens;
+    tokens.kind = inference::PayloadKind::Tokens;
+    tokens.tensor.dtype = "f32";
+    bool not_activation = false;
+    try {
+        (void) f16->encode(tokens);
+    } catch (const std::invalid_argument&) {
+        not_activation = true;
+    }
+    expect(not_activation, "codecs take activation payloads only");
+}
+
 int main() {
     test_prompt_lookup();
+    test_activation_codecs();
     test_accepts_prefix_and_rolls_back_suffix();
     test_recovery_pass_after_rejection();
     test_rollback_failure_emits_nothing_rejected();
