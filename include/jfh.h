@@ -155,6 +155,13 @@ jfh_status jfh_package_source_sha256(const jfh_package * package, uint8_t digest
 jfh_status jfh_model_open(const char * package_path, uint32_t layer_start, uint32_t layer_end,
                           uint32_t verify_hashes, jfh_model ** out);
 
+/* jf_model_compile's input side (runtime/compiler/jf_model_compile.cpp:549-645):
+ * a qwen2 GGUF file, memory-mapped, as a host model whose tensors are used in
+ * place; jfh_model_write_package then writes its JFM v2 package, recording
+ * the file's SHA-256 and size. Tensor types F32, F16, Q8_0, Q2_K, Q4_K, Q6_K;
+ * output.weight is required (JFM v2 has no tied output). */
+jfh_status jfh_model_open_gguf(const char * gguf_path, jfh_model ** out);
+
 /* Synthetic weights for benchmarks (no reference counterpart: the reference
  * imports real GGUFs, runtime/compiler/jf_model_compile.cpp:549-645). */
 jfh_status jfh_model_synthesize(const jfh_synth_spec * spec, jfh_model ** out);

@@ -98,6 +98,7 @@ SIGNATURES = {
     "jfh_tensor_type_layout": (Status, [c_uint32, POINTER(c_uint32), POINTER(c_uint32)]),
     "jfh_sha256": (Status, [c_void_p, c_size_t, POINTER(c_uint8)]),
     "jfh_model_open": (Status, [c_char_p, c_uint32, c_uint32, c_uint32, POINTER(c_void_p)]),
+    "jfh_model_open_gguf": (Status, [c_char_p, POINTER(c_void_p)]),
     "jfh_model_synthesize": (Status, [POINTER(SynthSpec), POINTER(c_void_p)]),
     "jfh_model_create": (Status, [POINTER(ModelParams), POINTER(c_void_p)]),
     "jfh_model_add_tensor": (Status, [c_void_p, c_char_p, c_uint32, c_uint32, POINTER(c_uint64), c_void_p, c_uint64]),

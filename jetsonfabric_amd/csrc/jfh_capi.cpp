@@ -198,6 +198,17 @@ jfh_status jfh_package_source_sha256(const jfh_package* package, uint8_t digest[
     });
 }
 
+jfh_status jfh_model_open_gguf(const char* gguf_path, jfh_model** out) {
+    return guarded([&] {
+        require(gguf_path && out, "GGUF path and output are required");
+        *out = nullptr;
+        auto m = std::make_unique<jfh_model>();
+        m->model = jfh::HostModel::open_gguf(gguf_path);
+        refresh_names(m.get());
+        *out = m.release();
+    });
+}
+
 jfh_status jfh_model_open(const char* package_path, uint32_t layer_start, uint32_t layer_end, uint32_t verify_hashes,
                           jfh_model** out) {
     return guarded([&] {

@@ -473,6 +473,124 @@ std::map<std::string, GgufValue> parse_gguf_kv(const uint8_t* data, size_t size)
     return out;
 }
 
+uint32_t jfm_type_from_ggml(uint32_t t) {
+    switch (t) {
+    case 0: return kF32;
+    case 1: return kF16;
+    case 8: return kQ8_0;
+    case 10: return kQ2_K;
+    case 12: return kQ4_K;
+    case 14: return kQ6_K;
+    default: return UINT32_MAX;
+    }
+}
+
+uint32_t ggml_type_from_jfm(uint32_t t) {
+    switch (t) {
+    case kF32: return 0;
+    case kF16: return 1;
+    case kQ8_0: return 8;
+    case kQ2_K: return 10;
+    case kQ4_K: return 12;
+    case kQ6_K: return 14;
+    default: return UINT32_MAX;
+    }
+}
+
+GgufLayout parse_gguf_layout(const uint8_t* data, size_t size) {
+    size_t c = 0;
+    auto need = [&](size_t n) { if (!fits(c, n, size)) fail(Status::FormatError, "GGUF header is truncated"); };
+    auto str = [&]() {
+        need(8);
+        const uint64_t n = rd64(data + c);
+        c += 8;
+        need(n);
+        std::string s(reinterpret_cast<const char*>(data + c), size_t(n));
+        c += size_t(n);
+        return s;
+    };
+    need(24);
+    if (std::memcmp(data, "GGUF", 4) != 0) fail(Status::FormatError, "file is not GGUF");
+    const uint32_t version = rd32(data + 4);
+    if (version < 2 || version > 3) fail(Status::FormatError, "unsupported GGUF version");
+    const uint64_t n_tensors = rd64(data + 8), n_kv = rd64(data + 16);
+    c = 24;
+    GgufLayout out;
+    for (uint64_t i = 0; i < n_kv; ++i) {
+        const std::string key = str();
+        need(4);
+        const uint32_t type = rd32(data + c);
+        c += 4;
+        if (type == G_STR) {
+            (void) str();
+        } else if (type == G_ARR) {
+            need(12);
+            const uint32_t et = rd32(data + c);
+            const uint64_t n = rd64(data + c + 4);
+            c += 12;
+            if (et == G_STR) {
+                for (uint64_t k = 0; k < n; ++k) (void) str();
+            } else {
+                const size_t es = scalar_size(et);
+                if (es == 0 || n > size / es) fail(Status::FormatError, "GGUF array is invalid");
+                need(size_t(n) * es);
+                c += size_t(n) * es;
+            }
+        } else {
+            const size_t es = scalar_size(type);
+            if (es == 0) fail(Status::FormatError, "GGUF value type is invalid");
+            need(es);
+            if (key == "general.alignment") {
+                if (type != G_U32) fail(Status::FormatError, "general.alignment must be u32");
+                out.alignment = rd32(data + c);
+                if (out.alignment == 0 || (out.alignment & (out.alignment - 1)) != 0) {
+                    fail(Status::FormatError, "general.alignment must be a power of two");
+                }
+            }
+            c += es;
+        }
+    }
+    if (n_tensors > size / 24) fail(Status::FormatError, "GGUF tensor count is invalid");
+    for (uint64_t i = 0; i < n_tensors; ++i) {
+        GgufTensorInfo t;
+        t.name = str();
+        need(4);
+        t.rank = rd32(data + c);
+        c += 4;
+        if (t.rank == 0 || t.rank > 4) fail(Status::FormatError, "GGUF tensor rank must be 1..4: " + t.name);
+        need(8 * size_t(t.rank) + 12);
+        for (uint32_t d = 0; d < t.rank; ++d) t.shape[d] = rd64(data + c + 8 * d);
+        c += 8 * size_t(t.rank);
+        t.type = rd32(data + c);
+        t.offset = rd64(data + c + 4);
+        c += 12;
+        out.tensors.push_back(std::move(t));
+    }
+    out.data_offset = (uint64_t(c) + out.alignment - 1) / out.alignment * out.alignment;
+    return out;
+}
+
+std::shared_ptr<const MappedFile> MappedFile::open(const std::string& path) {
+    const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+    if (fd < 0) fail(Status::IoError, "open " + path + ": " + std::strerror(errno));
+    struct stat st{};
+    if (::fstat(fd, &st) != 0 || !S_ISREG(st.st_mode) || st.st_size <= 0) {
+        ::close(fd);
+        fail(Status::IoError, path + " is not a regular, non-empty file");
+    }
+    void* addr = ::mmap(nullptr, size_t(st.st_size), PROT_READ, MAP_PRIVATE, fd, 0);
+    ::close(fd);
+    if (addr == MAP_FAILED) fail(Status::IoError, "map " + path);
+    auto m = std::shared_ptr<MappedFile>(new MappedFile());
+    m->data_ = static_cast<const uint8_t*>(addr);
+    m->size_ = size_t(st.st_size);
+    return m;
+}
+
+MappedFile::~MappedFile() {
+    if (data_) ::munmap(const_cast<uint8_t*>(data_), size_);
+}
+
 std::vector<uint8_t> write_gguf_header(const std::vector<std::pair<std::string, GgufValue>>& kv,
                                        const std::vector<GgufTensorInfo>& tensors) {
     std::vector<uint8_t> o;
@@ -493,7 +611,9 @@ std::vector<uint8_t> write_gguf_header(const std::vector<std::pair<std::string, 
         put_str(t.name);
         put32(o, t.rank);
         for (uint32_t d = 0; d < t.rank; ++d) put64(o, t.shape[d]);
-        put32(o, t.type);  // JFM ids equal GGML type ids for every type this engine writes
+        const uint32_t ggml = ggml_type_from_jfm(t.type);
+        if (ggml == UINT32_MAX) fail(Status::InvalidArgument, "tensor type has no GGML id: " + t.name);
+        put32(o, ggml);
         put64(o, t.offset);
     }
     pad(o, 32);
@@ -522,7 +642,8 @@ std::pair<std::array<uint8_t, 32>, uint64_t> source_digest(const std::vector<uin
 }
 
 void write_package(const std::string& dir, uint32_t layer_count, const std::vector<uint8_t>& gguf_header,
-                   const std::vector<TensorBlob>& tensors) {
+                   const std::vector<TensorBlob>& tensors,
+                   const std::pair<std::array<uint8_t, 32>, uint64_t>* source) {
     namespace fs = std::filesystem;
     std::error_code ec;
     fs::create_directories(dir, ec);
@@ -649,7 +770,7 @@ void write_package(const std::string& dir, uint32_t layer_count, const std::vect
     if (groups.count("shared.jfs")) take("shared.jfs");
     if (!groups.empty()) fail(Status::InvalidArgument, "tensor belongs to a layer outside the model");
 
-    const auto [src_sha, src_size] = source_digest(gguf_header, tensors);
+    const auto [src_sha, src_size] = source ? *source : source_digest(gguf_header, tensors);
 
     std::vector<uint8_t> man;
     man.insert(man.end(), {'J', 'F', 'M', 'O', 'D', 'E', 'L', '2'});

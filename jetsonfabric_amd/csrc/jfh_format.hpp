@@ -132,8 +132,40 @@ struct GgufTensorInfo {
 // Parses the KV section of a GGUF header; unknown value kinds are skipped.
 std::map<std::string, GgufValue> parse_gguf_kv(const uint8_t* data, size_t size);
 
-// Serializes a GGUF header: magic, version 3, KVs in order, tensor infos,
-// padded to the 32-byte data alignment (the bytes before the data section).
+// GGML type ids (the ids GGUF tensor infos carry) <-> JFM v2 tensor type ids
+// (engine.h:13-44; jf_model_compile.cpp:499-531) for the types this engine
+// runs; UINT32_MAX for any other.
+uint32_t jfm_type_from_ggml(uint32_t ggml_type);
+uint32_t ggml_type_from_jfm(uint32_t jfm_type);
+
+// The tensor section of a GGUF v2/v3 file: tensor infos (types as GGML ids)
+// and the data section's offset (header end rounded up to general.alignment).
+struct GgufLayout {
+    std::vector<GgufTensorInfo> tensors;
+    uint64_t data_offset = 0;
+    uint32_t alignment = 32;
+};
+GgufLayout parse_gguf_layout(const uint8_t* data, size_t size);
+
+// A read-only memory mapping of a whole file.
+class MappedFile {
+public:
+    static std::shared_ptr<const MappedFile> open(const std::string& path);
+    ~MappedFile();
+    MappedFile(const MappedFile&) = delete;
+    MappedFile& operator=(const MappedFile&) = delete;
+    const uint8_t* data() const { return data_; }
+    size_t size() const { return size_; }
+
+private:
+    MappedFile() = default;
+    const uint8_t* data_ = nullptr;
+    size_t size_ = 0;
+};
+
+// Serializes a GGUF header: magic, version 3, KVs in order, tensor infos
+// (JFM type ids written as their GGML ids), padded to the 32-byte data
+// alignment (the bytes before the data section).
 std::vector<uint8_t> write_gguf_header(const std::vector<std::pair<std::string, GgufValue>>& kv,
                                        const std::vector<GgufTensorInfo>& tensors);
 
@@ -155,7 +187,10 @@ std::pair<std::array<uint8_t, 32>, uint64_t> source_digest(const std::vector<uin
 
 // Writes a JFM v2 package: manifest.jfm, metadata.gguf, input/output/shared and
 // one segment per layer, grouped by name (runtime/compiler/jf_model_compile.cpp:612-624).
+// source: the source GGUF's SHA-256 and size for the manifest; by default
+// source_digest(gguf_header, tensors).
 void write_package(const std::string& dir, uint32_t layer_count, const std::vector<uint8_t>& gguf_header,
-                   const std::vector<TensorBlob>& tensors);
+                   const std::vector<TensorBlob>& tensors,
+                   const std::pair<std::array<uint8_t, 32>, uint64_t>* source = nullptr);
 
 }  // namespace jfh

@@ -305,6 +305,55 @@ std::unique_ptr<HostModel> HostModel::open_package(const std::string& dir, const
     return m;
 }
 
+std::unique_ptr<HostModel> HostModel::open_gguf(const std::string& path) {
+    auto m = std::unique_ptr<HostModel>(new HostModel());
+    m->gguf_file_ = MappedFile::open(path);
+    const uint8_t* data = m->gguf_file_->data();
+    const uint64_t size = m->gguf_file_->size();
+    m->params_ = parse_qwen2_params(data, size_t(size));
+    const GgufLayout layout = parse_gguf_layout(data, size_t(size));
+    if (layout.data_offset > size) fail(Status::FormatError, "GGUF data section starts past end of file");
+    m->gguf_data_offset_ = layout.data_offset;
+    for (const GgufTensorInfo& t : layout.tensors) {
+        TensorView v;
+        v.name = t.name;
+        v.type = jfm_type_from_ggml(t.type);
+        if (v.type == UINT32_MAX) fail(Status::FormatError, "unsupported GGUF tensor type for " + t.name);
+        v.rank = t.rank;
+        uint64_t rows = 1;
+        for (uint32_t d = 0; d < 4; ++d) {
+            v.shape[d] = d < t.rank ? t.shape[d] : 1;
+            if (v.shape[d] == 0) fail(Status::FormatError, "tensor has an invalid shape: " + t.name);
+            if (d > 0) rows *= v.shape[d];
+        }
+        uint32_t be = 0, bb = 0;
+        if (!type_layout(v.type, &be, &bb) || v.shape[0] % be != 0) {
+            fail(Status::FormatError, "tensor rows are not whole blocks: " + t.name);
+        }
+        v.size = row_bytes(v.type, v.shape[0]) * rows;
+        if (t.offset % layout.alignment != 0 || t.offset > size - layout.data_offset ||
+            v.size > size - layout.data_offset - t.offset) {
+            fail(Status::FormatError, "tensor exceeds the source GGUF: " + t.name);
+        }
+        v.data = data + layout.data_offset + t.offset;
+        if (t.name.rfind("blk.", 0) == 0) {
+            const uint32_t layer = uint32_t(std::stoul(t.name.substr(4, t.name.find('.', 4) - 4)));
+            if (layer >= m->params_.n_layer) fail(Status::FormatError, "tensor block exceeds model block count: " + t.name);
+            v.layer = int32_t(layer);
+        }
+        m->tensors_.push_back(v);
+    }
+    if (!m->find("output.weight")) {
+        fail(Status::FormatError, "tied output embeddings are not supported by JFM v2; output.weight is required");
+    }
+    m->gguf_sha_ = sha256(data, size_t(size));
+    m->source_sha256_ = hex(m->gguf_sha_.data(), 32);
+    m->layer_start_ = 0;
+    m->layer_end_ = m->params_.n_layer;
+    m->finalize();
+    return m;
+}
+
 std::unique_ptr<HostModel> HostModel::build(const ModelParams& params) {
     auto m = std::unique_ptr<HostModel>(new HostModel());
     m->params_ = params;
@@ -399,12 +448,13 @@ void HostModel::finalize() {
         shape(pre + "ffn_up.weight", {H, F});
         shape(pre + "ffn_down.weight", {F, H});
     }
-    if (!package_) {
+    if (!package_ && !gguf_file_) {
         source_sha256_ = hex(source_digest(gguf_header(), blobs()).first.data(), 32);
     }
 }
 
 std::vector<uint8_t> HostModel::gguf_header() const {
+    if (gguf_file_) return std::vector<uint8_t>(gguf_file_->data(), gguf_file_->data() + gguf_data_offset_);
     if (package_) {
         return std::vector<uint8_t>(package_->gguf_metadata(), package_->gguf_metadata() + package_->gguf_metadata_size());
     }
@@ -459,6 +509,12 @@ std::vector<TensorBlob> HostModel::blobs() const {
 
 void HostModel::write_package(const std::string& dir) const {
     if (layer_start_ != 0 || layer_end_ != params_.n_layer) fail(Status::InvalidArgument, "only a full model can be written as a package");
+    if (gguf_file_) {
+        // the manifest records the imported file itself
+        const std::pair<std::array<uint8_t, 32>, uint64_t> source{gguf_sha_, gguf_file_->size()};
+        jfh::write_package(dir, params_.n_layer, gguf_header(), blobs(), &source);
+        return;
+    }
     jfh::write_package(dir, params_.n_layer, gguf_header(), blobs());
 }
 

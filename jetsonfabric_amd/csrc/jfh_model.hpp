@@ -47,6 +47,10 @@ class HostModel {
 public:
     static std::unique_ptr<HostModel> open_package(const std::string& dir, const StagePlan& plan);
     static std::unique_ptr<HostModel> synthesize(const SynthSpec& spec);
+    // A qwen2 GGUF file (memory-mapped) as a model, for writing its JFM v2
+    // package (jf_model_compile.cpp:549-645): tensors of the types this
+    // engine runs, output.weight required, source SHA-256 of the whole file.
+    static std::unique_ptr<HostModel> open_gguf(const std::string& path);
     // Starts an empty model; tensors are added with add_tensor (bytes are copied).
     static std::unique_ptr<HostModel> build(const ModelParams& params);
 
@@ -76,6 +80,9 @@ private:
 
     ModelParams params_;
     std::unique_ptr<Package> package_;
+    std::shared_ptr<const MappedFile> gguf_file_;  // imported GGUF
+    uint64_t gguf_data_offset_ = 0;
+    std::array<uint8_t, 32> gguf_sha_{};
     std::vector<std::vector<uint8_t>> owned_;
     std::vector<TensorView> tensors_;
     uint32_t layer_start_ = 0;

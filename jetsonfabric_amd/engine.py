@@ -154,6 +154,14 @@ class Model:
         return cls(h.value)
 
     @classmethod
+    def open_gguf(cls, path: str) -> "Model":
+        """A qwen2 GGUF file as a model (jf_model_compile's input); write_package() then writes
+        its JFM v2 package with the file's SHA-256 as the source digest."""
+        h = ctypes.c_void_p()
+        check(library().jfh_model_open_gguf(path.encode(), ctypes.byref(h)))
+        return cls(h.value)
+
+    @classmethod
     def synthesize(cls, config: ModelConfig, type_linear: int = Q4_K, type_embd: int = Q4_K, type_output: int = Q6_K,
                    tied_output: bool = False, output_bias: bool = False, seed: int = 1234, stddev: float = 0.02,
                    threads: int = 0) -> "Model":
