@@ -750,8 +750,11 @@ struct TileQ4Quad {
 
 // Q6_K tiles x 4..8 int8 token rows on matrix cores, with the operand layout
 // of TileQ4Quad: one MFMA per 8-value chunk, two chunks per 16-value
-// sub-block, so D holds sub-block dots of lane group G' per (token, row); the
-// scale and offset arithmetic per lane group is Tile<13>::dot's.
+// sub-block, so D holds sub-block dots of lane group G' per (token, row). The
+// B operand carries the signed codes q - 32 (bytewise (q + 0x60) ^ 0x80 for
+// q in 0..63), so D is Tile<13>::dot's dm - 32 * s exactly (integer
+// arithmetic) and the code sums are not read; the scale arithmetic per lane
+// group is Tile<13>::dot's.
 struct TileQ6Quad {
     struct Regs {
         uint4 c0, c1, c2, sc;
@@ -784,8 +787,12 @@ struct TileQ6Quad {
             const uint32_t w1 = ((Lw[2 * m] >> 4) & M4) | ((Hb[m] << 2) & M30);
             const uint32_t w2 = (Lw[2 * m + 1] & M4) | (Hb[m] & M30);
             const uint32_t w3 = ((Lw[2 * m + 1] >> 4) & M4) | ((Hb[m] >> 2) & M30);
-            b[2 * m] = static_cast<long>(static_cast<uint64_t>(w0) | (static_cast<uint64_t>(w1) << 32));
-            b[2 * m + 1] = static_cast<long>(static_cast<uint64_t>(w2) | (static_cast<uint64_t>(w3) << 32));
+            // q - 32 per byte: q + 0x60 stays below 0x100, the xor moves the bias to -0x80
+            constexpr uint32_t B60 = 0x60606060u, S80 = 0x80808080u;
+            const uint32_t s0 = (w0 + B60) ^ S80, s1 = (w1 + B60) ^ S80;
+            const uint32_t s2 = (w2 + B60) ^ S80, s3 = (w3 + B60) ^ S80;
+            b[2 * m] = static_cast<long>(static_cast<uint64_t>(s0) | (static_cast<uint64_t>(s1) << 32));
+            b[2 * m + 1] = static_cast<long>(static_cast<uint64_t>(s2) | (static_cast<uint64_t>(s3) << 32));
         }
         const bool own = (i & 3) == L;
 #pragma unroll
@@ -805,18 +812,11 @@ struct TileQ6Quad {
             }
             const int tk = min(4 * q + L, nt - 1);
             const float xd = x.d[tk * x.d_stride];
-            const u32x4* sp = reinterpret_cast<const u32x4*>(x.s + tk * x.s_stride);
-            const u32x4 s03 = sp[0], s47 = sp[1];
-            const uint32_t sw[8] = {s03.x, s03.y, s03.z, s03.w, s47.x, s47.y, s47.z, s47.w};
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 int isum = 0;
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    const int j = 4 * g + m;  // sub-block of the block
-                    const int sj = static_cast<int16_t>((sw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
-                    isum += mul24(sext8(scw[g] >> (8 * m)), D[m][g] - 32 * sj);
-                }
+                for (int m = 0; m < 4; ++m) isum += mul24(sext8(scw[g] >> (8 * m)), D[m][g]);
                 acc[4 * q + g] = __builtin_fmaf(xd, d * static_cast<float>(isum), acc[4 * q + g]);
             }
         }
