@@ -136,3 +136,23 @@ def test_batch_of_sessions_matches_individual_steps(workload):
         s_ids, s_acc = single.verify(rows[i])
         assert ids[i] == s_ids and accepted[i] == s_acc, f"sequence {i}"
         single.close()
+
+
+def test_concurrent_generation_equals_each_alone(workload):
+    """The workload's continuous batching at its real widths: concurrent
+    runners (decode steps, and draft-verify steps where the workload drafts,
+    coalesced into one multi-sequence forward) give every request the tokens
+    and pass counts it gets alone."""
+    wl, cfg, _, engine, _, _ = workload
+    count = min(max(wl.concurrency, 2), 4)
+    prompts = []
+    for i in range(count):
+        seg = _prompt(10 + 2 * i, cfg.n_vocab, 60 + i)
+        prompts.append(seg + seg + seg[: 4 + i])  # repetitive: prompt lookup finds drafts
+    draft = wl.draft_max
+    results, _ = engine.generate_concurrent(prompts, 12, draft_max=draft, max_ngram=3, min_ngram=3,
+                                            batch_wait_us=2000)
+    for prompt, got in zip(prompts, results):
+        alone = engine.generate(prompt, 12, draft_max=draft, max_ngram=3, min_ngram=3)
+        assert got.sampled_tokens == alone.sampled_tokens
+        assert got.target_decode_passes == alone.target_decode_passes
