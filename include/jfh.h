@@ -178,6 +178,13 @@ jfh_status jfh_model_finalize(jfh_model * model);
  * runtime/compiler/jf_model_compile.cpp:612-624). */
 jfh_status jfh_model_write_package(const jfh_model * model, const char * directory);
 
+/* The layer range [layer_start, layer_end) of a finalized model as a model of
+ * its own (its tensors copied; the embedding when layer_start is 0, the
+ * output norm and head when layer_end is n_layer), the in-memory counterpart
+ * of opening a package with a layer range (jf_model_open, engine.h:106-111;
+ * engine.c:513-757). An engine created from it is that pipeline stage. */
+jfh_status jfh_model_slice(const jfh_model * model, uint32_t layer_start, uint32_t layer_end, jfh_model ** out);
+
 /* jf_model_close (engine.h:113). */
 void jfh_model_close(jfh_model * model);
 
@@ -231,16 +238,18 @@ jfh_status jfh_session_verify(jfh_session * session, const int32_t * tokens, uin
  * previous stage's activations, f32 [n][n_embd] (the residual stream after
  * its last layer); the last stage (layer_end n_layer) writes the greedy id of
  * the last row to out_token, earlier stages write every row's activations to
- * out_activations. Pass NULL for the unused input and output.
+ * out_activations. Pass NULL for the unused input and output. logits may be
+ * NULL; on the last stage it receives n_vocab floats for the last row (as
+ * jfh_session_prefill's logits), other stages reject it.
  * NativeSession::prefill_stage_tokens / prefill_stage_activations
  * (native_inference.hpp:112-113; qwen2_architecture.cpp:909-926, 977-1002). */
 jfh_status jfh_session_stage_prefill(jfh_session * session, const int32_t * tokens, const float * activations,
-                                     uint32_t n, int32_t * out_token, float * out_activations);
+                                     uint32_t n, int32_t * out_token, float * out_activations, float * logits);
 /* One row: NativeSession::decode_stage_token / decode_stage_activation
  * (native_inference.hpp:114-115; qwen2_architecture.cpp:928-947, 1004-1027).
  * token points to the first stage's input id (NULL on later stages). */
 jfh_status jfh_session_stage_decode(jfh_session * session, const int32_t * token, const float * activation,
-                                    int32_t * out_token, float * out_activation);
+                                    int32_t * out_token, float * out_activation, float * logits);
 
 /* Activation codecs between pipeline stages (ActivationCodec, created by
  * name from the default factory: runtime/activation/activation_codec.hpp:9-18,
@@ -259,10 +268,11 @@ jfh_status jfh_session_rollback(jfh_session * session, uint32_t n);
  * (Executor::execute_batch, runtime/inference/executor.hpp:20-28;
  * continuous_batching_executor.cpp:60-100). lengths[i] rows for sessions[i],
  * tokens concatenated; out_tokens receives sum(lengths) ids, out_accepted one
- * count per session (may be NULL). */
+ * count per session (may be NULL), logits (may be NULL) sum(lengths) *
+ * n_vocab floats, the rows in the order of out_tokens. */
 jfh_status jfh_engine_step_batch(jfh_engine * engine, jfh_session * const * sessions, uint32_t count,
                                  const int32_t * tokens, const uint32_t * lengths, int32_t * out_tokens,
-                                 uint32_t * out_accepted);
+                                 uint32_t * out_accepted, float * logits);
 
 /* Parity entry points: GPU dequantization of tensor rows (bit-exact with the
  * GGML layouts) and a matmul through the engine's kernels. */

@@ -104,6 +104,7 @@ SIGNATURES = {
     "jfh_model_add_tensor": (Status, [c_void_p, c_char_p, c_uint32, c_uint32, POINTER(c_uint64), c_void_p, c_uint64]),
     "jfh_model_finalize": (Status, [c_void_p]),
     "jfh_model_write_package": (Status, [c_void_p, c_char_p]),
+    "jfh_model_slice": (Status, [c_void_p, c_uint32, c_uint32, POINTER(c_void_p)]),
     "jfh_model_close": (None, [c_void_p]),
     "jfh_model_get_params": (Status, [c_void_p, POINTER(ModelParams)]),
     "jfh_model_get_stats": (Status, [c_void_p, POINTER(ModelStats)]),
@@ -126,11 +127,11 @@ SIGNATURES = {
     "jfh_activation_encode": (Status, [c_char_p, POINTER(c_float), c_size_t, c_void_p, c_size_t]),
     "jfh_activation_decode": (Status, [c_char_p, c_void_p, c_size_t, POINTER(c_float), c_size_t]),
     "jfh_session_stage_prefill": (Status, [c_void_p, POINTER(c_int32), POINTER(c_float), c_uint32, POINTER(c_int32),
-                                           POINTER(c_float)]),
+                                           POINTER(c_float), POINTER(c_float)]),
     "jfh_session_stage_decode": (Status, [c_void_p, POINTER(c_int32), POINTER(c_float), POINTER(c_int32),
-                                          POINTER(c_float)]),
+                                          POINTER(c_float), POINTER(c_float)]),
     "jfh_engine_step_batch": (Status, [c_void_p, POINTER(c_void_p), c_uint32, POINTER(c_int32), POINTER(c_uint32),
-                                       POINTER(c_int32), POINTER(c_uint32)]),
+                                       POINTER(c_int32), POINTER(c_uint32), POINTER(c_float)]),
     "jfh_engine_dequantize": (Status, [c_void_p, c_char_p, c_uint32, c_uint32, POINTER(c_float)]),
     "jfh_engine_matmul": (Status, [c_void_p, c_char_p, POINTER(c_float), c_uint32, POINTER(c_float)]),
     "jfh_session_read_kv": (Status, [c_void_p, c_uint32, c_uint32, POINTER(c_uint16), POINTER(c_uint16)]),

@@ -282,6 +282,17 @@ jfh_status jfh_model_write_package(const jfh_model* model, const char* directory
     });
 }
 
+jfh_status jfh_model_slice(const jfh_model* model, uint32_t layer_start, uint32_t layer_end, jfh_model** out) {
+    return guarded([&] {
+        require(model && out && model->finalized, "a finalized model and an output are required");
+        *out = nullptr;
+        auto m = std::make_unique<jfh_model>();
+        m->model = model->model->slice(layer_start, layer_end);
+        refresh_names(m.get());
+        *out = m.release();
+    });
+}
+
 void jfh_model_close(jfh_model* model) { delete model; }
 
 jfh_status jfh_model_get_params(const jfh_model* model, jfh_model_params* out) {
@@ -434,23 +445,25 @@ jfh_status jfh_session_verify(jfh_session* session, const int32_t* tokens, uint3
 }
 
 jfh_status jfh_session_stage_prefill(jfh_session* session, const int32_t* tokens, const float* activations,
-                                     uint32_t n, int32_t* out_token, float* out_activations) {
+                                     uint32_t n, int32_t* out_token, float* out_activations, float* logits) {
     return guarded([&] {
         require(session, "session is required");
         jfh::Engine& e = *session->owner->engine;
         require(!e.last_stage() || out_token, "the final stage writes a token");
-        const int32_t token = e.stage_prefill(*session->session, tokens, activations, n, out_activations);
+        require(e.last_stage() || !logits, "only the final stage computes logits");
+        const int32_t token = e.stage_prefill(*session->session, tokens, activations, n, out_activations, logits);
         if (out_token) *out_token = token;
     });
 }
 
 jfh_status jfh_session_stage_decode(jfh_session* session, const int32_t* token, const float* activation,
-                                    int32_t* out_token, float* out_activation) {
+                                    int32_t* out_token, float* out_activation, float* logits) {
     return guarded([&] {
         require(session, "session is required");
         jfh::Engine& e = *session->owner->engine;
         require(!e.last_stage() || out_token, "the final stage writes a token");
-        const int32_t t = e.stage_decode(*session->session, token, activation, out_activation);
+        require(e.last_stage() || !logits, "only the final stage computes logits");
+        const int32_t t = e.stage_decode(*session->session, token, activation, out_activation, logits);
         if (out_token) *out_token = t;
     });
 }
@@ -499,7 +512,7 @@ jfh_status jfh_session_rollback(jfh_session* session, uint32_t n) {
 
 jfh_status jfh_engine_step_batch(jfh_engine* engine, jfh_session* const* sessions, uint32_t count,
                                  const int32_t* tokens, const uint32_t* lengths, int32_t* out_tokens,
-                                 uint32_t* out_accepted) {
+                                 uint32_t* out_accepted, float* logits) {
     return guarded([&] {
         require(engine && sessions && tokens && lengths && out_tokens && count > 0, "batch arguments are required");
         std::vector<jfh::SeqStep> steps;
@@ -516,7 +529,7 @@ jfh_status jfh_engine_step_batch(jfh_engine* engine, jfh_session* const* session
             steps.push_back(st);
         }
         std::vector<int32_t> accepted(count);
-        engine->engine->forward(steps, out_tokens, accepted.data(), nullptr);
+        engine->engine->forward(steps, out_tokens, accepted.data(), logits);
         if (out_accepted) {
             for (uint32_t i = 0; i < count; ++i) out_accepted[i] = static_cast<uint32_t>(accepted[i]);
         }

@@ -940,7 +940,7 @@ int32_t Engine::prefill(Session& s, const int32_t* tokens, uint32_t n, float* lo
 }
 
 int32_t Engine::stage_prefill(Session& s, const int32_t* tokens, const float* activations, uint32_t n,
-                              float* act_out) {
+                              float* act_out, float* logits) {
     if (first_stage() && activations != nullptr) {
         fail(Status::InvalidArgument, "the first native stage does not accept activations");
     }
@@ -964,14 +964,16 @@ int32_t Engine::stage_prefill(Session& s, const int32_t* tokens, const float* ac
         st.activations = activations ? activations + done * H : nullptr;
         st.n = len;
         st.logits = last && last_stage() ? 1 : 0;
-        forward({st}, st.logits ? &token : nullptr, nullptr, nullptr, act_out ? act_out + done * H : nullptr);
+        forward({st}, st.logits ? &token : nullptr, nullptr, st.logits ? logits : nullptr,
+                act_out ? act_out + done * H : nullptr);
         done += len;
     }
     s.prefill_position_ = n;
     return token;
 }
 
-int32_t Engine::stage_decode(Session& s, const int32_t* token, const float* activation, float* act_out) {
+int32_t Engine::stage_decode(Session& s, const int32_t* token, const float* activation, float* act_out,
+                             float* logits) {
     if (first_stage() && activation != nullptr) {
         fail(Status::InvalidArgument, "the first native stage does not accept decode activations");
     }
@@ -991,7 +993,7 @@ int32_t Engine::stage_decode(Session& s, const int32_t* token, const float* acti
     st.n = 1;
     st.logits = last_stage() ? 1 : 0;
     int32_t out = -1;
-    forward({st}, st.logits ? &out : nullptr, nullptr, nullptr, act_out);
+    forward({st}, st.logits ? &out : nullptr, nullptr, st.logits ? logits : nullptr, act_out);
     return out;
 }
 

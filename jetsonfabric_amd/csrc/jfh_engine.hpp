@@ -119,9 +119,12 @@ public:
     // qwen2_architecture.cpp:909-947, 977-1027): token ids into the first
     // stage, activations into the others; the last stage returns the greedy
     // id of the last row, the others write every row's activations to
-    // act_out and return -1.
-    int32_t stage_prefill(Session& s, const int32_t* tokens, const float* activations, uint32_t n, float* act_out);
-    int32_t stage_decode(Session& s, const int32_t* token, const float* activation, float* act_out);
+    // act_out and return -1. The last stage also writes the last row's
+    // logits to `logits` when it is set.
+    int32_t stage_prefill(Session& s, const int32_t* tokens, const float* activations, uint32_t n, float* act_out,
+                          float* logits = nullptr);
+    int32_t stage_decode(Session& s, const int32_t* token, const float* activation, float* act_out,
+                         float* logits = nullptr);
 
     // Parity entry points: dequantize rows of a device tensor; multiply a
     // device matrix with host activations through the same kernels.

@@ -363,6 +363,25 @@ std::unique_ptr<HostModel> HostModel::build(const ModelParams& params) {
     return m;
 }
 
+std::unique_ptr<HostModel> HostModel::slice(uint32_t start, uint32_t end) const {
+    if (start >= end || start < layer_start_ || end > layer_end_) {
+        fail(Status::InvalidArgument, "native Qwen2 layer range is invalid");
+    }
+    auto m = build(params_);
+    m->layer_start_ = start;
+    m->layer_end_ = end;
+    for (const TensorView& t : tensors_) {
+        const bool keep = t.layer >= 0 ? static_cast<uint32_t>(t.layer) >= start && static_cast<uint32_t>(t.layer) < end
+                          : t.name == "token_embd.weight" ? start == 0
+                                                          : end == params_.n_layer;
+        if (keep) m->add_tensor(t.name, t.type, t.rank, t.shape, t.data, t.size);
+    }
+    m->source_sha256_ = source_sha256_;
+    m->keep_digest_ = true;
+    m->finalize();
+    return m;
+}
+
 void HostModel::add_tensor(const std::string& name, uint32_t type, uint32_t rank, const uint64_t* shape,
                            const void* data, uint64_t size) {
     if (package_) fail(Status::InvalidArgument, "cannot add tensors to a package-backed model");
@@ -448,7 +467,7 @@ void HostModel::finalize() {
         shape(pre + "ffn_up.weight", {H, F});
         shape(pre + "ffn_down.weight", {F, H});
     }
-    if (!package_ && !gguf_file_) {
+    if (!package_ && !gguf_file_ && !keep_digest_) {
         source_sha256_ = hex(source_digest(gguf_header(), blobs()).first.data(), 32);
     }
 }

@@ -53,6 +53,11 @@ public:
     static std::unique_ptr<HostModel> open_gguf(const std::string& path);
     // Starts an empty model; tensors are added with add_tensor (bytes are copied).
     static std::unique_ptr<HostModel> build(const ModelParams& params);
+    // The tensors of layers [start, end) of this model (plus the embedding
+    // for a first stage and the output norm and head for a last one) as a
+    // model of its own, as jf_model_open selects a package's layer range
+    // (engine.c:513-757). Bytes are copied; the source digest is kept.
+    std::unique_ptr<HostModel> slice(uint32_t start, uint32_t end) const;
 
     void add_tensor(const std::string& name, uint32_t type, uint32_t rank, const uint64_t* shape,
                     const void* data, uint64_t size);
@@ -88,6 +93,7 @@ private:
     uint32_t layer_start_ = 0;
     uint32_t layer_end_ = 0;
     std::string source_sha256_;
+    bool keep_digest_ = false;  // a slice keeps its source model's digest
 };
 
 // Parses and validates qwen2.* GGUF keys (qwen2_metadata.cpp:90-125).

@@ -186,6 +186,13 @@ class Model:
         check(lib.jfh_model_finalize(model._h))
         return model
 
+    def slice(self, layer_start: int, layer_end: int) -> "Model":
+        """Layers [layer_start, layer_end) as a model of their own: an engine over
+        it is that pipeline stage (jf_model_open's layer range, engine.h:106-111)."""
+        h = ctypes.c_void_p()
+        check(library().jfh_model_slice(self._h, layer_start, layer_end, ctypes.byref(h)))
+        return Model(h.value)
+
     def close(self) -> None:
         if self._h:
             library().jfh_model_close(self._h)
@@ -326,25 +333,41 @@ class NativeSession:
         return (src, src.ctypes.data_as(f32) if src is not None else None, out,
                 out.ctypes.data_as(f32) if out is not None else None)
 
-    def prefill_stage(self, tokens: Sequence[int] | None = None, activations: np.ndarray | None = None):
+    def _stage_logits(self, logits: bool):
+        if not logits:
+            return None, None
+        if not self._engine.last_stage:
+            raise ValueError("only the last stage computes logits")
+        buf = np.zeros(self._engine.vocab, dtype=np.float32)
+        return buf, buf.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+    def prefill_stage(self, tokens: Sequence[int] | None = None, activations: np.ndarray | None = None,
+                      logits: bool = False):
         """Pipeline-stage prefill (NativeSession::prefill_stage_tokens / _activations): token ids
         into the first stage, f32[n, n_embd] activations into later ones. Returns the greedy id of
-        the last row on the last stage, else the stage's output activations f32[n, n_embd]."""
+        the last row on the last stage (with the row's logits when asked), else the stage's output
+        activations f32[n, n_embd]."""
         n = len(tokens) if tokens is not None else (len(activations) if activations is not None else 0)
         src, src_p, out, out_p = self._stage_io(activations, n)
+        lg, lg_p = self._stage_logits(logits)
         tok = ctypes.c_int32(-1)
         check(library().jfh_session_stage_prefill(self._h, _i32(tokens) if tokens is not None else None, src_p, n,
-                                                  ctypes.byref(tok), out_p))
-        return tok.value if out is None else out
+                                                  ctypes.byref(tok), out_p, lg_p))
+        if out is not None:
+            return out
+        return (tok.value, lg) if logits else tok.value
 
-    def decode_stage(self, token: int | None = None, activation: np.ndarray | None = None):
+    def decode_stage(self, token: int | None = None, activation: np.ndarray | None = None, logits: bool = False):
         """One pipeline-stage decode row (NativeSession::decode_stage_token / _activation)."""
         src, src_p, out, out_p = self._stage_io(activation, 1)
+        lg, lg_p = self._stage_logits(logits)
         tok = ctypes.c_int32(-1)
         tin = ctypes.c_int32(token) if token is not None else None
         check(library().jfh_session_stage_decode(self._h, ctypes.byref(tin) if tin is not None else None, src_p,
-                                                 ctypes.byref(tok), out_p))
-        return tok.value if out is None else out
+                                                 ctypes.byref(tok), out_p, lg_p))
+        if out is not None:
+            return out
+        return (tok.value, lg) if logits else tok.value
 
     def rollback(self, token_count: int) -> None:
         check(library().jfh_session_rollback(self._h, token_count))
@@ -439,20 +462,26 @@ class NativeEngine:
         check(library().jfh_session_create(self._h, capacity, ctypes.byref(h)))
         return NativeSession(self, h.value)
 
-    def step_batch(self, sessions: Sequence[NativeSession], token_rows: Sequence[Sequence[int]]):
-        """One pass over several sessions; returns (ids per session, accepted per session)."""
+    def step_batch(self, sessions: Sequence[NativeSession], token_rows: Sequence[Sequence[int]],
+                   logits: bool = False):
+        """One pass over several sessions; returns (ids per session, accepted per session) and,
+        when asked, the logits rows of each session ([rows, vocab] per session)."""
         count = len(sessions)
         handles = (ctypes.c_void_p * count)(*[s.handle.value for s in sessions])
         flat = [t for row in token_rows for t in row]
         lengths = (ctypes.c_uint32 * count)(*[len(r) for r in token_rows])
         out = (ctypes.c_int32 * len(flat))()
         acc = (ctypes.c_uint32 * count)()
-        check(library().jfh_engine_step_batch(self._h, handles, count, _i32(flat), lengths, out, acc))
-        ids, o = [], 0
+        buf = np.zeros((len(flat), self.vocab), dtype=np.float32) if logits else None
+        ptr = buf.ctypes.data_as(ctypes.POINTER(ctypes.c_float)) if logits else None
+        check(library().jfh_engine_step_batch(self._h, handles, count, _i32(flat), lengths, out, acc, ptr))
+        ids, rows, o = [], [], 0
         for row in token_rows:
             ids.append([int(x) for x in out[o:o + len(row)]])
+            if logits:
+                rows.append(buf[o:o + len(row)])
             o += len(row)
-        return ids, [int(a) for a in acc]
+        return (ids, [int(a) for a in acc], rows) if logits else (ids, [int(a) for a in acc])
 
     def logits(self, tokens: Sequence[int]) -> np.ndarray:
         """Last-row logits of a fresh prefill (NativeEngine::logits, native_inference.cpp:396-411)."""

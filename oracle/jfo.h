@@ -135,6 +135,20 @@ int32_t jfo_session_position(const jfo_session * s);
 int32_t jfo_session_forward(jfo_session * s, const int32_t * tokens, int32_t n,
                             int32_t logits_rows, float * logits, int32_t * argmax_out);
 
+/*
+ * Stage forward over layers [layer_begin, layer_end) at positions pos..pos+n-1
+ * (advances the position; only the range's KV rows are written). The first
+ * stage (layer_begin 0) takes token ids and rows_in NULL; a later stage takes
+ * tokens NULL and the previous stage's f32 residual rows rows_in [n][n_embd].
+ * rows_out (may be NULL) receives (layer_end - layer_begin + 1) blocks of
+ * [n][n_embd]: the rows entering each layer of the range, then the rows after
+ * its last layer. Logits (as jfo_session_forward) only when layer_end is the
+ * model's last layer. Returns 0 or the errors of jfo_session_forward.
+ */
+int32_t jfo_session_forward_range(jfo_session * s, const int32_t * tokens, const float * rows_in, int32_t n,
+                                  int32_t layer_begin, int32_t layer_end, float * rows_out,
+                                  int32_t logits_rows, float * logits, int32_t * argmax_out);
+
 /* Rolls back n decoded positions: 0 < n <= position - prefill position. Returns 0 or -1. */
 int32_t jfo_session_rollback(jfo_session * s, int32_t n);
 

@@ -29,7 +29,7 @@ MODE_EXACT, MODE_Q8 = 0, 1
 
 __all__ = [
     "F32", "F16", "Q8_0", "Q2_K", "Q4_K", "Q6_K", "MODE_EXACT", "MODE_Q8", "lib", "block", "row_bytes",
-    "f16_to_f32", "f32_to_f16", "dequantize_row", "quantize_act", "vec_dot_q8", "vec_dot_f32", "matmul",
+    "f16_to_f32", "f32_to_f16", "dequantize_row", "quantize_act", "quantize_act_normed", "vec_dot_q8", "vec_dot_f32", "matmul",
     "rope_table", "argmax", "OracleModel", "OracleSession", "prompt_lookup", "speculative_generate",
     "ref_loader", "nrmse", "cosine",
 ]
@@ -59,6 +59,8 @@ _SIGS = {
     "jfo_type_block": (c_int32, [c_int32, POINTER(c_uint32), POINTER(c_uint32)]),
     "jfo_dequantize_row": (c_int32, [c_int32, c_void_p, POINTER(c_float), c_int64]),
     "jfo_quantize_act": (None, [POINTER(c_float), c_int64, POINTER(c_int8), POINTER(c_float), POINTER(c_int16)]),
+    "jfo_quantize_act_normed": (None, [POINTER(c_float), POINTER(c_float), c_int64, c_float, POINTER(c_int8),
+                                       POINTER(c_float), POINTER(c_int16)]),
     "jfo_vec_dot_q8": (c_double, [c_int32, c_void_p, POINTER(c_int8), POINTER(c_float), POINTER(c_int16), c_int64]),
     "jfo_vec_dot_f32": (c_double, [c_int32, c_void_p, POINTER(c_float), c_int64]),
     "jfo_matmul": (c_int32, [c_int32, c_void_p, c_int64, c_int64, POINTER(c_float), c_int64, POINTER(c_float), c_int32,
@@ -67,6 +69,8 @@ _SIGS = {
     "jfo_session_destroy": (None, [c_void_p]),
     "jfo_session_position": (c_int32, [c_void_p]),
     "jfo_session_forward": (c_int32, [c_void_p, POINTER(c_int32), c_int32, c_int32, POINTER(c_float), POINTER(c_int32)]),
+    "jfo_session_forward_range": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_float), c_int32, c_int32, c_int32,
+                                            POINTER(c_float), c_int32, POINTER(c_float), POINTER(c_int32)]),
     "jfo_session_rollback": (c_int32, [c_void_p, c_int32]),
     "jfo_session_fill_kv": (c_int32, [c_void_p, c_int32, c_uint64]),
     "jfo_session_read_kv": (c_int32, [c_void_p, c_int32, c_int32, POINTER(c_uint16), POINTER(c_uint16)]),
@@ -131,6 +135,19 @@ def quantize_act(x: np.ndarray):
     d = np.zeros(n // 256, dtype=np.float32)
     s = np.zeros(n // 16, dtype=np.int16)
     lib().jfo_quantize_act(_fp(x), n, q.ctypes.data_as(POINTER(c_int8)), _fp(d), s.ctypes.data_as(POINTER(c_int16)))
+    return q, d, s
+
+
+def quantize_act_normed(x: np.ndarray, gain: np.ndarray, eps: float):
+    """Codes, block scales and 16-value sums of RMSNorm(x) * gain as the engine stages them."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    g = np.ascontiguousarray(gain, dtype=np.float32)
+    n = x.size
+    q = np.zeros(n, dtype=np.int8)
+    d = np.zeros(n // 256, dtype=np.float32)
+    s = np.zeros(n // 16, dtype=np.int16)
+    lib().jfo_quantize_act_normed(_fp(x), _fp(g), n, eps, q.ctypes.data_as(POINTER(c_int8)), _fp(d),
+                                  s.ctypes.data_as(POINTER(c_int16)))
     return q, d, s
 
 
@@ -265,6 +282,33 @@ class OracleSession:
         if rc != 0:
             raise ValueError("oracle forward rejected its arguments")
         return [int(x) for x in ids[:logits_rows]], logits[:logits_rows]
+
+    def forward_range(self, layer_begin: int, layer_end: int, tokens: Sequence[int] | None = None,
+                      rows: np.ndarray | None = None, logits_rows: int = 0):
+        """Stage forward over layers [layer_begin, layer_end): token ids into the
+        first stage, f32 residual rows [n, n_embd] into a later one. Returns
+        (boundary rows [layer_end - layer_begin + 1, n, n_embd]: the rows entering
+        each layer, then the rows after the last; argmax ids; logits [rows, vocab]
+        when the range ends at the last layer and logits_rows > 0)."""
+        c = self.model.config
+        if (tokens is None) == (rows is None):
+            raise ValueError("give token ids or residual rows")
+        n = len(tokens) if tokens is not None else int(np.asarray(rows).shape[0])
+        out = np.zeros((layer_end - layer_begin + 1, n, c.n_embd), dtype=np.float32)
+        rows_in = None
+        if rows is not None:
+            rows_in = np.ascontiguousarray(rows, dtype=np.float32).reshape(n, c.n_embd)
+        logits = np.zeros((max(logits_rows, 1), c.n_vocab), dtype=np.float32) if logits_rows else None
+        ids = (c_int32 * max(logits_rows, 1))()
+        rc = lib().jfo_session_forward_range(self._h, (c_int32 * n)(*tokens) if tokens is not None else None,
+                                             _fp(rows_in) if rows_in is not None else None, n, layer_begin,
+                                             layer_end, _fp(out), logits_rows,
+                                             _fp(logits) if logits_rows else None, ids if logits_rows else None)
+        if rc == -2:
+            raise ValueError("native Qwen2 step is outside session capacity")
+        if rc != 0:
+            raise ValueError("oracle stage forward rejected its arguments")
+        return out, [int(x) for x in ids[:logits_rows]], (logits[:logits_rows] if logits_rows else None)
 
     def rollback(self, n: int) -> None:
         if lib().jfo_session_rollback(self._h, n) != 0:

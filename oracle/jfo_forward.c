@@ -327,10 +327,28 @@ static void attention(const jfo_session * s, int32_t layer, const float * q, int
 
 int32_t jfo_session_forward(jfo_session * s, const int32_t * tokens, int32_t n,
                             int32_t logits_rows, float * logits, int32_t * argmax_out) {
+    if (tokens == NULL) return -1;
+    return jfo_session_forward_range(s, tokens, NULL, n, 0, s->m->n_layer, NULL, logits_rows, logits, argmax_out);
+}
+
+/*
+ * One pipeline stage's forward over layers [layer_begin, layer_end):
+ * Qwen2Session::prefill_stage_* / decode_stage_* (qwen2_architecture.cpp:
+ * 909-947, 977-1027) build the same per-layer graph as the full model over
+ * the stage's LayerRange (model_architecture.hpp:15-21); the first stage
+ * embeds token ids, a later one starts from the previous stage's residual
+ * rows, and only the last one applies the output norm and head.
+ */
+int32_t jfo_session_forward_range(jfo_session * s, const int32_t * tokens, const float * rows_in, int32_t n,
+                                  int32_t layer_begin, int32_t layer_end, float * rows_out,
+                                  int32_t logits_rows, float * logits, int32_t * argmax_out) {
     const jfo_model * m = s->m;
     if (n <= 0 || (logits_rows != 0 && logits_rows != 1 && logits_rows != n)) return -1;
+    if (layer_begin < 0 || layer_begin >= layer_end || layer_end > m->n_layer) return -1;
+    if ((layer_begin == 0) != (tokens != NULL) || (tokens == NULL) == (rows_in == NULL)) return -1;
+    if (logits_rows > 0 && layer_end != m->n_layer) return -1;
     if ((int64_t) s->pos + n > s->capacity) return -2;
-    for (int32_t t = 0; t < n; ++t) {
+    for (int32_t t = 0; tokens && t < n; ++t) {
         if (tokens[t] < 0 || tokens[t] >= m->n_vocab) return -3;
     }
     const int64_t H = m->n_embd, F = m->n_ff, hd = s->head_dim;
@@ -349,8 +367,10 @@ int32_t jfo_session_forward(jfo_session * s, const int32_t * tokens, int32_t n,
         free(h); free(xn); free(q); free(k); free(v); free(att); free(o); free(g); free(u);
         return -1;
     }
-    /* embedding rows */
-    {
+    /* embedding rows (first stage) or the previous stage's residual rows */
+    if (rows_in) {
+        memcpy(h, rows_in, sizeof(float) * (size_t) (n * H));
+    } else {
         uint32_t be = 0, bb = 0;
         jfo_type_block(m->tok_embd.type, &be, &bb);
         const size_t row_bytes = (size_t) (H / be) * bb;
@@ -360,7 +380,8 @@ int32_t jfo_session_forward(jfo_session * s, const int32_t * tokens, int32_t n,
                                h + t * H, H);
         }
     }
-    for (int32_t l = 0; l < m->n_layer; ++l) {
+    for (int32_t l = layer_begin; l < layer_end; ++l) {
+        if (rows_out) memcpy(rows_out + (size_t) (l - layer_begin) * n * H, h, sizeof(float) * (size_t) (n * H));
         const jfo_layer * L = &m->layers[l];
         act_rows in;
         act_prepare(s, &in, h, &L->attn_norm, H, n, xn);
@@ -397,6 +418,9 @@ int32_t jfo_session_forward(jfo_session * s, const int32_t * tokens, int32_t n,
         linear(s, &L->w_down, &in, o);
         act_release(&in);
         for (int64_t i = 0; i < n * H; ++i) h[i] += o[i];
+    }
+    if (rows_out) {
+        memcpy(rows_out + (size_t) (layer_end - layer_begin) * n * H, h, sizeof(float) * (size_t) (n * H));
     }
     if (logits_rows > 0) {
         const int32_t first = n - logits_rows;

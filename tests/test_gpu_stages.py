@@ -16,6 +16,7 @@ import numpy as np
 import pytest
 
 import jetsonfabric_amd as jf
+import oracle as jo
 
 pytestmark = pytest.mark.gpu
 
@@ -71,6 +72,77 @@ def test_three_stage_pipeline_equals_full_model(staged, n_prompt):
         assert got == want, f"decode step {step}"
         tok = want
     assert [si.position() for si in s] == [ref.position()] * 3
+
+
+def test_stage_activations_match_the_oracle(staged):
+    """Each stage's output rows against the oracle's stage forward over the
+    same layer range and input rows (qwen2_architecture.cpp:909-947,
+    977-1027): prefill rows (16, multi-row kernels) and two decode rows;
+    NRMSE <= 5e-3 on the stage's update of the residual stream and on its
+    output, the last stage's logits within NRMSE 5e-3 / cosine 0.9995."""
+    full, stages = staged
+    model = jf.Model.synthesize(CFG, type_linear=jf.Q4_K, type_embd=jf.Q4_K, type_output=jf.Q6_K, seed=5)
+    om = jo.OracleModel.from_model(model)
+    prompt = _prompt(16, seed=13)
+    refs = [om.session(64, jo.MODE_Q8, 8) for _ in RANGES]
+    gpu = [e.create_session(64) for e in stages]
+
+    def check(i, rows_in, got, want, what):
+        upd, out = jo.nrmse(want - rows_in, got - rows_in), jo.nrmse(want, got)
+        assert upd <= 5e-3 and out <= 5e-3, f"stage {RANGES[i]} {what}: update {upd:.2e}, output {out:.2e}"
+
+    rows = None
+    for i, (a, b) in enumerate(RANGES):
+        last = b == CFG.n_layer
+        r_rows, _, r_lg = refs[i].forward_range(a, b, tokens=prompt if a == 0 else None,
+                                                rows=None if a == 0 else rows, logits_rows=1 if last else 0)
+        if last:
+            tok, lg = gpu[i].prefill_stage(activations=rows, logits=True)
+            assert jo.nrmse(r_lg[0], lg) <= 5e-3 and jo.cosine(r_lg[0], lg) >= 0.9995
+        else:
+            got = gpu[i].prefill_stage(tokens=prompt) if a == 0 else gpu[i].prefill_stage(activations=rows)
+            check(i, r_rows[0], got, r_rows[-1], "prefill")
+        rows = r_rows[-1]
+    for step in range(2):
+        token = prompt[step]
+        rows = None
+        for i, (a, b) in enumerate(RANGES):
+            last = b == CFG.n_layer
+            r_rows, _, r_lg = refs[i].forward_range(a, b, tokens=[token] if a == 0 else None,
+                                                    rows=None if a == 0 else rows, logits_rows=1 if last else 0)
+            if last:
+                _, lg = gpu[i].decode_stage(activation=rows, logits=True)
+                assert jo.nrmse(r_lg[0], lg) <= 5e-3 and jo.cosine(r_lg[0], lg) >= 0.9995
+            else:
+                got = gpu[i].decode_stage(token=token) if a == 0 else gpu[i].decode_stage(activation=rows)
+                check(i, r_rows[0], got, r_rows[-1], f"decode {step}")
+            rows = r_rows[-1]
+    for r in refs:
+        r.close()
+
+
+def test_in_memory_slices_are_the_package_stages(staged):
+    """Stages made from an in-memory model (Model.slice) hold the same layers
+    as the package opened with a layer range and give the same rows."""
+    _, stages = staged
+    model = jf.Model.synthesize(CFG, type_linear=jf.Q4_K, type_embd=jf.Q4_K, type_output=jf.Q6_K, seed=5)
+    prompt = _prompt(12, seed=17)
+    rows = None
+    for (a, b), pkg_stage in zip(RANGES, stages):
+        e = jf.NativeEngine(model.slice(a, b))
+        assert (e.layer_start, e.layer_end, e.weight_bytes) == (pkg_stage.layer_start, pkg_stage.layer_end,
+                                                               pkg_stage.weight_bytes)
+        s1, s2 = e.create_session(32), pkg_stage.create_session(32)
+        if a == 0:
+            got, want = s1.prefill_stage(tokens=prompt), s2.prefill_stage(tokens=prompt)
+        else:
+            got, want = s1.prefill_stage(activations=rows), s2.prefill_stage(activations=rows)
+        if b == CFG.n_layer:
+            assert got == want
+        else:
+            assert np.array_equal(got, want)
+            rows = got
+        e.close()
 
 
 def test_two_runs_of_a_stage_are_identical(staged):

@@ -213,6 +213,65 @@ def test_verify_equals_serial_and_rollback_replay():
         b.rollback(0)
 
 
+def test_stage_range_forward_equals_the_full_forward():
+    """The oracle's stage forward (layers [a, b) on token ids or residual rows,
+    qwen2_architecture.cpp:909-947, 977-1027) chained over a split of the
+    layers gives the full forward's logits bit for bit, prefill and decode,
+    and its boundary rows are the embedding rows, then each layer's output."""
+    cfg = jf.ModelConfig(n_layer=3, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, n_vocab=300, n_ctx=128)
+    model = jf.Model.synthesize(cfg, type_linear=jo.Q4_K, type_embd=jo.Q8_0, type_output=jo.Q6_K, seed=9,
+                                stddev=0.05)
+    om = jo.OracleModel.from_model(model)
+    prompt = [5, 17, 99, 3, 250, 7]
+    full = om.session(32, jo.MODE_Q8, 2)
+    f_ids, f_logits = full.forward(prompt, len(prompt))
+    whole = om.session(32, jo.MODE_Q8, 2)
+    rows, w_ids, w_logits = whole.forward_range(0, 3, tokens=prompt, logits_rows=len(prompt))
+    assert w_ids == f_ids and np.array_equal(w_logits, f_logits)
+    embd = model.tensor_bytes("token_embd.weight")
+    rb = jo.row_bytes(jo.Q8_0, cfg.n_embd)
+    for t, tok in enumerate(prompt):
+        assert np.array_equal(rows[0][t], jo.dequantize_row(jo.Q8_0, embd[tok * rb:(tok + 1) * rb], cfg.n_embd))
+    a, b = om.session(32, jo.MODE_Q8, 2), om.session(32, jo.MODE_Q8, 2)
+    a_rows, _, _ = a.forward_range(0, 1, tokens=prompt)
+    assert np.array_equal(a_rows, rows[:2])
+    b_rows, b_ids, b_logits = b.forward_range(1, 3, rows=a_rows[-1], logits_rows=len(prompt))
+    assert np.array_equal(b_rows, rows[1:]) and b_ids == f_ids and np.array_equal(b_logits, f_logits)
+    # one decode row through the split
+    d_ids, d_logits = full.forward([f_ids[-1]], 1)
+    a_rows, _, _ = a.forward_range(0, 1, tokens=[f_ids[-1]])
+    _, s_ids, s_logits = b.forward_range(1, 3, rows=a_rows[-1], logits_rows=1)
+    assert s_ids == d_ids and np.array_equal(s_logits, d_logits)
+    assert a.position() == b.position() == len(prompt) + 1
+    with pytest.raises(ValueError):
+        b.forward_range(1, 3, tokens=[1])  # a later stage takes rows, not ids
+    with pytest.raises(ValueError):
+        a.forward_range(0, 1, tokens=[1], logits_rows=1)  # logits only from the last stage
+
+
+def test_model_slices_hold_their_layer_range():
+    cfg = jf.ModelConfig(n_layer=3, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, n_vocab=300, n_ctx=128)
+    model = jf.Model.synthesize(cfg, type_linear=jo.Q4_K, type_embd=jo.Q4_K, type_output=jo.Q6_K, seed=3)
+    for start, end in ((0, 1), (1, 2), (2, 3), (0, 3), (1, 3)):
+        part = model.slice(start, end)
+        names = set(part.tensor_names())
+        assert ("token_embd.weight" in names) == (start == 0)
+        assert ("output.weight" in names) == ("output_norm.weight" in names) == (end == 3)
+        layers = {int(n.split(".")[1]) for n in names if n.startswith("blk.")}
+        assert layers == set(range(start, end))
+        for n in names:
+            assert part.tensor_bytes(n) == model.tensor_bytes(n)
+        assert part.stats()["layer_start"] == start and part.stats()["layer_end"] == end
+        assert part.source_sha256() == model.source_sha256()
+    inner = model.slice(1, 3).slice(2, 3)
+    assert set(inner.tensor_names()) == set(model.slice(2, 3).tensor_names())
+    for start, end in ((1, 1), (2, 1), (0, 4)):
+        with pytest.raises(jf.JfhError):
+            model.slice(start, end)
+    with pytest.raises(jf.JfhError):
+        model.slice(1, 3).slice(0, 2)  # outside the slice's own range
+
+
 def test_capacity_and_vocabulary_errors():
     model = _q4k_model()
     s = jo.OracleModel.from_model(model).session(8, jo.MODE_Q8, 1)

@@ -295,6 +295,38 @@ def test_activation_quantization_round_trip():
     assert np.array_equal(s, q.astype(np.int32).reshape(-1, 16).sum(axis=1))
 
 
+def test_normalized_activation_quantization():
+    """jfo_quantize_act_normed against the definition of the rule: the codes
+    are those of x * gain (one scale per 256 values, amax / 127), each block
+    scale is then multiplied by the row's 1 / sqrtf(mean(x^2) + eps), so the
+    dequantized codes reproduce RMSNorm(x) * gain (qwen2_architecture.cpp:
+    373-376) to half a code step."""
+    rng = np.random.default_rng(8)
+    n, eps = 1024, 1e-6
+    x = rng.normal(0, 3, n).astype(np.float32)
+    gain = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    gain[512:768] = 0.0  # one block of zero gains: zero codes, zero scale
+    q, d, s = jo.quantize_act_normed(x, gain, eps)
+    rs = np.float32(1.0) / np.sqrt(np.float32(np.sum(x.astype(np.float64) ** 2) / n) + np.float32(eps))
+    normed = (x.astype(np.float64) * float(rs)) * gain.astype(np.float64)
+    v = x * gain  # float32 products, the quantized values before normalization
+    for b in range(n // 256):
+        blk = slice(256 * b, 256 * b + 256)
+        d_unnormed = np.float32(np.abs(v[blk]).max()) / np.float32(127.0)
+        assert d[b] == np.float32(d_unnormed * rs), f"block {b} scale"
+        if d[b] == 0:
+            assert not q[blk].any()
+            continue
+        assert np.abs(q[blk]).max() == 127
+        err = np.abs(q[blk].astype(np.float64) * float(d[b]) - normed[blk])
+        assert err.max() <= 0.5 * float(d[b]) * (1 + 1e-5), f"block {b}: {err.max()} vs step {d[b]}"
+    assert d[2] == 0.0
+    assert np.array_equal(s, q.astype(np.int32).reshape(-1, 16).sum(axis=1))
+    # the unnormalized rule on x * gain gives the same codes
+    q2, d2, _ = jo.quantize_act(v)
+    assert np.array_equal(q, q2) and np.array_equal(d, (d2 * rs).astype(np.float32))
+
+
 @pytest.mark.parametrize("type_id", [jo.Q8_0, jo.Q2_K, jo.Q4_K, jo.Q6_K])
 def test_quantized_dot_equals_float64_brute_force(type_id):
     """vec_dot_q8 = sum over blocks of exact integer sums -> equals
