@@ -6,8 +6,6 @@
 #include <chrono>
 #include <condition_variable>
 #include <cstring>
-#include <deque>
-#include <future>
 #include <limits>
 #include <map>
 #include <stdexcept>
@@ -870,108 +868,93 @@ GenerationResult run_generation(const inference::Executor& executor, const Gener
 // ------------------------------------------------------------------ continuous batching
 namespace pipeline_parallel {
 
+// Decode steps are combined by the threads that submit them; there is no
+// worker thread. A submitted step waits in `arrived` (a pointer to a ticket
+// on its caller's stack). The first caller that finds no batch forming leads
+// the next one: it waits until max_batch_size steps have arrived or max_wait
+// has passed, takes up to max_batch_size of them in arrival order (its own
+// step need not be among them when more had queued), runs them as one
+// delegate execute_batch without holding the queue lock, writes each ticket's
+// result and wakes everyone. A caller whose ticket is still open afterwards
+// leads or joins the next batch. Steps arriving while a batch runs queue for
+// the next one, so the GPU goes from one batched step to the next.
 struct ContinuousBatchingExecutor::Impl {
-    struct Pending {
-        inference::StageInput input;
-        std::promise<inference::ExecutionResult> done;
+    struct Ticket {
+        const inference::StageInput* input = nullptr;
+        inference::ExecutionResult result;
+        bool answered = false;
     };
 
     std::unique_ptr<inference::Executor> delegate;
     ContinuousBatchingConfig config;
-    std::mutex delegate_mutex;
-    std::mutex queue_mutex;
-    std::condition_variable queued;
-    std::deque<std::shared_ptr<Pending>> queue;
-    bool stopping = false;
-    std::thread worker;
+    // delegate calls are serialized: batches, prefills, rollbacks and closes
+    std::mutex delegate_turn;
+    std::mutex state;
+    std::condition_variable changed;
+    std::vector<Ticket*> arrived;  // steps no leader has taken yet, oldest first
+    bool forming = false;          // a leader is gathering or running a batch
 
     Impl(std::unique_ptr<inference::Executor> d, ContinuousBatchingConfig c) : delegate(std::move(d)), config(c) {
-        if (!delegate) throw std::invalid_argument("continuous batching requires a layer executor");
-        if (config.max_batch_size < 2) throw std::invalid_argument("continuous batching size must be at least two");
+        if (!delegate) throw std::invalid_argument("a continuous-batching executor needs a delegate executor");
+        if (config.max_batch_size < 2) {
+            throw std::invalid_argument("a continuous-batching executor needs max_batch_size >= 2");
+        }
         if (config.max_wait < std::chrono::microseconds::zero()) {
-            throw std::invalid_argument("continuous batching wait must not be negative");
+            throw std::invalid_argument("a continuous-batching executor needs a non-negative max_wait");
         }
-        worker = std::thread([this] { serve(); });
     }
 
-    ~Impl() {
-        {
-            std::lock_guard lock(queue_mutex);
-            stopping = true;
+    // Runs the taken steps on the delegate; failures become per-step results
+    // with the reference's error codes.
+    std::vector<inference::ExecutionResult> run_batch(const std::vector<Ticket*>& taken) {
+        std::vector<inference::StageInput> inputs;
+        inputs.reserve(taken.size());
+        for (const Ticket* t : taken) inputs.push_back(*t->input);
+        std::vector<inference::ExecutionResult> out;
+        try {
+            std::lock_guard turn(delegate_turn);
+            out = delegate->execute_batch(inputs);
+        } catch (const std::exception& e) {
+            return std::vector<inference::ExecutionResult>(
+                taken.size(), inference::ExecutionResult::failure("continuous_batch_failed", e.what()));
         }
-        queued.notify_all();
-        worker.join();
+        if (out.size() != taken.size()) {
+            const std::string why = "the delegate answered " + std::to_string(out.size()) + " of " +
+                                    std::to_string(taken.size()) + " batched steps";
+            return std::vector<inference::ExecutionResult>(
+                taken.size(), inference::ExecutionResult::failure("continuous_batch_result_mismatch", why));
+        }
+        return out;
     }
 
-    inference::ExecutionResult submit(const inference::StageInput& input) {
-        if (input.phase == inference::Phase::Prefill) {
-            // prefill is not held back behind decoders
-            std::lock_guard lock(delegate_mutex);
-            return delegate->execute(input);
-        }
-        auto pending = std::make_shared<Pending>();
-        pending->input = input;
-        std::future<inference::ExecutionResult> result = pending->done.get_future();
-        {
-            std::lock_guard lock(queue_mutex);
-            if (stopping) {
-                return inference::ExecutionResult::failure("continuous_batch_stopped",
-                                                           "continuous batching executor stopped before execution");
+    inference::ExecutionResult step(const inference::StageInput& input) {
+        Ticket mine;
+        mine.input = &input;
+        std::unique_lock lock(state);
+        arrived.push_back(&mine);
+        changed.notify_all();  // a gathering leader may now hold a full batch
+        while (!mine.answered) {
+            if (forming) {
+                changed.wait(lock);
+                continue;
             }
-            queue.push_back(std::move(pending));
-        }
-        queued.notify_all();
-        return result.get();
-    }
-
-    // Waits for a first queued step, then up to max_wait for the batch to
-    // fill; takes at most max_batch_size steps in arrival order.
-    std::vector<std::shared_ptr<Pending>> take_batch() {
-        std::unique_lock lock(queue_mutex);
-        queued.wait(lock, [this] { return stopping || !queue.empty(); });
-        if (stopping) return {};
-        queued.wait_until(lock, std::chrono::steady_clock::now() + config.max_wait,
-                          [this] { return stopping || queue.size() >= config.max_batch_size; });
-        if (stopping) return {};
-        std::vector<std::shared_ptr<Pending>> batch;
-        while (!queue.empty() && batch.size() < config.max_batch_size) {
-            batch.push_back(std::move(queue.front()));
-            queue.pop_front();
-        }
-        return batch;
-    }
-
-    void serve() {
-        for (;;) {
-            std::vector<std::shared_ptr<Pending>> batch = take_batch();
-            if (batch.empty()) break;
-            std::vector<inference::StageInput> inputs;
-            inputs.reserve(batch.size());
-            for (const auto& p : batch) inputs.push_back(p->input);
-            std::vector<inference::ExecutionResult> results;
-            try {
-                std::lock_guard lock(delegate_mutex);
-                results = delegate->execute_batch(inputs);
-            } catch (const std::exception& e) {
-                results.assign(inputs.size(), inference::ExecutionResult::failure("continuous_batch_failed", e.what()));
+            forming = true;
+            changed.wait_until(lock, std::chrono::steady_clock::now() + config.max_wait,
+                               [this] { return arrived.size() >= config.max_batch_size; });
+            const std::size_t n = std::min(arrived.size(), config.max_batch_size);
+            std::vector<Ticket*> taken(arrived.begin(), arrived.begin() + static_cast<std::ptrdiff_t>(n));
+            arrived.erase(arrived.begin(), arrived.begin() + static_cast<std::ptrdiff_t>(n));
+            lock.unlock();
+            std::vector<inference::ExecutionResult> results = run_batch(taken);
+            lock.lock();
+            for (std::size_t i = 0; i < n; ++i) {
+                taken[i]->result = std::move(results[i]);
+                taken[i]->answered = true;
             }
-            if (results.size() != batch.size()) {
-                results.assign(batch.size(), inference::ExecutionResult::failure(
-                                                 "continuous_batch_result_mismatch",
-                                                 "layer executor returned the wrong number of batch results"));
-            }
-            for (std::size_t i = 0; i < batch.size(); ++i) batch[i]->done.set_value(std::move(results[i]));
+            forming = false;
+            changed.notify_all();
         }
-        // whatever is still queued when the executor stops fails
-        std::deque<std::shared_ptr<Pending>> left;
-        {
-            std::lock_guard lock(queue_mutex);
-            left.swap(queue);
-        }
-        for (const auto& p : left) {
-            p->done.set_value(inference::ExecutionResult::failure(
-                "continuous_batch_stopped", "continuous batching executor stopped before execution"));
-        }
+        return std::move(mine.result);
     }
 };
 
@@ -982,22 +965,27 @@ ContinuousBatchingExecutor::ContinuousBatchingExecutor(std::unique_ptr<inference
 ContinuousBatchingExecutor::~ContinuousBatchingExecutor() = default;
 
 inference::ExecutionResult ContinuousBatchingExecutor::execute(const inference::StageInput& input) const {
-    return impl_->submit(input);
+    if (input.phase == inference::Phase::Prefill) {
+        // a prompt is not held back to wait for decode steps
+        std::lock_guard turn(impl_->delegate_turn);
+        return impl_->delegate->execute(input);
+    }
+    return impl_->step(input);
 }
 
 std::vector<inference::ExecutionResult> ContinuousBatchingExecutor::execute_batch(
     const std::vector<inference::StageInput>& inputs) const {
-    std::lock_guard lock(impl_->delegate_mutex);
+    std::lock_guard turn(impl_->delegate_turn);
     return impl_->delegate->execute_batch(inputs);
 }
 
 void ContinuousBatchingExecutor::close_session(const std::string& session_id) const {
-    std::lock_guard lock(impl_->delegate_mutex);
+    std::lock_guard turn(impl_->delegate_turn);
     impl_->delegate->close_session(session_id);
 }
 
 void ContinuousBatchingExecutor::rollback_session(const std::string& session_id, int token_count) const {
-    std::lock_guard lock(impl_->delegate_mutex);
+    std::lock_guard turn(impl_->delegate_turn);
     impl_->delegate->rollback_session(session_id, token_count);
 }
 

@@ -283,11 +283,13 @@ struct ContinuousBatchingConfig {
     std::chrono::microseconds max_wait = std::chrono::microseconds(500);
 };
 
-// Coalesces concurrently arriving decode steps: a worker thread takes up to
-// max_batch_size queued decode inputs (waiting at most max_wait for the batch
-// to fill once one is queued) and runs them as one delegate execute_batch.
-// Prefill runs immediately on the caller's thread. Same contract and error
-// codes as the reference (continuous_batching_executor.cpp:14-200).
+// Coalesces concurrently arriving decode steps into delegate execute_batch
+// calls of up to max_batch_size steps, waiting at most max_wait for a batch
+// to fill; the submitting threads themselves form and run the batches (one
+// of them leads each batch). Prefill runs immediately on the caller's thread.
+// Contract and error codes of the reference's decorator
+// (continuous_batching_executor.hpp:16-39, continuous_batching_executor.cpp:
+// 44-127): continuous_batch_failed, continuous_batch_result_mismatch.
 class ContinuousBatchingExecutor final : public inference::Executor {
 public:
     ContinuousBatchingExecutor(std::unique_ptr<inference::Executor> delegate, ContinuousBatchingConfig config);

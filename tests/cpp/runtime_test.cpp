@@ -186,6 +186,7 @@ public:
     mutable std::vector<std::size_t> batches;
     mutable int prefills = 0, closes = 0, rollbacks = 0;
     bool fail_batches = false;
+    bool short_batches = false;  // answers one step fewer than it is handed
 
     inference::ExecutionResult execute(const inference::StageInput& in) const override {
         inference::StageOutput out;
@@ -207,6 +208,7 @@ public:
         if (fail_batches) throw std::runtime_error("injected batch failure");
         std::vector<inference::ExecutionResult> out;
         for (const auto& in : inputs) out.push_back(execute(in));
+        if (short_batches) out.pop_back();
         return out;
     }
     void close_session(const std::string&) const override { ++closes; }
@@ -271,6 +273,37 @@ void test_continuous_batching() {
         ContinuousBatchingExecutor ex(std::move(rec), ContinuousBatchingConfig{2, microseconds(0)});
         const inference::ExecutionResult a = ex.execute(step_input(inference::Phase::Decode, "a", 5));
         expect(!a.ok && a.error.code == "continuous_batch_failed", "batch failure is reported per step");
+    }
+    // a delegate that answers the wrong number of steps fails every step of the batch
+    {
+        auto rec = std::make_unique<BatchRecorder>();
+        rec->short_batches = true;
+        ContinuousBatchingExecutor ex(std::move(rec), ContinuousBatchingConfig{2, microseconds(0)});
+        const inference::ExecutionResult a = ex.execute(step_input(inference::Phase::Decode, "a", 5));
+        expect(!a.ok && a.error.code == "continuous_batch_result_mismatch", "a short batch answer is a mismatch");
+    }
+    // more concurrent steps than one batch holds: every step gets its own
+    // answer, in batches of at most max_batch_size
+    {
+        auto rec = std::make_unique<BatchRecorder>();
+        const BatchRecorder* r = rec.get();
+        ContinuousBatchingExecutor ex(std::move(rec), ContinuousBatchingConfig{3, microseconds(2000)});
+        std::vector<inference::ExecutionResult> res(8);
+        std::vector<std::thread> ts;
+        for (int i = 0; i < 8; ++i) {
+            ts.emplace_back([&, i] { res[i] = ex.execute(step_input(inference::Phase::Decode, std::to_string(i), 100 * i)); });
+        }
+        for (auto& t : ts) t.join();
+        std::size_t total = 0;
+        for (const std::size_t b : r->batches) {
+            expect(b >= 1 && b <= 3, "a batch holds at most max_batch_size steps");
+            total += b;
+        }
+        expect(total == 8, "every step ran exactly once");
+        for (int i = 0; i < 8; ++i) {
+            expect(res[i].ok && inference::decode_token_ids(res[i].output.payload) == std::vector<std::int32_t>{100 * i + 1},
+                   "every step gets its own answer");
+        }
     }
     // configuration errors
     bool threw = false;
