@@ -550,6 +550,14 @@ jfh_status jfh_engine_matmul(jfh_engine* engine, const char* tensor, const float
     });
 }
 
+jfh_status jfh_engine_matmul_noalloc(jfh_engine* engine, const char* tensor, const float* x, uint32_t n_tok,
+                                     float* y) {
+    return guarded([&] {
+        require(engine && tensor && x && y, "engine, tensor and device buffers are required");
+        engine->engine->matmul_noalloc(tensor, x, n_tok, y);
+    });
+}
+
 jfh_status jfh_session_read_kv(const jfh_session* session, uint32_t layer, uint32_t n, uint16_t* k, uint16_t* v) {
     return guarded([&] {
         require(session && k && v, "cache read arguments are required");

@@ -325,6 +325,11 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
         fail(Status::DeviceError, "the native engine's kernels are built for gfx950 only; device is " + device_name_);
     }
     hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "create stream");
+    try {
+        gpu::scratch_setup(options.device);
+    } catch (const std::exception& e) {
+        fail(Status::DeviceError, e.what());
+    }
 
     // a pipeline stage holds the model's layer range [layer_start, layer_end)
     // (engine.c:181-196): the first stage the embedding, the last the head
@@ -1021,6 +1026,53 @@ void Engine::dequantize(const std::string& name, uint32_t row0, uint32_t n_rows,
     (void) hipFree(dev);
 }
 
+namespace {
+
+// Bytes of the int8 copy of n_tok rows of K values (codes, one scale per 256
+// values, one sum per 16).
+size_t act8_bytes(size_t n_tok, size_t K) { return n_tok * K + n_tok * (K / 256) * sizeof(float) + n_tok * (K / 16) * 2; }
+
+gpu::Act8 act8_at(uint8_t* base, size_t n_tok, size_t K) {
+    gpu::Act8 xq;
+    xq.K = static_cast<int32_t>(K);
+    xq.q = reinterpret_cast<int8_t*>(base);
+    xq.d = reinterpret_cast<float*>(base + n_tok * K);
+    xq.s = reinterpret_cast<int16_t*>(base + n_tok * K + n_tok * (K / 256) * sizeof(float));
+    return xq;
+}
+
+size_t round256(size_t n) { return (n + 255) / 256 * 256; }
+
+}  // namespace
+
+// Quantized formats from 3 rows on are quantized once (xq, n_tok x K) and
+// run on the matrix-core paths a step takes (token quads up to 8 rows, the
+// wide kernel beyond, where the format has one); y_full receives the whole
+// device matrix's output rows, n_tok x rows.
+bool Engine::matmul_staged(const gpu::DMat& m, uint32_t n_tok) {
+    return n_tok >= 3 && quantized(m.type) && m.cols % 256 == 0;
+}
+
+void Engine::run_matmul(const gpu::DMat& m, const float* x, uint32_t n_tok, float* y_full, const gpu::Act8& xq) {
+    const bool wide = n_tok > 8 && gpu::wide_matmul_supported(m.type) && m.cols % 256 == 0;
+    gpu::GemvArgs a;
+    a.mat = m;
+    a.mat.bias = nullptr;
+    a.mode = gpu::kStore;
+    a.n_tok = static_cast<int32_t>(n_tok);
+    a.y = y_full;
+    a.y_stride = static_cast<int32_t>(m.rows);
+    if (matmul_staged(m, n_tok)) {
+        gpu::launch_quantize(x, static_cast<int32_t>(m.cols), static_cast<int32_t>(n_tok), xq, stream_);
+        a.xq = xq;
+        if (wide) gpu::launch_gemv_wide(a, stream_);
+        else gpu::launch_gemv(a, stream_);
+    } else {
+        a.x = {x, static_cast<int32_t>(m.cols), nullptr, nullptr, 0.0F};
+        gpu::launch_gemv(a, stream_);
+    }
+}
+
 void Engine::matmul(const std::string& name, const float* x_host, uint32_t n_tok, float* y_host) {
     std::lock_guard lock(mutex_);
     const TensorRef& ref = find_ref(name);
@@ -1038,11 +1090,6 @@ void Engine::matmul(const std::string& name, const float* x_host, uint32_t n_tok
         fail(Status::OutOfMemory, "allocate matmul output");
     }
     std::vector<float> full(static_cast<size_t>(n_tok) * m.rows);
-    // quantized formats from 3 rows on: quantized once, then the matrix-core paths a step takes (token
-    // quads up to 8 rows, the wide kernel beyond, where the format has one)
-    const bool wide = n_tok > 8 && gpu::wide_matmul_supported(m.type) && m.cols % 256 == 0;
-    const bool quads = n_tok >= 3 && quantized(m.type) && m.cols % 256 == 0;
-    gpu::Act8 xq;
     uint8_t* xq_mem = nullptr;
     auto release = [&] {
         (void) hipFree(x);
@@ -1051,28 +1098,12 @@ void Engine::matmul(const std::string& name, const float* x_host, uint32_t n_tok
     };
     try {
         hip_check(hipMemcpyAsync(x, x_host, x_bytes, hipMemcpyHostToDevice, stream_), "upload activations");
-        gpu::GemvArgs a;
-        a.mat = m;
-        a.mat.bias = nullptr;
-        a.mode = gpu::kStore;
-        a.n_tok = static_cast<int32_t>(n_tok);
-        a.y = y;
-        a.y_stride = static_cast<int32_t>(m.rows);
-        if (wide || quads) {
-            const size_t K = m.cols, nq = n_tok * K, nd = n_tok * (K / 256), ns = n_tok * (K / 16);
-            hip_check(hipMalloc(&xq_mem, nq + nd * sizeof(float) + ns * sizeof(int16_t)), "allocate int8 rows");
-            xq.K = static_cast<int32_t>(K);
-            xq.q = reinterpret_cast<int8_t*>(xq_mem);
-            xq.d = reinterpret_cast<float*>(xq_mem + nq);
-            xq.s = reinterpret_cast<int16_t*>(xq_mem + nq + nd * sizeof(float));
-            gpu::launch_quantize(x, static_cast<int32_t>(K), static_cast<int32_t>(n_tok), xq, stream_);
-            a.xq = xq;
-            if (wide) gpu::launch_gemv_wide(a, stream_);
-            else gpu::launch_gemv(a, stream_);
-        } else {
-            a.x = {x, static_cast<int32_t>(m.cols), nullptr, nullptr, 0.0F};
-            gpu::launch_gemv(a, stream_);
+        gpu::Act8 xq;
+        if (matmul_staged(m, n_tok)) {
+            hip_check(hipMalloc(&xq_mem, act8_bytes(n_tok, m.cols)), "allocate int8 rows");
+            xq = act8_at(xq_mem, n_tok, m.cols);
         }
+        run_matmul(m, x, n_tok, y, xq);
         hip_check(hipMemcpyAsync(full.data(), y, y_bytes, hipMemcpyDeviceToHost, stream_), "download matmul");
         hip_check(hipStreamSynchronize(stream_), "matmul");
     } catch (...) {
@@ -1085,6 +1116,35 @@ void Engine::matmul(const std::string& name, const float* x_host, uint32_t n_tok
             y_host[static_cast<size_t>(t) * ref.rows + r] = full[static_cast<size_t>(t) * m.rows + device_row(ref, r)];
         }
     }
+}
+
+void Engine::matmul_noalloc(const std::string& name, const float* x_dev, uint32_t n_tok, float* y_dev) {
+    std::lock_guard lock(mutex_);
+    const TensorRef& ref = find_ref(name);
+    const gpu::DMat& m = ref.dev->mat;
+    if (n_tok == 0 || n_tok > static_cast<uint32_t>(gpu::kMaxRows)) {
+        fail(Status::InvalidArgument, "matmul shape is outside the engine workspace");
+    }
+    // staging in the GPU's static scratch: [int8 rows][the device matrix's output rows]
+    const size_t xq_bytes = matmul_staged(m, n_tok) ? round256(act8_bytes(n_tok, m.cols)) : 0;
+    const size_t y_bytes = round256(static_cast<size_t>(n_tok) * m.rows * sizeof(float));
+    if (xq_bytes + y_bytes > gpu::kScratchBytes) {
+        fail(Status::InvalidArgument, "allocation-free matmul of " + name + " over " + std::to_string(n_tok) +
+                                          " rows needs " + std::to_string(xq_bytes + y_bytes) +
+                                          " bytes of staging; the static scratch holds " +
+                                          std::to_string(gpu::kScratchBytes));
+    }
+    uint8_t* base = static_cast<uint8_t*>(gpu::scratch_address(options_.device));
+    if (base == nullptr) fail(Status::DeviceError, "the device's static scratch was not set up");
+    std::lock_guard use(gpu::scratch_lock(options_.device));
+    gpu::Act8 xq;
+    if (xq_bytes) xq = act8_at(base, n_tok, m.cols);
+    float* y_full = reinterpret_cast<float*>(base + xq_bytes);
+    run_matmul(m, x_dev, n_tok, y_full, xq);
+    gpu::launch_gather_rows(y_full, static_cast<int32_t>(m.rows), y_dev, static_cast<int32_t>(ref.rows),
+                            static_cast<int32_t>(n_tok), static_cast<int32_t>(ref.offset),
+                            static_cast<int32_t>(ref.kind), static_cast<int32_t>(ref.head_dim), stream_);
+    hip_check(hipStreamSynchronize(stream_), "allocation-free matmul");
 }
 
 }  // namespace jfh

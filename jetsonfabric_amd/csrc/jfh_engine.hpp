@@ -130,6 +130,9 @@ public:
     // device matrix with host activations through the same kernels.
     void dequantize(const std::string& name, uint32_t row0, uint32_t n_rows, float* out_host);
     void matmul(const std::string& name, const float* x_host, uint32_t n_tok, float* y_host);
+    // The same matmul on device rows (x_dev [n_tok][cols], y_dev [n_tok][rows])
+    // with its staging in the GPU's static scratch: no device allocation.
+    void matmul_noalloc(const std::string& name, const float* x_dev, uint32_t n_tok, float* y_dev);
 
     // Runs the step `iterations` times without graphs, timing every kernel
     // launch; sessions are restored to their starting positions.
@@ -168,6 +171,8 @@ private:
     };
 
     static uint32_t device_row(const TensorRef& r, uint32_t row);
+    static bool matmul_staged(const gpu::DMat& m, uint32_t n_tok);
+    void run_matmul(const gpu::DMat& m, const float* x, uint32_t n_tok, float* y_full, const gpu::Act8& xq);
     const DeviceTensor& upload_rows(const std::string& key, uint32_t type, uint64_t cols,
                                     const std::vector<RowSource>& rows, const float* bias);
     const DeviceTensor& upload_single(const TensorView& t);

@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <type_traits>
@@ -2080,9 +2081,34 @@ __global__ void k_finish(unsigned long long* best, const StepDev* step, int32_t 
     }
 }
 
+// ------------------------------------------------------------------ static scratch
+// Staging of the allocation-free matmul (int8 activation rows, the device
+// matrix's full output rows). Kernels reach it only through the per-device
+// address that scratch_setup looks up.
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+__global__ __launch_bounds__(256) void k_gather_rows(const float* __restrict__ full, int32_t full_stride,
+                                                     float* __restrict__ y, int32_t rows, int32_t offset, int32_t kind,
+                                                     int32_t head_dim) {
+    const int t = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= rows) return;
+    int dr = offset + r;
+    if (kind == 1) {
+        const int head = r / head_dim, i = r - head * head_dim, half = head_dim / 2;
+        dr = offset + head * head_dim + (i < half ? 2 * i : 2 * (i - half) + 1);
+    } else if (kind == 2 || kind == 3) {
+        dr = (r / kGluGroup) * 2 * kGluGroup + (kind == 3 ? kGluGroup : 0) + r % kGluGroup;
+    }
+    y[static_cast<size_t>(t) * rows + r] = full[static_cast<size_t>(t) * full_stride + dr];
+}
+
 void check(hipError_t e, const char* what) {
     if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
+
+std::mutex g_scratch_table;
+void* g_scratch_address[kScratchDevices] = {};
+std::mutex g_scratch_use[kScratchDevices];
 
 // Events of the launch being timed (set_launch_events). The first launch
 // records `start` when its dispatch begins; every launch records `stop` when
@@ -2212,6 +2238,37 @@ void gemv_f(const GemvArgs& a, hipStream_t stream) {
 }
 
 }  // namespace
+
+void scratch_setup(int device) {
+    if (device < 0 || device >= kScratchDevices) throw std::invalid_argument("device ordinal outside the scratch table");
+    std::lock_guard lock(g_scratch_table);
+    if (g_scratch_address[device] != nullptr) return;
+    void* p = nullptr;
+    check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "scratch symbol address");
+    if (p == nullptr) throw std::runtime_error("scratch symbol address is null");
+    g_scratch_address[device] = p;
+}
+
+void* scratch_address(int device) {
+    if (device < 0 || device >= kScratchDevices) return nullptr;
+    std::lock_guard lock(g_scratch_table);
+    return g_scratch_address[device];
+}
+
+std::mutex& scratch_lock(int device) {
+    if (device < 0 || device >= kScratchDevices) throw std::invalid_argument("device ordinal outside the scratch table");
+    return g_scratch_use[device];
+}
+
+void launch_gather_rows(const float* full, int32_t full_stride, float* y, int32_t rows, int32_t n_tok, int32_t offset,
+                        int32_t kind, int32_t head_dim, hipStream_t stream) {
+    if (rows <= 0 || n_tok <= 0 || (kind == 1 && (head_dim <= 0 || head_dim % 2 != 0))) {
+        throw std::invalid_argument("row gather shape is invalid");
+    }
+    launch(k_gather_rows, dim3((rows + 255) / 256, n_tok), dim3(256), 0, stream, full, full_stride, y, rows, offset,
+           kind, head_dim);
+    check(hipGetLastError(), "row gather launch");
+}
 
 void set_launch_events(hipEvent_t start, hipEvent_t stop) {
     t_start = start;

@@ -6,6 +6,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <mutex>
 
 namespace jfh::gpu {
 
@@ -187,6 +188,26 @@ size_t attention_partial_floats(int32_t rows, int32_t n_head, int32_t head_dim, 
 void launch_finish(unsigned long long* best, const StepDev* step, int32_t n_out, StepOut* out,
                    hipStream_t stream);
 void launch_dequant_rows(const DMat& m, int32_t row0, int32_t n_rows, float* out, hipStream_t stream);
+
+// Static device scratch of the allocation-free matmul: one array of
+// kScratchBytes per GPU, a file-scope __device__ variable that lives until
+// the process ends. scratch_setup looks up this GPU's address of it
+// (hipGetSymbolAddress) once per device and must run with that device
+// current; scratch_address returns it (nullptr before setup). Kernels take
+// the address as an argument: the variable's host-side name is no device
+// address. Every user of one GPU's scratch holds scratch_lock(device) for
+// the duration of its kernels.
+constexpr size_t kScratchBytes = size_t{16} << 20;
+constexpr int kScratchDevices = 64;
+void scratch_setup(int device);
+void* scratch_address(int device);
+std::mutex& scratch_lock(int device);
+// y[t][r] = full[t][device row of r] for r < rows, t < n_tok: the rows of one
+// model tensor out of its (possibly fused) device matrix's output rows
+// (kind 0 contiguous from offset, 1 RoPE pair order per head, 2 / 3 gate /
+// up rows of the interleaved GLU matrix).
+void launch_gather_rows(const float* full, int32_t full_stride, float* y, int32_t rows, int32_t n_tok, int32_t offset,
+                        int32_t kind, int32_t head_dim, hipStream_t stream);
 // Host evaluation of the device tile decoder: value k (< 256) of row (< 16) of one tile.
 float dequant_tile_value(uint32_t type, const uint8_t* tile, uint32_t row, uint32_t k);
 
