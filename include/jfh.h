@@ -205,6 +205,15 @@ jfh_status jfh_model_source_sha256(const jfh_model * model, char hex[65]);
 jfh_status jfh_engine_create(const jfh_model * model, const jfh_engine_options * options, jfh_engine ** out);
 void jfh_engine_destroy(jfh_engine * engine);
 jfh_status jfh_engine_get_info(const jfh_engine * engine, jfh_engine_info * out);
+/* End-of-generation ids of the stage's tokenizer (Tokenizer::is_end_token,
+ * runtime/tokenization/tokenizer.hpp:16). The on-GPU acceptance of every later
+ * verify step (jfh_session_verify, jfh_engine_step_batch out_accepted) stops
+ * at a draft position whose greedy id is one of them, as the runner's
+ * acceptance loop does (runtime/pipeline_parallel/generation_runner.cpp:
+ * 512-517); jfh_generate and jfh_generate_concurrent end a request at one
+ * (finish reason "stop"). At most 16 ids, each inside the vocabulary; n = 0
+ * clears the set (the default). */
+jfh_status jfh_engine_set_end_tokens(jfh_engine * engine, const int32_t * ids, uint32_t n);
 
 /* NativeEngine::create_session (native_inference.hpp:143). */
 jfh_status jfh_session_create(jfh_engine * engine, uint32_t capacity, jfh_session ** out);
@@ -337,6 +346,8 @@ typedef struct jfh_generation_stats {
     uint32_t speculative_accepted_tokens;
     double time_to_first_token_ms;
     double decode_ms;
+    uint32_t stopped;  /* 1: ended at an end-of-generation id (finish reason "stop"), 0: at max_tokens */
+    uint32_t reserved;
 } jfh_generation_stats;
 
 /* GenerationRunner::run speculative loop (generation_runner.cpp:398-566) over

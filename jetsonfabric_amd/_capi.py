@@ -68,6 +68,7 @@ class GenerationStats(ctypes.Structure):
         ("completion_tokens", c_uint32), ("target_decode_passes", c_uint32),
         ("speculative_draft_tokens", c_uint32), ("speculative_accepted_tokens", c_uint32),
         ("time_to_first_token_ms", c_double), ("decode_ms", c_double),
+        ("stopped", c_uint32), ("reserved", c_uint32),
     ]
 
 
@@ -115,6 +116,7 @@ SIGNATURES = {
     "jfh_engine_create": (Status, [c_void_p, POINTER(EngineOptions), POINTER(c_void_p)]),
     "jfh_engine_destroy": (None, [c_void_p]),
     "jfh_engine_get_info": (Status, [c_void_p, POINTER(EngineInfo)]),
+    "jfh_engine_set_end_tokens": (Status, [c_void_p, POINTER(c_int32), c_uint32]),
     "jfh_session_create": (Status, [c_void_p, c_uint32, POINTER(c_void_p)]),
     "jfh_session_destroy": (None, [c_void_p]),
     "jfh_session_capacity": (c_uint32, [c_void_p]),

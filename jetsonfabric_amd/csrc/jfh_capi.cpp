@@ -385,6 +385,13 @@ jfh_status jfh_engine_get_info(const jfh_engine* engine, jfh_engine_info* out) {
     });
 }
 
+jfh_status jfh_engine_set_end_tokens(jfh_engine* engine, const int32_t* ids, uint32_t n) {
+    return guarded([&] {
+        require(engine, "engine is required");
+        engine->engine->set_end_tokens(ids, n);
+    });
+}
+
 jfh_status jfh_session_create(jfh_engine* engine, uint32_t capacity, jfh_session** out) {
     return guarded([&] {
         require(engine && out, "engine and output are required");
@@ -652,7 +659,7 @@ jfh_status jfh_generate(jfh_engine* engine, const int32_t* prompt, uint32_t n_pr
         const jfh::ModelParams& p = engine->engine->params();
         rt::adapters::HipStageConfig cfg;
         cfg.engine = engine->engine;
-        cfg.tokenizer = std::make_shared<rt::tokenization::IdTokenizer>();
+        cfg.tokenizer = std::make_shared<rt::tokenization::IdTokenizer>(engine->engine->end_tokens());
         cfg.ctx_size = static_cast<int>(std::min<uint64_t>(p.n_ctx, static_cast<uint64_t>(n_prompt) + max_tokens));
         cfg.position = {0, 1};
         cfg.layers = {0, static_cast<int>(p.n_layer)};
@@ -675,6 +682,8 @@ jfh_status jfh_generate(jfh_engine* engine, const int32_t* prompt, uint32_t n_pr
             stats->speculative_accepted_tokens = static_cast<uint32_t>(r.speculative_accepted_tokens);
             stats->time_to_first_token_ms = r.time_to_first_token_ms;
             stats->decode_ms = r.decode_ms;
+            stats->stopped = r.finish_reason == "stop" ? 1U : 0U;
+            stats->reserved = 0;
         }
     });
 }
@@ -702,7 +711,7 @@ jfh_status jfh_generate_concurrent(jfh_engine* engine, uint32_t n_requests, cons
         }
         rt::adapters::HipStageConfig cfg;
         cfg.engine = engine->engine;
-        cfg.tokenizer = std::make_shared<rt::tokenization::IdTokenizer>();
+        cfg.tokenizer = std::make_shared<rt::tokenization::IdTokenizer>(engine->engine->end_tokens());
         cfg.ctx_size = static_cast<int>(std::min<uint64_t>(p.n_ctx, longest + max_tokens));
         cfg.position = {0, 1};
         cfg.layers = {0, static_cast<int>(p.n_layer)};
@@ -775,6 +784,8 @@ jfh_status jfh_generate_concurrent(jfh_engine* engine, uint32_t n_requests, cons
                 stats[i].speculative_accepted_tokens = static_cast<uint32_t>(r.speculative_accepted_tokens);
                 stats[i].time_to_first_token_ms = r.time_to_first_token_ms;
                 stats[i].decode_ms = r.decode_ms;
+                stats[i].stopped = r.finish_reason == "stop" ? 1U : 0U;
+                stats[i].reserved = 0;
             }
             last = std::max(last, finished[i]);
         }

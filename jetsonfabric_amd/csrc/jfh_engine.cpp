@@ -791,6 +791,27 @@ void Engine::require_full_model() const {
     }
 }
 
+void Engine::set_end_tokens(const int32_t* ids, uint32_t n) {
+    if (n > static_cast<uint32_t>(gpu::kMaxEndTokens)) {
+        fail(Status::InvalidArgument, "at most " + std::to_string(gpu::kMaxEndTokens) + " end-of-generation ids");
+    }
+    if (n > 0 && ids == nullptr) fail(Status::InvalidArgument, "end-of-generation ids are required");
+    std::vector<int32_t> next;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (ids[i] < 0 || static_cast<uint32_t>(ids[i]) >= params_.n_vocab) {
+            fail(Status::InvalidArgument, "end-of-generation id is outside model vocabulary");
+        }
+        next.push_back(ids[i]);
+    }
+    std::lock_guard lock(mutex_);
+    end_tokens_ = std::move(next);
+}
+
+std::vector<int32_t> Engine::end_tokens() const {
+    std::lock_guard lock(mutex_);
+    return end_tokens_;
+}
+
 void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int32_t* accepted, float* logits,
                      float* act_out) {
     std::lock_guard lock(mutex_);
@@ -860,6 +881,8 @@ void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int
     }
     sd.n_seq = static_cast<int32_t>(steps.size());
     sd.n_out = outs;
+    sd.n_end = static_cast<int32_t>(end_tokens_.size());
+    std::copy(end_tokens_.begin(), end_tokens_.end(), sd.end_token);
     const bool store = logits != nullptr && outs > 0;
     hip_check(hipMemcpyAsync(step_dev_, step_host_, sizeof(gpu::StepDev), hipMemcpyHostToDevice, stream_), "upload step");
     // input rows of a later stage: the previous stage's residual stream

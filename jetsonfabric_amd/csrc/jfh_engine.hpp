@@ -101,6 +101,14 @@ public:
 
     std::unique_ptr<Session> create_session(uint32_t capacity);
 
+    // End-of-generation ids (at most gpu::kMaxEndTokens, each inside the
+    // vocabulary): a verify row's draft token is accepted only while the
+    // greedy id it is compared with is none of them, as the reference runner
+    // stops acceptance at an end token. Replaces the previous set; empty by
+    // default.
+    void set_end_tokens(const int32_t* ids, uint32_t n);
+    std::vector<int32_t> end_tokens() const;
+
     // Runs token rows for several sessions in one pass. Positions advance by
     // each sequence's row count. out_tokens receives one greedy id per logits
     // row (sequence order); accepted (optional) one accepted-draft count per
@@ -233,7 +241,8 @@ private:
 
     // captured step graphs keyed by (rows, seqs, outs, store_logits)
     std::map<uint64_t, hipGraphExec_t> graphs_;
-    std::mutex mutex_;
+    std::vector<int32_t> end_tokens_;
+    mutable std::mutex mutex_;
 };
 
 }  // namespace jfh

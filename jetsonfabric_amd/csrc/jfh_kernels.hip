@@ -2068,13 +2068,19 @@ __global__ void k_finish(unsigned long long* best, const StepDev* step, int32_t 
         best[i] = 0ull;
     }
     __syncthreads();
+    // A draft token is accepted while the greedy id after the previous row
+    // equals it and is no end-of-generation id
+    // (runtime/pipeline_parallel/generation_runner.cpp:512-517).
+    const int n_end = step->n_end;
     for (int s = threadIdx.x; s < step->n_seq; s += blockDim.x) {
         int accepted = 0;
         bool open = true;
         for (int i = 0; i < n_out; ++i) {
             const int r = step->out_row[i];
             if (step->seq[r] != s || !open) continue;
-            if (step->draft[i] >= 0 && tok[i] == step->draft[i]) ++accepted;
+            bool end = false;
+            for (int e = 0; e < n_end; ++e) end |= tok[i] == step->end_token[e];
+            if (step->draft[i] >= 0 && tok[i] == step->draft[i] && !end) ++accepted;
             else open = false;
         }
         out->accepted[s] = accepted;

@@ -22,6 +22,7 @@ constexpr int kMaxSeq = 16;         // sequences of one batched step
 constexpr int kActBlock = 256;      // activation quantization block (values)
 constexpr int kTileRows = 16;       // rows of one weight tile
 constexpr int kMaxAttnQGroups = 8;  // query groups of 8 rows per kv head in one step
+constexpr int kMaxEndTokens = 16;   // end-of-generation ids the on-GPU acceptance stops at
 
 // Bytes of one weight tile (16 rows x 256 values) of a quantized type, 0 for
 // float types. The tile holds the 16 rows' GGML blocks rearranged so that
@@ -78,19 +79,20 @@ struct StepDev {
     int32_t n_rows;
     int32_t n_seq;
     int32_t n_out;                 // rows that produce logits
-    int32_t pad;
+    int32_t n_end;                 // end-of-generation ids in end_token
     int32_t token[kMaxRows];
     int32_t pos[kMaxRows];
     int32_t seq[kMaxRows];
     int32_t out_row[kMaxRows];     // step row of each logits row
     int32_t draft[kMaxRows];       // token the logits row is compared with (-1: none)
+    int32_t end_token[kMaxEndTokens];
     SeqDev seqs[kMaxSeq];
 };
 
 // Result block copied back to the host after a step.
 struct StepOut {
     int32_t token[kMaxRows];       // argmax of each logits row (first max)
-    int32_t accepted[kMaxSeq];     // accepted draft prefix per sequence
+    int32_t accepted[kMaxSeq];     // accepted draft prefix per sequence (stops at an end id)
 };
 
 enum GemvMode : int32_t {

@@ -259,6 +259,7 @@ class GenerationResult:
     target_decode_passes: int = 0
     speculative_draft_tokens: int = 0
     speculative_accepted_tokens: int = 0
+    finish_reason: str = "length"  # "stop": ended at an end-of-generation id
     extra: dict = field(default_factory=dict)
 
 
@@ -457,6 +458,13 @@ class NativeEngine:
     def model_info(self) -> ModelConfig:
         return self._config
 
+    def set_end_tokens(self, ids: Sequence[int]) -> None:
+        """End-of-generation ids (Tokenizer::is_end_token, tokenization/tokenizer.hpp:16): the
+        on-GPU acceptance stops at them (generation_runner.cpp:512-517) and generation ends at
+        one. At most 16; an empty list clears the set."""
+        ids = list(ids)
+        check(library().jfh_engine_set_end_tokens(self._h, _i32(ids), len(ids)))
+
     def create_session(self, capacity: int) -> NativeSession:
         h = ctypes.c_void_p()
         check(library().jfh_session_create(self._h, capacity, ctypes.byref(h)))
@@ -533,6 +541,7 @@ class NativeEngine:
             target_decode_passes=int(stats.target_decode_passes),
             speculative_draft_tokens=int(stats.speculative_draft_tokens),
             speculative_accepted_tokens=int(stats.speculative_accepted_tokens),
+            finish_reason="stop" if stats.stopped else "length",
         )
 
 
@@ -560,6 +569,7 @@ class NativeEngine:
                 target_decode_passes=int(st.target_decode_passes),
                 speculative_draft_tokens=int(st.speculative_draft_tokens),
                 speculative_accepted_tokens=int(st.speculative_accepted_tokens),
+                finish_reason="stop" if st.stopped else "length",
             ))
         return results, wall.value
 

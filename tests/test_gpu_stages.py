@@ -186,6 +186,16 @@ def test_stage_input_errors(staged):
     assert isinstance(t, int) and t == full.create_session(16).prefill_greedy([1, 2, 3])
 
 
+def _library_inputs():
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    csrc = os.path.join(root, "jetsonfabric_amd", "csrc")
+    yield os.path.join(root, "jetsonfabric_amd", "libjfh.so")
+    yield os.path.join(root, "include", "jfh.h")
+    for name in os.listdir(csrc):
+        if name.endswith(".hpp"):
+            yield os.path.join(csrc, name)
+
+
 def test_stage_executors_chain_like_the_whole_model(capfd):
     """tests/cpp/stage_test.cpp, in this process: two HipStageExecutors over
     layer ranges, chained by activation payloads (f32, and f16 on the wire),
@@ -193,6 +203,10 @@ def test_stage_executors_chain_like_the_whole_model(capfd):
     errors."""
     path = os.path.join(os.path.dirname(__file__), "cpp", "libstage_test.so")
     assert os.path.exists(path), "tests/cpp/libstage_test.so is not built (make -C tests/cpp)"
+    # it constructs the engine's C++ classes itself: built against older headers
+    # it would allocate them with a stale layout
+    newest = max(os.path.getmtime(f) for f in _library_inputs())
+    assert os.path.getmtime(path) >= newest, "tests/cpp/libstage_test.so is older than the library: make -C tests/cpp"
     jf.library()  # the engine library first, so the test links against the loaded copy
     rc = ctypes.CDLL(path).jfh_stage_test_main()
     out = capfd.readouterr().out
