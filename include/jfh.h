@@ -35,6 +35,17 @@ typedef struct jfh_status {
     char message[256];
 } jfh_status;
 
+/* Tensor type ids of the JFM v2 format: the values of jf_tensor_type
+ * (engine.h:13-42) for the types this engine runs. */
+typedef enum jfh_tensor_type {
+    JFH_TENSOR_F32 = 1,
+    JFH_TENSOR_F16 = 2,
+    JFH_TENSOR_Q8_0 = 7,
+    JFH_TENSOR_Q2_K = 9,
+    JFH_TENSOR_Q4_K = 11,
+    JFH_TENSOR_Q6_K = 13
+} jfh_tensor_type;
+
 typedef struct jfh_model jfh_model;     /* host-resident weights + hparams */
 typedef struct jfh_engine jfh_engine;   /* device-resident weights, one HIP stream */
 typedef struct jfh_session jfh_session; /* one sequence's F16 KV cache + position */
@@ -205,6 +216,9 @@ jfh_status jfh_model_source_sha256(const jfh_model * model, char hex[65]);
 jfh_status jfh_engine_create(const jfh_model * model, const jfh_engine_options * options, jfh_engine ** out);
 void jfh_engine_destroy(jfh_engine * engine);
 jfh_status jfh_engine_get_info(const jfh_engine * engine, jfh_engine_info * out);
+/* Hyper-parameters of the engine's model (NativeEngine::model_info,
+ * native_inference.hpp:138; the whole model's n_layer also for a stage). */
+jfh_status jfh_engine_get_params(const jfh_engine * engine, jfh_model_params * out);
 /* End-of-generation ids of the stage's tokenizer (Tokenizer::is_end_token,
  * runtime/tokenization/tokenizer.hpp:16). The on-GPU acceptance of every later
  * verify step (jfh_session_verify, jfh_engine_step_batch out_accepted) stops

@@ -117,6 +117,7 @@ SIGNATURES = {
     "jfh_engine_destroy": (None, [c_void_p]),
     "jfh_engine_get_info": (Status, [c_void_p, POINTER(EngineInfo)]),
     "jfh_engine_set_end_tokens": (Status, [c_void_p, POINTER(c_int32), c_uint32]),
+    "jfh_engine_get_params": (Status, [c_void_p, POINTER(ModelParams)]),
     "jfh_session_create": (Status, [c_void_p, c_uint32, POINTER(c_void_p)]),
     "jfh_session_destroy": (None, [c_void_p]),
     "jfh_session_capacity": (c_uint32, [c_void_p]),

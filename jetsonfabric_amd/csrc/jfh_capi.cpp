@@ -320,9 +320,9 @@ jfh_status jfh_model_get_stats(const jfh_model* model, jfh_model_stats* out) {
         out->layer_end = m.layer_end();
         out->layer_count = m.params().n_layer;
         out->selected_weight_bytes = m.weight_bytes();
-        out->total_weight_bytes = m.weight_bytes();
+        out->total_weight_bytes = m.total_weight_bytes();
         out->selected_tensor_count = m.tensors().size();
-        out->total_tensor_count = m.tensors().size();
+        out->total_tensor_count = m.total_tensor_count();
     });
 }
 
@@ -382,6 +382,15 @@ jfh_status jfh_engine_get_info(const jfh_engine* engine, jfh_engine_info* out) {
         std::snprintf(out->device_name, sizeof(out->device_name), "%s", engine->engine->device_name().c_str());
         out->layer_start = engine->engine->layer_start();
         out->layer_end = engine->engine->layer_end();
+    });
+}
+
+jfh_status jfh_engine_get_params(const jfh_engine* engine, jfh_model_params* out) {
+    return guarded([&] {
+        require(engine && out, "engine and output are required");
+        const jfh::ModelParams& p = engine->engine->params();
+        *out = jfh_model_params{p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_head_kv,
+                                p.n_ctx,   p.n_vocab, p.head_dim, p.rope_base, p.rms_eps};
     });
 }
 

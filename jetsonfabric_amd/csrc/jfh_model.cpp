@@ -297,6 +297,8 @@ std::unique_ptr<HostModel> HostModel::open_package(const std::string& dir, const
     m->tensors_ = m->package_->tensors();
     m->layer_start_ = m->package_->stats().layer_start;
     m->layer_end_ = m->package_->stats().layer_end;
+    m->total_weight_bytes_ = m->package_->stats().total_weight_bytes;
+    m->total_tensor_count_ = m->package_->stats().total_tensor_count;
     m->source_sha256_ = hex(m->package_->source_sha256().data(), 32);
     if (m->package_->stats().layer_count != m->params_.n_layer) {
         fail(Status::FormatError, "package layer count does not match qwen2.block_count");
@@ -378,6 +380,8 @@ std::unique_ptr<HostModel> HostModel::slice(uint32_t start, uint32_t end) const 
     }
     m->source_sha256_ = source_sha256_;
     m->keep_digest_ = true;
+    m->total_weight_bytes_ = total_weight_bytes();
+    m->total_tensor_count_ = total_tensor_count();
     m->finalize();
     return m;
 }

@@ -71,6 +71,11 @@ public:
     uint32_t layer_start() const { return layer_start_; }
     uint32_t layer_end() const { return layer_end_; }
     uint64_t weight_bytes() const;
+    // Weight bytes and tensors of the whole model this one selects a layer
+    // range of (its package, or the model it was sliced from); equal to its
+    // own otherwise (jf_model_stats::total_*, engine.h:74-83).
+    uint64_t total_weight_bytes() const { return total_weight_bytes_ != 0 ? total_weight_bytes_ : weight_bytes(); }
+    uint64_t total_tensor_count() const { return total_tensor_count_ != 0 ? total_tensor_count_ : tensors_.size(); }
     std::string source_sha256() const { return source_sha256_; }
 
     // GGUF header bytes for the model's metadata (written or as loaded).
@@ -94,6 +99,8 @@ private:
     uint32_t layer_end_ = 0;
     std::string source_sha256_;
     bool keep_digest_ = false;  // a slice keeps its source model's digest
+    uint64_t total_weight_bytes_ = 0;  // 0: this model is whole
+    uint64_t total_tensor_count_ = 0;
 };
 
 // Parses and validates qwen2.* GGUF keys (qwen2_metadata.cpp:90-125).

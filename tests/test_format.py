@@ -177,3 +177,23 @@ def test_model_validation_rejects_missing_and_misshapen_tensors():
     bad = [(n, ty, (8, 4) if n == "blk.0.attn_q.weight" else s, b) for n, ty, s, b in tensors]
     with pytest.raises(jf.JfhError):
         jf.Model.build(cfg, bad)
+
+
+def test_stage_model_stats_count_the_whole_model(tmp_path):
+    """A model opened or sliced for a layer range reports its own weights as
+    selected and the whole model's as total (jf_model_stats, engine.h:74-83)."""
+    cfg = jf.ModelConfig(n_layer=4, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, n_vocab=512, n_ctx=64)
+    whole = jf.Model.synthesize(cfg, seed=5)
+    whole.write_package(str(tmp_path / "m.jfm"))
+    total = whole.stats()["total_weight_bytes"]
+    assert total == whole.stats()["selected_weight_bytes"]
+    parts = []
+    for a, b in ((0, 2), (2, 4)):
+        for stage in (jf.Model.open(str(tmp_path / "m.jfm"), a, b), whole.slice(a, b)):
+            s = stage.stats()
+            assert s["total_weight_bytes"] == total and s["selected_weight_bytes"] < total
+            assert s["total_tensor_count"] == whole.stats()["total_tensor_count"]
+            parts.append(s["selected_weight_bytes"])
+            stage.close()
+    assert parts[0] + parts[2] == total and parts[1] + parts[3] == total
+    whole.close()
