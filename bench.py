@@ -179,6 +179,9 @@ def main() -> int:
                     help="other workloads' legs: default = the 1.5B prompt-lookup legs; all = also 14B and 32B")
     ap.add_argument("--copy-probe-mib", type=int, default=256,
                     help="size of the device-to-device copy that calibrates PMC byte counters (0: none)")
+    ap.add_argument("--trace-decode", action="store_true",
+                    help="only a prefill and --warmup + --steps batch-1 decode steps, for kernel traces of the "
+                         "captured decode graph; prints no JSON line")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -199,6 +202,8 @@ def main() -> int:
     engine = jf.NativeEngine(model)
     log(f"engine on {engine.device_name}: {engine.weight_bytes / 1e9:.3f} GB of weights uploaded in "
         f"{time.perf_counter() - t0:.1f}s")
+    if args.trace_decode:
+        return trace_decode(engine, cfg, context, args)
     copy_gbs = copy_probe(args.copy_probe_mib) if args.copy_probe_mib > 0 else None
 
     # ---- headline: continuous-batching decode at the workload's concurrency
@@ -385,6 +390,23 @@ def main() -> int:
         "configs": legs,
     }
     print(json.dumps(line), flush=True)
+    return 0
+
+
+def trace_decode(engine, cfg, context, args) -> int:
+    """A prefill of `context` uniform tokens, then warmup + steps greedy decode
+    steps (one captured graph per step shape): the workload of a kernel trace."""
+    s = engine.create_session(context + args.warmup + args.steps + 8)
+    tok = s.prefill_greedy(uniform_prompt(context, cfg.n_vocab, args.seed))
+    for _ in range(args.warmup):
+        tok = s.decode_greedy(tok)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        tok = s.decode_greedy(tok)
+    log(f"decode: {(time.perf_counter() - t0) * 1e6 / args.steps:.1f} us/step over {args.steps} steps at "
+        f"positions {s.position() - args.steps}..{s.position()}")
+    s.close()
+    engine.close()
     return 0
 
 
