@@ -1373,11 +1373,16 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
 // row) is the decode matmul's (q4k_term), accumulated per wave and lane
 // group in the same tile order and summed over waves, then lane groups, in
 // the same order: every row equals that row computed alone, bit for bit.
+// The token tile's per-block scales and code sums, which the 16 lanes of a
+// lane group all need, are read from global memory once per wave and
+// shared through LDS (one lane per 16 bytes instead of 16 broadcast reads).
 __global__ __launch_bounds__(kMmThreads) void k_mm_wide_q4k(GemvArgs a) {
     constexpr int W = kMmWaves;
     constexpr uint32_t TB = tile_bytes(11);
     __shared__ float red[W][4][16][16];  // [wave][lane group][token][row] of one token tile
     __shared__ float vals[kWideRows][16];
+    __shared__ u32x4 stage_s[W][16][2];
+    __shared__ float stage_d[W][16];
     const int K = static_cast<int>(a.mat.cols), nb = K / 256, n_tok = a.n_tok;
     const int rg = blockIdx.x;
     const int lane = threadIdx.x & (kWave - 1);
@@ -1397,9 +1402,6 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide_q4k(GemvArgs a) {
         }
         // A operand rows: token 16 tt + i; D fragment tokens: 16 tt + 4 G + j
         const int8_t* xa_row = xq.q + static_cast<size_t>(min(16 * tt + i, n_tok - 1)) * K + 64 * G;
-        int tok[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) tok[j] = min(16 * tt + 4 * G + j, n_tok - 1);
         for (int b = wave; b < nb; b += W) {
             const uint8_t* t = base + static_cast<size_t>(b) * TB;
             const uint4 hdr = *reinterpret_cast<const uint4*>(t + 16 * i);
@@ -1411,15 +1413,29 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide_q4k(GemvArgs a) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) av[p][c] = *reinterpret_cast<const long*>(xa_row + b * 256 + 32 * p + 8 * c);
             }
+            // the token tile's block scales and code sums, read once per wave
+            // (lanes 0..31: token lane / 2, half lane % 2 of its 16 sums;
+            // lanes 32..47: the scale of token lane - 32) and shared through LDS
+            {
+                const int tl = lane < 32 ? lane >> 1 : lane - 32;
+                const int tk = min(16 * tt + (tl & 15), n_tok - 1);
+                if (lane < 32) {
+                    stage_s[wave][tl][lane & 1] =
+                        reinterpret_cast<const u32x4*>(xq.s + static_cast<size_t>(tk) * (K / 16) + b * 16)[lane & 1];
+                } else if (lane < 48) {
+                    stage_d[wave][tl] = xq.d[static_cast<size_t>(tk) * nb + b];
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
             float xd[4];
             u32x4 sums[4][2];  // the 16 code sums (int16) of each D token's block
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                xd[j] = xq.d[static_cast<size_t>(tok[j]) * nb + b];
-                const u32x4* sp = reinterpret_cast<const u32x4*>(xq.s + static_cast<size_t>(tok[j]) * (K / 16) + b * 16);
-                sums[j][0] = sp[0];
-                sums[j][1] = sp[1];
+                xd[j] = stage_d[wave][4 * G + j];
+                sums[j][0] = stage_s[wave][4 * G + j][0];
+                sums[j][1] = stage_s[wave][4 * G + j][1];
             }
+            __builtin_amdgcn_wave_barrier();
             const float d = h2f(hdr.x), dmin = h2f(hdr.x >> 16);
             // row i's 24-bit fields sc 2g | sc 2g+1 | m 2g | m 2g+1 of the four lane groups
             const uint32_t F[4] = {hdr.y & 0xFFFFFFu, (hdr.y >> 24) | ((hdr.z & 0xFFFFu) << 8),
