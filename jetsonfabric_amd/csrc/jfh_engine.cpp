@@ -17,6 +17,12 @@ namespace {
 #endif
 constexpr int32_t kNormedPrologueRows = JFH_NORMED_PROLOGUE_ROWS;
 
+// Token rows from which a step runs its Q4_K matrices in the wide matmul.
+#ifndef JFH_WIDE_FROM_ROWS
+#define JFH_WIDE_FROM_ROWS 9
+#endif
+constexpr int32_t kWideFromRows = JFH_WIDE_FROM_ROWS;
+
 void hip_check(hipError_t e, const char* what) {
     if (e != hipSuccess) throw Error(Status::DeviceError, std::string(what) + ": " + hipGetErrorString(e));
 }
@@ -506,10 +512,11 @@ uint64_t mat_bytes(const gpu::DMat& m) { return static_cast<uint64_t>(m.rows) * 
 std::string gemv_label(const gpu::GemvArgs& a) {
     const uint32_t t = a.mat.type;
     const bool fl = t == kF32 || t == kF16;
-    const int nt = a.n_tok > 8 ? 8 : a.n_tok;
-    // int8 or normalized rows of the quantized formats run in token quads (4 or 8 slots)
-    const bool quads = quantized(t) && (a.xq.q != nullptr || a.x.gain != nullptr) && nt >= gpu::kQuadMinRows;
-    const int slot = quads ? (nt <= 4 ? 4 : 8) : nt <= 2 ? nt : nt <= 4 ? 4 : nt <= 6 ? 6 : 8;
+    // int8 or normalized rows of the quantized formats run in token quads (4, 8 or 16 slots)
+    const bool quads = quantized(t) && (a.xq.q != nullptr || a.x.gain != nullptr) && a.n_tok >= gpu::kQuadMinRows;
+    const int nt = a.n_tok > (quads ? gpu::kQuadGroupRows : 8) ? (quads ? gpu::kQuadGroupRows : 8) : a.n_tok;
+    const int slot = quads ? (nt <= 4 ? 4 : nt <= 8 ? 8 : gpu::kQuadGroupRows)
+                           : nt <= 2 ? nt : nt <= 4 ? 4 : nt <= 6 ? 6 : 8;
     if (fl) return "k_gemv_f<" + std::to_string(nt) + ">";
     // template arguments of the launched kernel: type, token slots, input kind
     // (0 int8 rows, 1 RMS-normalized float rows, 2 float rows)
@@ -575,10 +582,10 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
             gpu::launch_embed(embd_->mat, step_dev_, h_, n_rows, H, best_, gpu::kMaxRows, s);
         });
     }
-    // Steps with more rows than one 8-row group run Q4_K matrices on matrix
-    // cores with int8 rows quantized once per step (same codes as the decode
-    // prologue, same results per row).
-    const bool wide = n_rows > 8 && n_rows <= gpu::kWideRows;
+    // Steps of more than kWideFromRows rows run Q4_K matrices in the wide
+    // matmul with int8 rows quantized once per step (same codes as the decode
+    // prologue, same results per row); shorter ones in token-quad groups.
+    const bool wide = n_rows >= kWideFromRows && n_rows <= gpu::kWideRows;
     auto wide_ok = [&](const gpu::DMat& m) { return wide && gpu::wide_matmul_supported(m.type); };
     auto matmul = [&](gpu::GemvArgs& a, const char* role) {
         if (wide_ok(a.mat) && a.xq.q != nullptr) {
@@ -1077,7 +1084,8 @@ bool Engine::matmul_staged(const gpu::DMat& m, uint32_t n_tok) {
 }
 
 void Engine::run_matmul(const gpu::DMat& m, const float* x, uint32_t n_tok, float* y_full, const gpu::Act8& xq) {
-    const bool wide = n_tok > 8 && gpu::wide_matmul_supported(m.type) && m.cols % 256 == 0;
+    const bool wide = static_cast<int32_t>(n_tok) >= kWideFromRows && gpu::wide_matmul_supported(m.type) &&
+                      m.cols % 256 == 0;
     gpu::GemvArgs a;
     a.mat = m;
     a.mat.bias = nullptr;

@@ -2237,7 +2237,8 @@ void mm_nt(const GemvArgs& a, hipStream_t stream) {
         // int8 or normalized rows from kQuadMinRows tokens on: token quads on matrix cores
         if ((a.xq.q != nullptr || a.x.gain != nullptr) && a.n_tok >= kQuadMinRows) {
             if (a.n_tok <= 4) mm<TYPE, 4>(a, stream);
-            else mm<TYPE, 8>(a, stream);
+            else if (a.n_tok <= 8) mm<TYPE, 8>(a, stream);
+            else mm<TYPE, kQuadGroupRows>(a, stream);
             return;
         }
     }
@@ -2314,10 +2315,13 @@ void launch_gemv(const GemvArgs& a_in, hipStream_t stream) {
     if ((a_in.mode == kSwiGLU && a_in.mat.rows % (2 * kGluGroup) != 0) || (a_in.mode == kQKV && a_in.mat.rows % 2 != 0)) {
         throw std::invalid_argument("matmul rows do not fit the fused row layout");
     }
-    // token groups of at most 8 rows
-    for (int t0 = 0; t0 < a_in.n_tok; t0 += 8) {
+    // token groups of at most 8 rows; int8 or normalized rows of the quantized
+    // formats run on matrix cores in groups of up to kQuadGroupRows
+    const bool quads = quantized && (a_in.xq.q != nullptr || a_in.x.gain != nullptr) && a_in.n_tok >= kQuadMinRows;
+    const int group = quads ? kQuadGroupRows : 8;
+    for (int t0 = 0; t0 < a_in.n_tok; t0 += group) {
         GemvArgs a = a_in;
-        a.n_tok = a_in.n_tok - t0 < 8 ? a_in.n_tok - t0 : 8;
+        a.n_tok = a_in.n_tok - t0 < group ? a_in.n_tok - t0 : group;
         if (a.xq.q) {
             a.xq.q += static_cast<size_t>(t0) * a.xq.K;
             a.xq.d += static_cast<size_t>(t0) * (a.xq.K / 256);

@@ -18,6 +18,12 @@ constexpr int kMaxRows = 64;
 #define JFH_QUAD_MIN_ROWS 2
 #endif
 constexpr int kQuadMinRows = JFH_QUAD_MIN_ROWS;        // token rows of one step (sum over sequences)
+// Token rows per matrix-core launch of the token-quad matmul (longer steps
+// run in groups of this many rows).
+#ifndef JFH_QUAD_GROUP_ROWS
+#define JFH_QUAD_GROUP_ROWS 16
+#endif
+constexpr int kQuadGroupRows = JFH_QUAD_GROUP_ROWS;
 constexpr int kMaxSeq = 16;         // sequences of one batched step
 constexpr int kActBlock = 256;      // activation quantization block (values)
 constexpr int kTileRows = 16;       // rows of one weight tile
