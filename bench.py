@@ -244,14 +244,6 @@ def main() -> int:
     step_bytes = sum(p["bytes"] for p in prof1)
     log("decode profile (ms/step): " + ", ".join(f"{p['kernel']} {p['ms']:.3f} ({p['launches']:.0f}x)"
                                                 for p in prof1[:8]))
-    # the headline's step shape: two one-row sequences, logits of both rows -> the
-    # kernels of a two-row step with two logits rows
-    prof2 = session.profile_step(cont[:conc], iterations=args.profile_iters, all_logits=True) if conc > 1 else prof1
-    groups2 = kernel_groups(prof2)
-    dominant = max(groups2.values(), key=lambda g: g["ms"])
-    us_l, bytes_l, achieved = launch_rate(dominant)
-    log("two-row step profile (ms/step): " + ", ".join(f"{p['kernel']} {p['ms']:.3f}" for p in prof2[:8]))
-    log(f"dominant {dominant['kernel']}: {bytes_l / 1e6:.2f} MB/launch, {us_l:.2f} us/launch -> {achieved:.0f} GB/s")
     vprof = session.profile_step(cont[:1 + k], iterations=args.profile_iters)
     verify_bytes = sum(p["bytes"] for p in vprof)
     log("verify profile (ms/step): " + ", ".join(f"{p['kernel']} {p['ms']:.3f}" for p in vprof[:8]))
@@ -259,13 +251,19 @@ def main() -> int:
     pprof = session.profile_step(chunk, iterations=1, all_logits=False)
     log("prefill chunk (64 rows) profile (ms): " + ", ".join(f"{p['kernel']} {p['ms']:.3f}" for p in pprof[:8]))
     session.close()
-    # the two-row profile reads one sequence's cache; the batched step reads one per sequence
-    kv1 = sum(p["bytes"] for p in prof1 if p["kernel"].startswith("k_attention"))
-    cstep_bytes = sum(p["bytes"] for p in prof2) + (conc - 1) * kv1
 
     # the headline's batched step driven directly (no runner threads)
     bsess = [engine.create_session(context + 64) for _ in range(conc)]
     btok = [s_.prefill_greedy(cp) for s_, cp in zip(bsess, cprompts)]
+    # its kernels: one row per sequence, each row's logits and greedy id
+    prof2 = engine.profile_batch(bsess, [[t] for t in btok], iterations=args.profile_iters)
+    groups2 = kernel_groups(prof2)
+    dominant = max(groups2.values(), key=lambda g: g["ms"])
+    us_l, bytes_l, achieved = launch_rate(dominant)
+    cstep_bytes = sum(p["bytes"] for p in prof2)  # weights once, every sequence's cache
+    log(f"batched step of {conc} sequences profile (ms/step): " + ", ".join(f"{p['kernel']} {p['ms']:.3f}"
+                                                                          for p in prof2[:8]))
+    log(f"dominant {dominant['kernel']}: {bytes_l / 1e6:.2f} MB/launch, {us_l:.2f} us/launch -> {achieved:.0f} GB/s")
     for it in range(40):
         if it == 8:
             t1 = time.perf_counter()
@@ -370,7 +368,7 @@ def main() -> int:
         "roofline": {
             "bound": "hbm",
             "kernel": dominant["kernel"],
-            "step": f"{conc} one-token rows with logits (the headline's batched step)",
+            "step": f"the headline's batched step: {conc} sequences x 1 row, each row's logits",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -384,7 +382,7 @@ def main() -> int:
         "parity": parity,
         "kernels": [{"kernel": p["kernel"], "launches": p["launches"], "us_per_step": round(p["ms"] * 1e3, 1),
                      "bytes_per_step": round(p["bytes"])} for p in prof1],
-        "kernels_two_row_step": [{"kernel": p["kernel"], "launches": p["launches"],
+        "kernels_batched_step": [{"kernel": p["kernel"], "launches": p["launches"],
                                   "us_per_step": round(p["ms"] * 1e3, 1), "bytes_per_step": round(p["bytes"])}
                                  for p in prof2],
         "configs": legs,
@@ -489,17 +487,16 @@ def step_leg(wl, args, batch, rows, context):
         for s_ in sess:
             s_.rollback(rows)
     us = (time.perf_counter() - t1) * 1e6 / 10
-    prof = sess[0].profile_step(token_rows[0], iterations=2, all_logits=rows > 1)
-    per_seq = sum(p["bytes"] for p in prof)
-    kv = sum(p["bytes"] for p in prof if p["kernel"].startswith("k_attention"))
-    step_bytes = per_seq + (batch - 1) * kv  # weights once, every sequence's cache
+    prof = engine.profile_batch(sess, token_rows, iterations=2, all_logits=rows > 1)
+    step_bytes = sum(p["bytes"] for p in prof)  # weights once, every sequence's cache
     for s_ in sess:
         s_.close()
     engine.close()
     model.close()
     log(f"{wl.name}: {batch} x {rows}-row steps at context {context}: {us:.1f} us/step")
     return {"us_per_step": round(us, 1), "batch": batch, "rows_per_sequence": rows, "context": context,
-            "hbm_fraction": round(step_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "step_bytes": round(step_bytes)}
+            "hbm_fraction": round(step_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "step_bytes": round(step_bytes),
+            "kernels_us_per_step": {p["kernel"]: round(p["ms"] * 1e3, 1) for p in prof[:8]}}
 
 
 def large_legs(args) -> dict:

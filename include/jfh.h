@@ -346,6 +346,14 @@ typedef struct jfh_kernel_stat {
 
 jfh_status jfh_session_profile_step(jfh_session * session, const int32_t * tokens, uint32_t n, uint32_t all_logits,
                                     uint32_t iterations, jfh_kernel_stat * out, uint32_t capacity, uint32_t * count);
+/* The same profile for one batched step over several sessions (the rows of
+ * jfh_engine_step_batch: lengths[i] rows for sessions[i], tokens concatenated),
+ * every row producing logits when all_logits is set, else the last row of each
+ * session; the sessions are rolled back after every iteration. */
+jfh_status jfh_engine_profile_batch(jfh_engine * engine, jfh_session * const * sessions, uint32_t count,
+                                    const int32_t * tokens, const uint32_t * lengths, uint32_t all_logits,
+                                    uint32_t iterations, jfh_kernel_stat * out, uint32_t capacity,
+                                    uint32_t * out_count);
 
 /* ---------------------------------------------------------------- speculation */
 

@@ -88,6 +88,8 @@ class KernelStat(ctypes.Structure):
 SIGNATURES = {
     "jfh_session_profile_step": (Status, [c_void_p, POINTER(c_int32), c_uint32, c_uint32, c_uint32, POINTER(KernelStat),
                                           c_uint32, POINTER(c_uint32)]),
+    "jfh_engine_profile_batch": (Status, [c_void_p, POINTER(c_void_p), c_uint32, POINTER(c_int32), POINTER(c_uint32),
+                                         c_uint32, c_uint32, POINTER(KernelStat), c_uint32, POINTER(c_uint32)]),
     "jfh_package_open": (Status, [c_char_p, c_uint32, c_uint32, c_uint32, POINTER(c_void_p)]),
     "jfh_package_close": (None, [c_void_p]),
     "jfh_package_get_stats": (Status, [c_void_p, POINTER(PackageStats)]),

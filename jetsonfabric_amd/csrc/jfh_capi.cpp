@@ -646,6 +646,36 @@ jfh_status jfh_session_profile_step(jfh_session* session, const int32_t* tokens,
     });
 }
 
+jfh_status jfh_engine_profile_batch(jfh_engine* engine, jfh_session* const* sessions, uint32_t count,
+                                    const int32_t* tokens, const uint32_t* lengths, uint32_t all_logits,
+                                    uint32_t iterations, jfh_kernel_stat* out, uint32_t capacity, uint32_t* out_count) {
+    return guarded([&] {
+        require(engine && sessions && tokens && lengths && out && out_count && count > 0 && iterations > 0,
+                "profile arguments are required");
+        std::vector<jfh::SeqStep> steps(count);
+        uint32_t offset = 0;
+        for (uint32_t i = 0; i < count; ++i) {
+            require(sessions[i] && sessions[i]->owner == engine, "every session must belong to the engine");
+            require(lengths[i] > 0, "every session needs rows");
+            require(sessions[i]->session->position() > 0, "profiling requires prefilled sessions");
+            steps[i].session = sessions[i]->session.get();
+            steps[i].tokens = tokens + offset;
+            steps[i].n = lengths[i];
+            steps[i].logits = all_logits ? 2 : 1;
+            offset += lengths[i];
+        }
+        const std::vector<jfh::KernelStat> stats = engine->engine->profile(steps, iterations);
+        const uint32_t k = std::min<uint32_t>(capacity, static_cast<uint32_t>(stats.size()));
+        for (uint32_t i = 0; i < k; ++i) {
+            std::snprintf(out[i].label, sizeof(out[i].label), "%s", stats[i].label.c_str());
+            out[i].launches = stats[i].launches;
+            out[i].total_ms = stats[i].total_ms;
+            out[i].bytes = stats[i].bytes;
+        }
+        *out_count = k;
+    });
+}
+
 jfh_status jfh_prompt_lookup_propose(const uint32_t* history, size_t n, uint32_t max_ngram, uint32_t min_ngram,
                                      uint32_t max_tokens, uint32_t* out, uint32_t* out_count) {
     return guarded([&] {

@@ -491,6 +491,22 @@ class NativeEngine:
             o += len(row)
         return (ids, [int(a) for a in acc], rows) if logits else (ids, [int(a) for a in acc])
 
+    def profile_batch(self, sessions: Sequence[NativeSession], token_rows: Sequence[Sequence[int]],
+                      iterations: int = 3, all_logits: bool = False) -> list[dict]:
+        """Per-kernel device time and algorithmic bytes of one batched step (as step_batch) over
+        several sessions, rolled back after every iteration."""
+        count = len(sessions)
+        handles = (ctypes.c_void_p * count)(*[s.handle.value for s in sessions])
+        flat = [t for row in token_rows for t in row]
+        lengths = (ctypes.c_uint32 * count)(*[len(r) for r in token_rows])
+        cap = 64
+        out = (_capi.KernelStat * cap)()
+        n = ctypes.c_uint32()
+        check(library().jfh_engine_profile_batch(self._h, handles, count, _i32(flat), lengths, int(all_logits),
+                                                 iterations, out, cap, ctypes.byref(n)))
+        return [{"kernel": out[i].label.decode(), "launches": out[i].launches, "ms": out[i].total_ms,
+                 "bytes": out[i].bytes} for i in range(n.value)]
+
     def logits(self, tokens: Sequence[int]) -> np.ndarray:
         """Last-row logits of a fresh prefill (NativeEngine::logits, native_inference.cpp:396-411)."""
         s = self.create_session(len(tokens))
