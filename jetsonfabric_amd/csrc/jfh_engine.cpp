@@ -17,12 +17,6 @@ namespace {
 #endif
 constexpr int32_t kNormedPrologueRows = JFH_NORMED_PROLOGUE_ROWS;
 
-// Token rows from which a step runs its Q4_K matrices in the wide matmul.
-#ifndef JFH_WIDE_FROM_ROWS
-#define JFH_WIDE_FROM_ROWS 9
-#endif
-constexpr int32_t kWideFromRows = JFH_WIDE_FROM_ROWS;
-
 void hip_check(hipError_t e, const char* what) {
     if (e != hipSuccess) throw Error(Status::DeviceError, std::string(what) + ": " + hipGetErrorString(e));
 }
@@ -582,14 +576,17 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
             gpu::launch_embed(embd_->mat, step_dev_, h_, n_rows, H, best_, gpu::kMaxRows, s);
         });
     }
-    // Steps of more than kWideFromRows rows run Q4_K matrices in the wide
-    // matmul with int8 rows quantized once per step (same codes as the decode
-    // prologue, same results per row); shorter ones in token-quad groups.
-    const bool wide = n_rows >= kWideFromRows && n_rows <= gpu::kWideRows;
-    auto wide_ok = [&](const gpu::DMat& m) { return wide && gpu::wide_matmul_supported(m.type); };
+    // Steps of a format's wide_min_rows rows or more run its matrices in the
+    // wide matmul with int8 rows quantized once per step (same codes as the
+    // decode prologue, same results per row); shorter ones in token-quad
+    // groups. The head goes wide only beyond one token-quad group: below,
+    // the quads' row groups per work-group merge the argmax more cheaply.
     auto matmul = [&](gpu::GemvArgs& a, const char* role) {
-        if (wide_ok(a.mat) && a.xq.q != nullptr) {
-            timed(std::string("k_mm_wide_q4k:") + role, gemv_bytes(a), [&] { gpu::launch_gemv_wide(a, s); });
+        const int32_t min_rows = gpu::wide_min_rows(a.mat.type);
+        const int32_t from = a.mode == gpu::kLogits ? std::max(min_rows, gpu::kQuadGroupRows + 1) : min_rows;
+        if (min_rows > 0 && a.n_tok >= from && a.n_tok <= gpu::kWideRows && a.xq.q != nullptr) {
+            timed("k_mm_wide<" + std::to_string(a.mat.type) + ">:" + role, gemv_bytes(a),
+                  [&] { gpu::launch_gemv_wide(a, s); });
         } else {
             timed(gemv_label(a) + ":" + role, gemv_bytes(a), [&] { gpu::launch_gemv(a, s); });
         }
@@ -688,7 +685,7 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         head.y_stride = static_cast<int32_t>(p.n_vocab);
         head.best = best_;
         head.store_logits = store_logits ? 1 : 0;
-        timed(gemv_label(head) + ":output", gemv_bytes(head), [&] { gpu::launch_gemv(head, s); });
+        matmul(head, "output");
         timed("k_finish", 1024.0, [&] { gpu::launch_finish(best_, step_dev_, n_out, out_dev_, s); });
     }
 }
@@ -1084,8 +1081,9 @@ bool Engine::matmul_staged(const gpu::DMat& m, uint32_t n_tok) {
 }
 
 void Engine::run_matmul(const gpu::DMat& m, const float* x, uint32_t n_tok, float* y_full, const gpu::Act8& xq) {
-    const bool wide = static_cast<int32_t>(n_tok) >= kWideFromRows && gpu::wide_matmul_supported(m.type) &&
-                      m.cols % 256 == 0;
+    const int32_t min_rows = gpu::wide_min_rows(m.type);
+    const bool wide = min_rows > 0 && static_cast<int32_t>(n_tok) >= min_rows &&
+                      static_cast<int32_t>(n_tok) <= gpu::kWideRows && m.cols % 256 == 0;
     gpu::GemvArgs a;
     a.mat = m;
     a.mat.bias = nullptr;

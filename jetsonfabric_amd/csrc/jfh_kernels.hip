@@ -1025,7 +1025,8 @@ __device__ __forceinline__ void qkv_store(const GemvArgs& a, int t, int gr, floa
 // greedy argmax. `sum(j, t)` returns the dot of local row j for token t;
 // lv holds nrows * n_tok floats of scratch.
 template <int NTHR, typename Sum>
-__device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, float* lv) {
+__device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, float* lv,
+                              unsigned long long* best_lds = nullptr) {
     constexpr int W = NTHR / kWave;
     const int n = nrows * a.n_tok;
     switch (a.mode) {
@@ -1090,7 +1091,11 @@ __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, f
                 const unsigned long long q = __shfl_xor(p, o);
                 p = q > p ? q : p;
             }
-            if (lane == 0 && p != 0ull) atomicMax(a.best + t, p);
+            // best_lds: a work-group's running best per token, merged into a.best once at its end
+            if (lane == 0 && p != 0ull) {
+                if (best_lds != nullptr) best_lds[t] = p > best_lds[t] ? p : best_lds[t];
+                else atomicMax(a.best + t, p);
+            }
         }
         break;
     }
@@ -1362,132 +1367,437 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
 }
 
 // ------------------------------------------------------------------ wide matmul on matrix cores
-// Q4_K x int8 rows for steps of up to kWideRows tokens (prefill chunks,
-// large batches). Work-group
-// = one 16-row group and every token; wave w takes the K tiles w, w + W, ...
-// as the decode matmul does. For each lane group g (values 64 g .. 64 g + 63
-// of a tile, sub-blocks 2 g and 2 g + 1) the integer dots of the 16 rows with
-// 16 tokens at a time come from v_mfma_i32_16x16x32_i8 with lane group g's
-// 8-byte code chunks as the only non-zero B operand, so every product stays
-// within one sub-block. The scale arithmetic per (tile, lane group, token,
-// row) is the decode matmul's (q4k_term), accumulated per wave and lane
-// group in the same tile order and summed over waves, then lane groups, in
-// the same order: every row equals that row computed alone, bit for bit.
-// The token tile's per-block scales and code sums, which the 16 lanes of a
-// lane group all need, are read from global memory once per wave and
-// shared through LDS (one lane per 16 bytes instead of 16 broadcast reads).
-__global__ __launch_bounds__(kMmThreads) void k_mm_wide_q4k(GemvArgs a) {
+// Quantized tiles x int8 rows for steps of 9 .. kWideRows tokens (prefill
+// chunks, long drafts, large batches). Work-group = one 16-row group and one
+// 16-token tile; wave w takes the K tiles w, w + W, ... as the decode matmul
+// does. Each v_mfma_i32_16x16x32_i8 contracts one 32-value stretch of a tile:
+// lane (i, G) brings token i's activation codes 32 s + 8 G .. + 7 (the A
+// operand) and row i's codes at the same positions (the B operand), so the
+// product is one GGML block (Q8_0), one sub-block (Q4_K), or, with the lane
+// groups of the other half zeroed, one 16-value sub-block (Q6_K, Q2_K). D
+// gives lane (i, G) the integer dots of row i with tokens 4 G + j for every
+// block, and the lane applies the decode matmul's scale arithmetic per
+// (tile, lane group, token) in the same order (q4k_term, q8_term, the Q6_K
+// scale sum). The min sums Σ m · (code sum) are exact integers below 2^24
+// and come from v_mfma_f32_16x16x4f32 as exact floats. Sums run over waves,
+// then lane groups, in the decode order: every row equals that row computed
+// alone, bit for bit.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) {
+    return static_cast<long>(static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32));
+}
+
+__device__ __forceinline__ i32x4 mfma_i8(long a, long b) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, i32x4{0, 0, 0, 0}, 0, 0, 0);
+}
+
+// D[token][row] = sum over the 4 lane groups k of A[token][k] * B[k][row]
+__device__ __forceinline__ f32x4 mfma_f32k4(float a, float b) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, f32x4{0.0F, 0.0F, 0.0F, 0.0F}, 0, 0, 0);
+}
+
+// q4k_term with the min sum given as the float of that integer
+__device__ __forceinline__ float q4k_term_f(float acc, float xd, float d, float dmin, int isum, float msum) {
+    const float t = __builtin_fmaf(d, static_cast<float>(isum), -(dmin * msum));
+    return __builtin_fmaf(xd, t, acc);
+}
+
+// Per-format operands of one tile for lane (row i, lane group G) and the
+// scale arithmetic of its 16 (lane group g, token 4 G + j) terms.
+template <uint32_t TYPE>
+struct WideTile;
+
+// Q4_K: c[g] = code chunk G of lane group g (values 64 g + 8 G .. + 7 of
+// sub-block 2 g in the low nibbles, 64 g + 32 + 8 G .. of 2 g + 1 in the high
+// ones). The min sum ma · S(2 g) + mb · S(2 g + 1) is a K = 2 product over
+// lane groups 0 and 1 (S: a 32-value code sum of the token).
+template <>
+struct WideTile<11> {
+    static constexpr bool kSums = true;
+    struct Wt {
+        uint4 hdr;
+        uint2 c[4];
+    };
+    struct Xt {
+        float s[4];
+    };
+    static __device__ __forceinline__ Wt load_w(const uint8_t* t, int i, int G) {
+        Wt w;
+        w.hdr = *reinterpret_cast<const uint4*>(t + 16 * i);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            w.c[g] = *reinterpret_cast<const uint2*>(t + 256 + 1024 * (G >> 1) + 16 * (16 * g + i) + 8 * (G & 1));
+        return w;
+    }
+    // xs: the token's 16-value code sums of this block (16 int16, in LDS)
+    static __device__ __forceinline__ Xt load_x(const uint32_t* xs, int G) {
+        Xt x;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t v = xs[2 * g + (G & 1)];  // sums 4 g + 2 G, + 1: sub-block 2 g + G
+            const int S = static_cast<int16_t>(v & 0xFFFFu) + (static_cast<int32_t>(v) >> 16);
+            x.s[g] = G < 2 ? static_cast<float>(S) : 0.0F;
+        }
+        return x;
+    }
+    static __device__ __forceinline__ void accumulate(const Wt& w, const long (&av)[8], const Xt& x,
+                                                      const float (&xd)[4], int G, float (&acc)[4][4]) {
+        const float d = h2f(w.hdr.x), dmin = h2f(w.hdr.x >> 16);
+        // row i's 24-bit fields sc 2g | sc 2g+1 | m 2g | m 2g+1 of the four lane groups
+        const uint32_t F[4] = {w.hdr.y & 0xFFFFFFu, (w.hdr.y >> 24) | ((w.hdr.z & 0xFFFFu) << 8),
+                               (w.hdr.z >> 16) | ((w.hdr.w & 0xFFu) << 16), w.hdr.w >> 8};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t f = F[g];
+            const int sca = f & 63, scb = (f >> 6) & 63;
+            const uint2 c = w.c[g];
+            const long lo = pack2(c.x & 0x0F0F0F0Fu, c.y & 0x0F0F0F0Fu);
+            const long hi = pack2((c.x >> 4) & 0x0F0F0F0Fu, (c.y >> 4) & 0x0F0F0F0Fu);
+            const i32x4 da = mfma_i8(av[2 * g], lo), db = mfma_i8(av[2 * g + 1], hi);
+            const float mB = G < 2 ? static_cast<float>((f >> (12 + 6 * G)) & 63u) : 0.0F;
+            const f32x4 ms = mfma_f32k4(x.s[g], mB);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int isum = mul24(sca, da[j]) + mul24(scb, db[j]);
+                acc[g][j] = q4k_term_f(acc[g][j], xd[j], d, dmin, isum, ms[j]);
+            }
+        }
+    }
+};
+
+// Q8_0: c[2 g + e] = values 8 G .. + 7 of GGML block 2 g + e (signed codes).
+template <>
+struct WideTile<7> {
+    static constexpr bool kSums = false;
+    struct Wt {
+        uint4 dd;
+        uint2 c[8];
+    };
+    struct Xt {};
+    static __device__ __forceinline__ Wt load_w(const uint8_t* t, int i, int G) {
+        Wt w;
+        w.dd = *reinterpret_cast<const uint4*>(t + 16 * i);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+                w.c[2 * g + e] = *reinterpret_cast<const uint2*>(t + 256 + 1024 * (2 * e + (G >> 1)) + 16 * (16 * g + i) +
+                                                                 8 * (G & 1));
+        }
+        return w;
+    }
+    static __device__ __forceinline__ Xt load_x(const uint32_t*, int) { return {}; }
+    static __device__ __forceinline__ void accumulate(const Wt& w, const long (&av)[8], const Xt&,
+                                                      const float (&xd)[4], int, float (&acc)[4][4]) {
+        const uint32_t D[4] = {w.dd.x, w.dd.y, w.dd.z, w.dd.w};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float da = h2f(D[g]), db = h2f(D[g] >> 16);
+            const i32x4 ia = mfma_i8(av[2 * g], pack2(w.c[2 * g].x, w.c[2 * g].y));
+            const i32x4 ib = mfma_i8(av[2 * g + 1], pack2(w.c[2 * g + 1].x, w.c[2 * g + 1].y));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[g][j] = q8_term(acc[g][j], xd[j], da, db, ia[j], ib[j]);
+        }
+    }
+};
+
+// Q6_K: per 32-value stretch h = 2 g + e (sub-blocks 4 g + 2 e, + 1), L[h] /
+// H[h] = the low-nibble and high-bit words that hold values 32 e + 8 G .. + 7
+// of lane group g. The codes enter as q - 32, so the dot is the decode's
+// dm - 32 · (code sum) without the sums.
+template <>
+struct WideTile<13> {
+    static constexpr bool kSums = false;
+    struct Wt {
+        uint4 sc;
+        uint32_t d;
+        uint32_t L[8], H[8];
+    };
+    struct Xt {};
+    static __device__ __forceinline__ Wt load_w(const uint8_t* t, int i, int G) {
+        Wt w;
+        w.d = *reinterpret_cast<const uint16_t*>(t + 2 * i);
+        w.sc = *reinterpret_cast<const uint4*>(t + 32 + 16 * i);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int lane_off = 16 * (16 * g + i);
+                w.L[2 * g + e] = *reinterpret_cast<const uint32_t*>(t + 288 + 1024 * e + lane_off + 4 * G);
+                w.H[2 * g + e] = *reinterpret_cast<const uint32_t*>(t + 2336 + lane_off + 4 * (2 * e + (G >> 1)));
+            }
+        }
+        return w;
+    }
+    static __device__ __forceinline__ Xt load_x(const uint32_t*, int) { return {}; }
+    static __device__ __forceinline__ void accumulate(const Wt& w, const long (&av)[8], const Xt&,
+                                                      const float (&xd)[4], int G, float (&acc)[4][4]) {
+        constexpr uint32_t M4 = 0x0F0F0F0Fu, M30 = 0x30303030u;
+        const float d = h2f(w.d);
+        const uint32_t SC[4] = {w.sc.x, w.sc.y, w.sc.z, w.sc.w};
+        const int hshift = (G & 1) ? 0 : 4;
+        const bool low = G < 2;  // lane groups 0, 1: the stretch's first sub-block
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            i32x4 dm[4];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t Lw = w.L[2 * g + e], H1 = w.H[2 * g + e] << hshift;
+                uint32_t w0 = (Lw & M4) | (H1 & M30), w1 = ((Lw >> 4) & M4) | ((H1 >> 2) & M30);
+                // q - 32 per byte (q < 64: no carry between bytes)
+                w0 = (w0 + 0x60606060u) ^ 0x80808080u;
+                w1 = (w1 + 0x60606060u) ^ 0x80808080u;
+                const long B = pack2(w0, w1);
+                dm[2 * e] = mfma_i8(av[2 * g + e], low ? B : 0L);
+                dm[2 * e + 1] = mfma_i8(av[2 * g + e], low ? 0L : B);
+            }
+            int sc[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) sc[m] = sext8(SC[g] >> (8 * m));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                int isum = 0;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) isum += mul24(sc[m], dm[m][j]);
+                acc[g][j] = __builtin_fmaf(xd[j], d * static_cast<float>(isum), acc[g][j]);
+            }
+        }
+    }
+};
+
+// Q2_K: Q[2 g + e] = the code word of sub-block 4 g + 2 e + G / 2; the min
+// sum Σ mn · (16-value code sum) is a K = 4 product over the lane groups.
+template <>
+struct WideTile<9> {
+    static constexpr bool kSums = true;
+    struct Wt {
+        uint32_t dd;
+        uint4 sc;
+        uint32_t Q[8];
+    };
+    struct Xt {
+        float s[4];
+    };
+    static __device__ __forceinline__ Wt load_w(const uint8_t* t, int i, int G) {
+        Wt w;
+        w.dd = *reinterpret_cast<const uint32_t*>(t + 4 * i);
+        w.sc = *reinterpret_cast<const uint4*>(t + 64 + 16 * i);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+                w.Q[2 * g + e] = *reinterpret_cast<const uint32_t*>(t + 320 + 16 * (16 * g + i) + 4 * (2 * e + (G >> 1)));
+        }
+        return w;
+    }
+    static __device__ __forceinline__ Xt load_x(const uint32_t* xs, int G) {
+        Xt x;
+        const int16_t* s = reinterpret_cast<const int16_t*>(xs);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) x.s[g] = static_cast<float>(s[4 * g + G]);
+        return x;
+    }
+    static __device__ __forceinline__ void accumulate(const Wt& w, const long (&av)[8], const Xt& x,
+                                                      const float (&xd)[4], int G, float (&acc)[4][4]) {
+        const float d = h2f(w.dd), dmin = h2f(w.dd >> 16);
+        const uint32_t SC[4] = {w.sc.x, w.sc.y, w.sc.z, w.sc.w};
+        const int qshift = 4 * (G & 1);
+        const bool low = G < 2;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            i32x4 dm[4];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t q = w.Q[2 * g + e] >> qshift;
+                const long B = pack2(q & 0x03030303u, (q >> 2) & 0x03030303u);
+                dm[2 * e] = mfma_i8(av[2 * g + e], low ? B : 0L);
+                dm[2 * e + 1] = mfma_i8(av[2 * g + e], low ? 0L : B);
+            }
+            const f32x4 ms = mfma_f32k4(x.s[g], static_cast<float>((SC[g] >> (8 * G + 4)) & 0xFu));
+            int sc[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) sc[m] = (SC[g] >> (8 * m)) & 0xF;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                int isum = 0;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) isum += mul24(sc[m], dm[m][j]);
+                acc[g][j] = q4k_term_f(acc[g][j], xd[j], d, dmin, isum, ms[j]);
+            }
+        }
+    }
+};
+
+// The arguments of tokens t0 .. t0 + nt - 1 of a step, as token 0 .. nt - 1.
+__device__ __forceinline__ GemvArgs token_slice(const GemvArgs& a, int t0, int nt) {
+    GemvArgs b = a;
+    b.n_tok = nt;
+    if (b.y != nullptr) b.y += static_cast<size_t>(t0) * b.y_stride;
+    if (b.best != nullptr) b.best += t0;
+    b.qkv.row0 += t0;
+    if (b.qkv.q != nullptr) b.qkv.q += static_cast<size_t>(t0) * b.qkv.n_head * b.qkv.head_dim;
+    return b;
+}
+
+// One wave's activation loads for one (token tile, K tile) item: lane
+// (i, G)'s natural bytes 64 G .. 64 G + 63 of token i, and its share of the
+// token tile's code sums and scales (lanes 0..31: token lane / 2, half
+// lane % 2 of its 16 sums; lanes 32..47: the scale of token lane - 32),
+// which the wave passes through LDS.
+struct WideAct {
+    uint4 xa[4];
+    u32x4 st;
+};
+
+// A operands from natural activation bytes: stretch s = 2 h + e (values
+// 32 s .. 32 s + 31) of lane group G is chunk 4 e + G of lane group h, so
+// for each e and 32-bit half the (chunk, lane group) 4 x 4 block is
+// transposed with two rounds of lane-group swaps.
+__device__ __forceinline__ void wide_a_operands(const uint4 (&xa)[4], long (&av)[8]) {
+    const uint32_t n[16] = {xa[0].x, xa[0].y, xa[0].z, xa[0].w, xa[1].x, xa[1].y, xa[1].z, xa[1].w,
+                            xa[2].x, xa[2].y, xa[2].z, xa[2].w, xa[3].x, xa[3].y, xa[3].z, xa[3].w};
+    uint32_t t[2][2][4];  // [e][half][h]
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            // X_r = word 8 e + 2 r + hf (chunk 4 e + r); after the swaps register r holds Y_r
+            uint32_t x0 = n[8 * e + hf], x1 = n[8 * e + 2 + hf], x2 = n[8 * e + 4 + hf], x3 = n[8 * e + 6 + hf];
+            const auto p02 = __builtin_amdgcn_permlane32_swap(x0, x2, false, false);
+            const auto p13 = __builtin_amdgcn_permlane32_swap(x1, x3, false, false);
+            const auto q01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+            const auto q23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+            t[e][hf][0] = q01[0];
+            t[e][hf][1] = q01[1];
+            t[e][hf][2] = q23[0];
+            t[e][hf][3] = q23[1];
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) av[2 * h + e] = pack2(t[e][0][h], t[e][1][h]);
+    }
+}
+
+// Work-group = `rpw` 16-row groups (rg, rg + 8, ..., all on one XCD; more
+// than one only for the logits head, which then merges one running best per
+// token into the step's argmax instead of one per row group) and up to
+// kWideTpw consecutive 16-token tiles (`tpw`). A wave keeps each of its K
+// tiles' weight operands in registers while it runs that tile for every
+// token tile of the group, with one accumulator set per token tile.
+#ifndef JFH_WIDE_TPW
+#define JFH_WIDE_TPW 2
+#endif
+constexpr int kWideTpw = JFH_WIDE_TPW;
+
+template <uint32_t TYPE, bool MERGED>
+__global__ __launch_bounds__(kMmThreads) void k_mm_wide(GemvArgs a, int32_t n_rg, int32_t tpw, int32_t rpw) {
+    using T = WideTile<TYPE>;
     constexpr int W = kMmWaves;
-    constexpr uint32_t TB = tile_bytes(11);
+    constexpr uint32_t TB = tile_bytes(TYPE);
     __shared__ float red[W][4][16][16];  // [wave][lane group][token][row] of one token tile
     __shared__ float vals[kWideRows][16];
     __shared__ u32x4 stage_s[W][16][2];
     __shared__ float stage_d[W][16];
-    const int K = static_cast<int>(a.mat.cols), nb = K / 256, n_tok = a.n_tok;
-    const int rg = blockIdx.x;
+    __shared__ unsigned long long best[kWideRows];
+    float* lv = &red[0][0][0][0];  // the epilogue's scratch (kWideRows x 16 floats) once red is read
+    static_assert(sizeof(red) >= sizeof(float) * kWideRows * 16, "epilogue scratch");
+    const int n_tok = a.n_tok, n_tt = (n_tok + 15) / 16, n_grp = (n_tt + tpw - 1) / tpw;
+    // work-group k runs on XCD k % 8: the token groups of one row group share an XCD (and its L2)
+    const int q = static_cast<int>(blockIdx.x) >> 3;
+    const int grp = q % n_grp, rg_first = (q / n_grp) * 8 * rpw + static_cast<int>(blockIdx.x & 7u);
+    if (rg_first >= n_rg) return;
+    const int K = static_cast<int>(a.mat.cols), nb = K / 256;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
     const int i = lane & 15, G = lane >> 4;
-    const uint8_t* base = a.mat.data + static_cast<size_t>(rg) * nb * TB;
+    const int tt0 = grp * tpw, ntl = min(n_tt, tt0 + tpw) - tt0;
+    const int t0 = 16 * tt0, nt = min(16 * (tt0 + ntl), n_tok) - t0;
+    const GemvArgs out = token_slice(a, t0, nt);
+    if (MERGED && threadIdx.x < kWideRows) best[threadIdx.x] = 0ull;
     const Act8 xq = a.xq;
-    // one token tile (16 tokens) at a time: the row group's tiles are re-read
-    // from L2 for each, which keeps the accumulators in registers
-#pragma unroll 1
-    for (int tt = 0; tt < (n_tok + 15) / 16; ++tt) {
-        float acc[4][4];
+    auto load_act = [&](int tt, int b) {
+        // token rows past the step repeat its last row; their sums are never stored
+        const size_t tok = static_cast<size_t>(min(16 * tt + i, n_tok - 1));
+        WideAct r;
+        const uint4* xa = reinterpret_cast<const uint4*>(xq.q + tok * K + b * 256 + 64 * G);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
+        for (int u = 0; u < 4; ++u) r.xa[u] = xa[u];
+        const int tl = lane < 32 ? lane >> 1 : lane - 32;
+        const size_t tk = static_cast<size_t>(min(16 * tt + (tl & 15), n_tok - 1));
+        if (lane >= 32) r.st.x = __float_as_uint(xq.d[tk * nb + b]);
+        else if (T::kSums) r.st = reinterpret_cast<const u32x4*>(xq.s + tk * (K / 16) + 16 * b)[lane & 1];
+        return r;
+    };
+    for (int rr = 0; rr < (MERGED ? rpw : 1); ++rr) {
+        const int rg = rg_first + 8 * rr;
+        if (rg >= n_rg) break;
+        const uint8_t* base = a.mat.data + static_cast<size_t>(rg) * nb * TB;
+        float acc[kWideTpw][4][4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[g][j] = 0.0F;
-        }
-        // A operand rows: token 16 tt + i; D fragment tokens: 16 tt + 4 G + j
-        const int8_t* xa_row = xq.q + static_cast<size_t>(min(16 * tt + i, n_tok - 1)) * K + 64 * G;
-        for (int b = wave; b < nb; b += W) {
-            const uint8_t* t = base + static_cast<size_t>(b) * TB;
-            const uint4 hdr = *reinterpret_cast<const uint4*>(t + 16 * i);
-            const uint4 w0 = *reinterpret_cast<const uint4*>(t + 256 + 16 * lane);
-            const uint4 w1 = *reinterpret_cast<const uint4*>(t + 1280 + 16 * lane);
-            long av[2][4];
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-#pragma unroll
-                for (int c = 0; c < 4; ++c) av[p][c] = *reinterpret_cast<const long*>(xa_row + b * 256 + 32 * p + 8 * c);
-            }
-            // the token tile's block scales and code sums, read once per wave
-            // (lanes 0..31: token lane / 2, half lane % 2 of its 16 sums;
-            // lanes 32..47: the scale of token lane - 32) and shared through LDS
-            {
-                const int tl = lane < 32 ? lane >> 1 : lane - 32;
-                const int tk = min(16 * tt + (tl & 15), n_tok - 1);
-                if (lane < 32) {
-                    stage_s[wave][tl][lane & 1] =
-                        reinterpret_cast<const u32x4*>(xq.s + static_cast<size_t>(tk) * (K / 16) + b * 16)[lane & 1];
-                } else if (lane < 48) {
-                    stage_d[wave][tl] = xq.d[static_cast<size_t>(tk) * nb + b];
-                }
-            }
-            __builtin_amdgcn_wave_barrier();
-            float xd[4];
-            u32x4 sums[4][2];  // the 16 code sums (int16) of each D token's block
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                xd[j] = stage_d[wave][4 * G + j];
-                sums[j][0] = stage_s[wave][4 * G + j][0];
-                sums[j][1] = stage_s[wave][4 * G + j][1];
-            }
-            __builtin_amdgcn_wave_barrier();
-            const float d = h2f(hdr.x), dmin = h2f(hdr.x >> 16);
-            // row i's 24-bit fields sc 2g | sc 2g+1 | m 2g | m 2g+1 of the four lane groups
-            const uint32_t F[4] = {hdr.y & 0xFFFFFFu, (hdr.y >> 24) | ((hdr.z & 0xFFFFu) << 8),
-                                   (hdr.z >> 16) | ((hdr.w & 0xFFu) << 16), hdr.w >> 8};
-            const uint32_t pw[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        for (int tl = 0; tl < kWideTpw; ++tl) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const uint32_t f = F[g];
-                const int sca = f & 63, scb = (f >> 6) & 63, ma = (f >> 12) & 63, mb = (f >> 18) & 63;
-                i32x4 da = {0, 0, 0, 0}, db = {0, 0, 0, 0};
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    // lane group g's 8 codes of chunk c (low nibbles: sub-block 2g, high: 2g + 1); zero elsewhere
-                    const uint32_t l0 = pw[2 * c] & 0x0F0F0F0Fu, l1 = pw[2 * c + 1] & 0x0F0F0F0Fu;
-                    const uint32_t h0 = (pw[2 * c] >> 4) & 0x0F0F0F0Fu, h1 = (pw[2 * c + 1] >> 4) & 0x0F0F0F0Fu;
-                    const long bl = G == g ? static_cast<long>(static_cast<uint64_t>(l0) | (static_cast<uint64_t>(l1) << 32)) : 0L;
-                    const long bh = G == g ? static_cast<long>(static_cast<uint64_t>(h0) | (static_cast<uint64_t>(h1) << 32)) : 0L;
-                    da = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[0][c], bl, da, 0, 0, 0);
-                    db = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[1][c], bh, db, 0, 0, 0);
-                }
+                for (int j = 0; j < 4; ++j) acc[tl][g][j] = 0.0F;
+            }
+        }
+        for (int b = wave; b < nb; b += W) {
+            const typename T::Wt w = T::load_w(base + static_cast<size_t>(b) * TB, i, G);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    // 16-value sums 4g .. 4g+3 of the token's block
-                    const uint32_t s01 = sums[j][g >> 1][2 * (g & 1)], s23 = sums[j][g >> 1][2 * (g & 1) + 1];
-                    const int s0 = static_cast<int16_t>(s01 & 0xFFFFu), s1 = static_cast<int16_t>(s01 >> 16);
-                    const int s2 = static_cast<int16_t>(s23 & 0xFFFFu), s3 = static_cast<int16_t>(s23 >> 16);
-                    const int isum = mul24(sca, da[j]) + mul24(scb, db[j]);
-                    const int msum = mul24(ma, s0 + s1) + mul24(mb, s2 + s3);
-                    acc[g][j] = q4k_term(acc[g][j], xd[j], d, dmin, isum, msum);
+            for (int tl = 0; tl < kWideTpw; ++tl) {
+                if (tl < ntl) {
+                    const WideAct r = load_act(tt0 + tl, b);
+                    if (lane < 32) {
+                        if (T::kSums) stage_s[wave][lane >> 1][lane & 1] = r.st;
+                    } else if (lane < 48) {
+                        stage_d[wave][lane - 32] = __uint_as_float(r.st.x);
+                    }
+                    __builtin_amdgcn_wave_barrier();
+                    float xd[4];  // scales of tokens 4 G + j
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) xd[j] = stage_d[wave][4 * G + j];
+                    const typename T::Xt x = T::load_x(reinterpret_cast<const uint32_t*>(&stage_s[wave][i][0]), G);
+                    __builtin_amdgcn_wave_barrier();
+                    long av[8];
+                    wide_a_operands(r.xa, av);
+                    T::accumulate(w, av, x, xd, G, acc[tl]);
                 }
             }
         }
-        // sum over waves of ((g0 + g1) + (g2 + g3)) (the decode matmul's order)
-        __syncthreads();
+        // per token tile: sum over waves of ((g0 + g1) + (g2 + g3)) (the decode matmul's order)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
+        for (int tl = 0; tl < kWideTpw; ++tl) {
+            if (tl < ntl) {
+                __syncthreads();
 #pragma unroll
-            for (int j = 0; j < 4; ++j) red[wave][g][4 * G + j][i] = acc[g][j];
+                for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) red[wave][g][4 * G + j][i] = acc[tl][g][j];
+                }
+                __syncthreads();
+                if (threadIdx.x < 256) {
+                    const int tk = threadIdx.x >> 4, r = threadIdx.x & 15;
+                    float v = 0.0F;
+#pragma unroll
+                    for (int w = 0; w < W; ++w)
+                        v += (red[w][0][tk][r] + red[w][1][tk][r]) + (red[w][2][tk][r] + red[w][3][tk][r]);
+                    vals[16 * tl + tk][r] = v;
+                }
+            }
         }
         __syncthreads();
-        if (threadIdx.x < 256) {
-            const int tk = threadIdx.x >> 4, r = threadIdx.x & 15;
-            float v = 0.0F;
-#pragma unroll
-            for (int w = 0; w < W; ++w) v += (red[w][0][tk][r] + red[w][1][tk][r]) + (red[w][2][tk][r] + red[w][3][tk][r]);
-            vals[16 * tt + tk][r] = v;
-        }
+        const int row0 = rg * 16;
+        const int nrows = min(16, static_cast<int>(a.mat.rows) - row0);
+        gemv_epilogue<kMmThreads>(out, row0, nrows, [&](int j, int t) { return vals[t][j]; }, lv,
+                                  MERGED ? best : nullptr);
     }
-    __syncthreads();
-    const int row0 = rg * 16;
-    const int nrows = min(16, static_cast<int>(a.mat.rows) - row0);
-    gemv_epilogue<kMmThreads>(a, row0, nrows, [&](int j, int t) { return vals[t][j]; }, &vals[0][0]);
+    if (MERGED) {
+        __syncthreads();
+        if (threadIdx.x < nt && best[threadIdx.x] != 0ull) atomicMax(out.best + threadIdx.x, best[threadIdx.x]);
+    }
 }
 
 // Float weights (F32/F16, small models): one wave per row, lanes over K,
@@ -2372,19 +2682,69 @@ void launch_quantize_norm(const float* x, int32_t stride, const int32_t* gather,
     check(hipGetLastError(), "normalized quantize launch");
 }
 
-bool wide_matmul_supported(uint32_t type) { return type == 11; }
+#ifndef JFH_WIDE_MIN_WGS
+#define JFH_WIDE_MIN_WGS 512
+#endif
+constexpr int kWideMinWgs = JFH_WIDE_MIN_WGS;
+#ifndef JFH_WIDE_LOGITS_WGS
+#define JFH_WIDE_LOGITS_WGS 1024
+#endif
+constexpr int kWideLogitsWgs = JFH_WIDE_LOGITS_WGS;
+
+bool wide_matmul_supported(uint32_t type) { return type == 7 || type == 9 || type == 11 || type == 13; }
+
+// Measured on 7B-shaped layers: Q4_K and Q8_0 from 9 rows; Q6_K and Q2_K,
+// whose 16-value sub-blocks take two half-masked MFMAs per 32 values, only
+// beyond one 16-slot token-quad group.
+#ifndef JFH_WIDE_FROM_ROWS
+#define JFH_WIDE_FROM_ROWS 9
+#endif
+int32_t wide_min_rows(uint32_t type) {
+    switch (type) {
+    case 7:
+    case 11: return JFH_WIDE_FROM_ROWS;
+    case 9:
+    case 13: return kQuadGroupRows + 1;
+    default: return 0;
+    }
+}
 
 void launch_gemv_wide(const GemvArgs& a, hipStream_t stream) {
     if (!wide_matmul_supported(a.mat.type) || a.xq.q == nullptr || a.xq.K != static_cast<int32_t>(a.mat.cols) ||
         a.mat.cols % kActBlock != 0 || a.n_tok < 1 || a.n_tok > kWideRows) {
-        throw std::invalid_argument("wide matmul takes Q4_K weights and up to 64 pre-quantized token rows");
+        throw std::invalid_argument("wide matmul takes Q4_K / Q6_K / Q8_0 / Q2_K weights and up to 64 pre-quantized token rows");
     }
-    if (a.mode == kLogits || (a.mode == kSwiGLU && a.mat.rows % (2 * kGluGroup) != 0) ||
-        (a.mode == kQKV && a.mat.rows % 2 != 0)) {
+    if ((a.mode == kSwiGLU && a.mat.rows % (2 * kGluGroup) != 0) || (a.mode == kQKV && a.mat.rows % 2 != 0) ||
+        (a.mode == kLogits && a.best == nullptr)) {
         throw std::invalid_argument("wide matmul mode or row layout not supported");
     }
-    const int grid = (static_cast<int>(a.mat.rows) + 15) / 16;
-    launch(k_mm_wide_q4k, dim3(grid), dim3(kMmThreads), 0, stream, a);
+    const int n_rg = (static_cast<int>(a.mat.rows) + 15) / 16, n_tt = (a.n_tok + 15) / 16;
+    // as many token tiles per work-group as still leave kWideMinWgs work-groups
+    int tpw = min(n_tt, kWideTpw);
+    while (tpw > 1 && n_rg * ((n_tt + tpw - 1) / tpw) < kWideMinWgs) --tpw;
+    // the head: row groups per work-group so that about kWideLogitsWgs work-groups merge their argmax
+    const int rpw = a.mode == kLogits ? std::max(1, n_rg / kWideLogitsWgs) : 1;
+    const int grid = (n_rg + 8 * rpw - 1) / (8 * rpw) * 8 * ((n_tt + tpw - 1) / tpw);
+    const dim3 g(grid), b(kMmThreads);
+    const bool merged = rpw > 1;
+    switch (a.mat.type) {
+    case 7:
+        if (merged) launch(k_mm_wide<7, true>, g, b, 0, stream, a, n_rg, tpw, rpw);
+        else launch(k_mm_wide<7, false>, g, b, 0, stream, a, n_rg, tpw, rpw);
+        break;
+    case 9:
+        if (merged) launch(k_mm_wide<9, true>, g, b, 0, stream, a, n_rg, tpw, rpw);
+        else launch(k_mm_wide<9, false>, g, b, 0, stream, a, n_rg, tpw, rpw);
+        break;
+    case 11:
+        if (merged) launch(k_mm_wide<11, true>, g, b, 0, stream, a, n_rg, tpw, rpw);
+        else launch(k_mm_wide<11, false>, g, b, 0, stream, a, n_rg, tpw, rpw);
+        break;
+    default:
+        if (merged) launch(k_mm_wide<13, true>, g, b, 0, stream, a, n_rg, tpw, rpw);
+        else launch(k_mm_wide<13, false>, g, b, 0, stream, a, n_rg, tpw, rpw);
+        break;
+    }
     check(hipGetLastError(), "wide matmul launch");
 }
 

@@ -174,9 +174,12 @@ void launch_quantize_norm(const float* x, int32_t stride, const int32_t* gather,
 constexpr int kWideRows = 64;
 // Whether launch_gemv_wide takes matrices of this type.
 bool wide_matmul_supported(uint32_t type);
-// Matmul of 9..kWideRows pre-quantized token rows (a.xq) on matrix cores;
-// every row's result equals launch_gemv's for that row alone. Modes kStore,
-// kAdd, kSwiGLU and kQKV.
+// Fewest token rows from which launch_gemv_wide outruns the token-quad
+// matmul for a format (0: no wide kernel for it).
+int32_t wide_min_rows(uint32_t type);
+// Matmul of up to kWideRows pre-quantized token rows (a.xq) on matrix cores,
+// 16-token tiles per work-group; every row's result equals launch_gemv's for
+// that row alone. All modes.
 void launch_gemv_wide(const GemvArgs& a, hipStream_t stream);
 // Split-K causal GQA flash attention over the f16 caches of the step's
 // sequences. Every (row, head, split) writes its (max, sum, unnormalized

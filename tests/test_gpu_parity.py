@@ -92,11 +92,12 @@ def test_matmul_matches_oracle(typed, n_tok):
         assert jo.nrmse(exact, gpu) < 1e-2
 
 
-@pytest.mark.parametrize("n_tok", [3, 4, 5, 8, 9, 33, 64])
+@pytest.mark.parametrize("n_tok", [3, 4, 5, 8, 9, 16, 17, 33, 64])
 def test_wide_matmul_rows_equal_single_rows(typed, n_tok):
     """Steps of 3 or more int8 rows run every quantized format on matrix cores
-    (token quads up to 8 rows; for Q4_K the wide kernel beyond); every row must
-    equal the same row computed alone (the decode path), bit for bit."""
+    (token quads below the format's wide threshold, 9 rows for Q4_K / Q8_0 and
+    17 for Q6_K / Q2_K, the wide kernel from there, in 16-token tiles); every
+    row must equal the same row computed alone (the decode path), bit for bit."""
     t, model, engine = typed
     rng = np.random.default_rng(100 + n_tok)
     for name in ("blk.0.attn_q.weight", "blk.1.ffn_down.weight"):
