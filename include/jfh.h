@@ -355,6 +355,39 @@ jfh_status jfh_engine_profile_batch(jfh_engine * engine, jfh_session * const * s
                                     uint32_t iterations, jfh_kernel_stat * out, uint32_t capacity,
                                     uint32_t * out_count);
 
+/* ---------------------------------------------------------------- tokenizer */
+
+/* Byte-level BPE tokenizer of a Qwen2 GGUF vocabulary: the reference's
+ * LlamaCppTokenizer (runtime/adapters/llama_cpp_tokenizer.hpp:11-31,
+ * llama_cpp_tokenizer.cpp:50-137), which serves native packages from their
+ * preserved metadata.gguf. `path`: a package directory (its metadata.gguf)
+ * or a GGUF file. JFH_STATUS_NOT_FOUND for a package without metadata.gguf,
+ * JFH_STATUS_FORMAT_ERROR for metadata without a "gpt2" vocabulary. */
+typedef struct jfh_tokenizer jfh_tokenizer;
+jfh_status jfh_tokenizer_open(const char * path, jfh_tokenizer ** out);
+void jfh_tokenizer_destroy(jfh_tokenizer * tokenizer);
+/* Tokenizer::tokenize (runtime/tokenization/tokenizer.hpp:14; llama_cpp_tokenizer.cpp:100-110):
+ * special tokens in the text are parsed, BOS/EOS added as the metadata asks;
+ * an empty result is JFH_STATUS_INVALID_ARGUMENT. *out_count receives the
+ * number of ids; a buffer of fewer than that many is
+ * JFH_STATUS_INVALID_ARGUMENT (ask with capacity 0 first). */
+jfh_status jfh_tokenizer_tokenize(const jfh_tokenizer * tokenizer, const char * text, size_t length, int32_t * ids,
+                                  uint32_t capacity, uint32_t * out_count);
+/* Tokenizer::token_piece (tokenizer.hpp:15; llama_cpp_tokenizer.cpp:112-133): the
+ * token's bytes (not NUL-terminated) into buf; *out_length receives their
+ * count, a smaller buffer is JFH_STATUS_INVALID_ARGUMENT. */
+jfh_status jfh_tokenizer_token_piece(const jfh_tokenizer * tokenizer, int32_t token, char * buf, uint32_t capacity,
+                                     uint32_t * out_length);
+/* Tokenizer::is_end_token (tokenizer.hpp:16; llama_cpp_tokenizer.cpp:135-137). */
+jfh_status jfh_tokenizer_is_end_token(const jfh_tokenizer * tokenizer, int32_t token, uint32_t * out);
+/* The end-of-generation ids in ascending order (the set is_end_token tests,
+ * without -1), e.g. for jfh_engine_set_end_tokens; *out_count receives their
+ * number, a smaller buffer is JFH_STATUS_INVALID_ARGUMENT. */
+jfh_status jfh_tokenizer_end_tokens(const jfh_tokenizer * tokenizer, int32_t * ids, uint32_t capacity,
+                                    uint32_t * out_count);
+/* Number of tokens in the vocabulary. */
+jfh_status jfh_tokenizer_vocab_size(const jfh_tokenizer * tokenizer, uint32_t * out);
+
 /* ---------------------------------------------------------------- speculation */
 
 /* PromptLookupDraft::propose (runtime/speculative/prompt_lookup_draft.cpp:15-44). */

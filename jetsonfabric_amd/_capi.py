@@ -146,6 +146,13 @@ SIGNATURES = {
                                         POINTER(c_double)]),
     "jfh_prompt_lookup_propose": (Status, [POINTER(c_uint32), c_size_t, c_uint32, c_uint32, c_uint32,
                                            POINTER(c_uint32), POINTER(c_uint32)]),
+    "jfh_tokenizer_open": (Status, [c_char_p, POINTER(c_void_p)]),
+    "jfh_tokenizer_destroy": (None, [c_void_p]),
+    "jfh_tokenizer_tokenize": (Status, [c_void_p, c_char_p, c_size_t, POINTER(c_int32), c_uint32, POINTER(c_uint32)]),
+    "jfh_tokenizer_token_piece": (Status, [c_void_p, c_int32, c_char_p, c_uint32, POINTER(c_uint32)]),
+    "jfh_tokenizer_is_end_token": (Status, [c_void_p, c_int32, POINTER(c_uint32)]),
+    "jfh_tokenizer_end_tokens": (Status, [c_void_p, POINTER(c_int32), c_uint32, POINTER(c_uint32)]),
+    "jfh_tokenizer_vocab_size": (Status, [c_void_p, POINTER(c_uint32)]),
     "jfh_generate": (Status, [c_void_p, POINTER(c_int32), c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
                               POINTER(c_int32), POINTER(c_uint32), POINTER(GenerationStats)]),
     "jfh_generate_concurrent": (Status, [c_void_p, c_uint32, POINTER(c_int32), POINTER(c_uint32), c_uint32, c_uint32,

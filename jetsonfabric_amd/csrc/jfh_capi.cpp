@@ -3,6 +3,7 @@
 
 #include "jfh_engine.hpp"
 #include "jfh_runtime.hpp"
+#include "jfh_tokenizer.hpp"
 
 #include <hip/hip_runtime_api.h>
 
@@ -70,6 +71,8 @@ jfh_status guarded(F&& fn) {
 void require(bool condition, const char* message) {
     if (!condition) throw jfh::Error(jfh::Status::InvalidArgument, message);
 }
+
+void require(bool condition, const std::string& message) { require(condition, message.c_str()); }
 
 void fill_view(const jfh_model* m, size_t index, jfh_tensor_view* out) {
     const jfh::TensorView& t = m->model->tensors()[index];
@@ -673,6 +676,69 @@ jfh_status jfh_engine_profile_batch(jfh_engine* engine, jfh_session* const* sess
             out[i].bytes = stats[i].bytes;
         }
         *out_count = k;
+    });
+}
+
+struct jfh_tokenizer {
+    std::shared_ptr<const jfh::runtime::tokenization::BpeTokenizer> tokenizer;
+};
+
+jfh_status jfh_tokenizer_open(const char* path, jfh_tokenizer** out) {
+    return guarded([&] {
+        require(path && out, "tokenizer path and output are required");
+        *out = nullptr;
+        auto t = std::make_unique<jfh_tokenizer>();
+        t->tokenizer = jfh::runtime::tokenization::BpeTokenizer::open(path);
+        *out = t.release();
+    });
+}
+
+void jfh_tokenizer_destroy(jfh_tokenizer* tokenizer) { delete tokenizer; }
+
+jfh_status jfh_tokenizer_tokenize(const jfh_tokenizer* tokenizer, const char* text, size_t length, int32_t* ids,
+                                  uint32_t capacity, uint32_t* out_count) {
+    return guarded([&] {
+        require(tokenizer && (text || length == 0) && out_count && (ids || capacity == 0), "tokenizer arguments are required");
+        const std::vector<int32_t> v = tokenizer->tokenizer->tokenize(std::string_view(text ? text : "", length));
+        *out_count = static_cast<uint32_t>(v.size());
+        require(v.size() <= capacity, "id buffer holds fewer than the " + std::to_string(v.size()) + " ids");
+        std::copy(v.begin(), v.end(), ids);
+    });
+}
+
+jfh_status jfh_tokenizer_token_piece(const jfh_tokenizer* tokenizer, int32_t token, char* buf, uint32_t capacity,
+                                     uint32_t* out_length) {
+    return guarded([&] {
+        require(tokenizer && out_length && (buf || capacity == 0), "tokenizer arguments are required");
+        const std::string piece = tokenizer->tokenizer->token_piece(token);
+        *out_length = static_cast<uint32_t>(piece.size());
+        require(piece.size() <= capacity, "piece buffer holds fewer than the " + std::to_string(piece.size()) + " bytes");
+        std::copy(piece.begin(), piece.end(), buf);
+    });
+}
+
+jfh_status jfh_tokenizer_is_end_token(const jfh_tokenizer* tokenizer, int32_t token, uint32_t* out) {
+    return guarded([&] {
+        require(tokenizer && out, "tokenizer arguments are required");
+        *out = tokenizer->tokenizer->is_end_token(token) ? 1 : 0;
+    });
+}
+
+jfh_status jfh_tokenizer_end_tokens(const jfh_tokenizer* tokenizer, int32_t* ids, uint32_t capacity,
+                                    uint32_t* out_count) {
+    return guarded([&] {
+        require(tokenizer && out_count && (ids || capacity == 0), "tokenizer arguments are required");
+        const std::vector<int32_t> v = tokenizer->tokenizer->end_tokens();
+        *out_count = static_cast<uint32_t>(v.size());
+        require(v.size() <= capacity, "id buffer holds fewer than the " + std::to_string(v.size()) + " ids");
+        std::copy(v.begin(), v.end(), ids);
+    });
+}
+
+jfh_status jfh_tokenizer_vocab_size(const jfh_tokenizer* tokenizer, uint32_t* out) {
+    return guarded([&] {
+        require(tokenizer && out, "tokenizer arguments are required");
+        *out = static_cast<uint32_t>(tokenizer->tokenizer->vocab_size());
     });
 }
 

@@ -417,7 +417,7 @@ size_t scalar_size(uint32_t t) {
 }
 }  // namespace
 
-std::map<std::string, GgufValue> parse_gguf_kv(const uint8_t* data, size_t size) {
+std::map<std::string, GgufValue> parse_gguf_kv(const uint8_t* data, size_t size, bool arrays) {
     size_t c = 0;
     auto need = [&](size_t n) { if (!fits(c, n, size)) fail(Status::FormatError, "GGUF metadata is truncated"); };
     auto str = [&]() {
@@ -450,17 +450,38 @@ std::map<std::string, GgufValue> parse_gguf_kv(const uint8_t* data, size_t size)
             v.kind = GgufValue::F32; std::memcpy(&v.f32, &bits, 4); out[key] = v;
         } else if (type == G_STR) {
             v.kind = GgufValue::Str; v.str = str(); out[key] = v;
+        } else if (type == G_BOOL || type == G_I32) {
+            const size_t es = scalar_size(type);
+            need(es);
+            v.kind = type == G_BOOL ? GgufValue::Bool : GgufValue::I32;
+            v.u32 = type == G_BOOL ? data[c] : rd32(data + c);
+            c += es;
+            out[key] = v;
         } else if (type == G_ARR) {
             need(12);
             const uint32_t et = rd32(data + c);
             const uint64_t n = rd64(data + c + 4);
             c += 12;
             if (et == G_STR) {
-                for (uint64_t k = 0; k < n; ++k) (void) str();
+                if (n > size / 8) fail(Status::FormatError, "GGUF array is invalid");
+                if (arrays) {
+                    v.kind = GgufValue::StrArr;
+                    v.strs.reserve(size_t(n));
+                    for (uint64_t k = 0; k < n; ++k) v.strs.push_back(str());
+                    out[key] = std::move(v);
+                } else {
+                    for (uint64_t k = 0; k < n; ++k) (void) str();
+                }
             } else {
                 const size_t es = scalar_size(et);
                 if (es == 0 || n > size / es) fail(Status::FormatError, "GGUF array is invalid");
                 need(size_t(n) * es);
+                if (arrays && (et == G_I32 || et == G_U32)) {
+                    v.kind = GgufValue::I32Arr;
+                    v.ints.resize(size_t(n));
+                    for (size_t k = 0; k < size_t(n); ++k) v.ints[k] = static_cast<int32_t>(rd32(data + c + 4 * k));
+                    out[key] = std::move(v);
+                }
                 c += size_t(n) * es;
             }
         } else {
@@ -605,6 +626,16 @@ std::vector<uint8_t> write_gguf_header(const std::vector<std::pair<std::string, 
         case GgufValue::U32: put32(o, G_U32); put32(o, v.u32); break;
         case GgufValue::F32: { put32(o, G_F32); uint32_t bits; std::memcpy(&bits, &v.f32, 4); put32(o, bits); break; }
         case GgufValue::Str: put32(o, G_STR); put_str(v.str); break;
+        case GgufValue::Bool: put32(o, G_BOOL); o.push_back(v.u32 ? 1 : 0); break;
+        case GgufValue::I32: put32(o, G_I32); put32(o, v.u32); break;
+        case GgufValue::StrArr:
+            put32(o, G_ARR); put32(o, G_STR); put64(o, v.strs.size());
+            for (const std::string& e : v.strs) put_str(e);
+            break;
+        case GgufValue::I32Arr:
+            put32(o, G_ARR); put32(o, G_I32); put64(o, v.ints.size());
+            for (const int32_t e : v.ints) put32(o, static_cast<uint32_t>(e));
+            break;
         }
     }
     for (const GgufTensorInfo& t : tensors) {

@@ -113,12 +113,16 @@ private:
     PackageStats stats_;
 };
 
-// Minimal GGUF v3 key/value metadata (only what the qwen2 path reads and writes).
+// Minimal GGUF v3 key/value metadata (what the qwen2 path and its tokenizer
+// read; the writer emits U32, F32 and Str). Bool and I32 scalars keep their
+// value in u32; string and 32-bit integer arrays are kept on request.
 struct GgufValue {
-    enum Kind { U32, F32, Str } kind = U32;
+    enum Kind { U32, F32, Str, Bool, I32, StrArr, I32Arr } kind = U32;
     uint32_t u32 = 0;
     float f32 = 0.0F;
     std::string str;
+    std::vector<std::string> strs;
+    std::vector<int32_t> ints;
 };
 
 struct GgufTensorInfo {
@@ -129,8 +133,9 @@ struct GgufTensorInfo {
     uint64_t offset = 0;
 };
 
-// Parses the KV section of a GGUF header; unknown value kinds are skipped.
-std::map<std::string, GgufValue> parse_gguf_kv(const uint8_t* data, size_t size);
+// Parses the KV section of a GGUF header; unknown value kinds are skipped,
+// and so are arrays unless `arrays` is set.
+std::map<std::string, GgufValue> parse_gguf_kv(const uint8_t* data, size_t size, bool arrays = false);
 
 // GGML type ids (the ids GGUF tensor infos carry) <-> JFM v2 tensor type ids
 // (engine.h:13-44; jf_model_compile.cpp:499-531) for the types this engine

@@ -590,6 +590,66 @@ class NativeEngine:
         return results, wall.value
 
 
+class Tokenizer:
+    """Byte-level BPE tokenizer of a Qwen2 GGUF vocabulary (LlamaCppTokenizer,
+    runtime/adapters/llama_cpp_tokenizer.cpp:50-137) from a package directory's
+    metadata.gguf or a GGUF file."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        check(library().jfh_tokenizer_open(os.fsencode(path), ctypes.byref(h)))
+        self._h = h
+        n = ctypes.c_uint32()
+        check(library().jfh_tokenizer_vocab_size(self._h, ctypes.byref(n)))
+        self.vocab_size = int(n.value)
+
+    def close(self) -> None:
+        if self._h:
+            library().jfh_tokenizer_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tokenize(self, text: str | bytes) -> list[int]:
+        """Tokenizer::tokenize (tokenization/tokenizer.hpp:14): special tokens parsed, BOS/EOS as
+        the metadata asks; raises InvalidArgument when nothing results."""
+        data = text.encode("utf-8") if isinstance(text, str) else bytes(text)
+        n = ctypes.c_uint32()
+        cap = 3 * len(data) + 8  # an invalid UTF-8 byte becomes U+FFFD: three byte tokens
+        out = (ctypes.c_int32 * cap)()
+        check(library().jfh_tokenizer_tokenize(self._h, data, len(data), out, cap, ctypes.byref(n)))
+        return [int(out[i]) for i in range(n.value)]
+
+    def token_piece(self, token: int) -> bytes:
+        """Tokenizer::token_piece (tokenizer.hpp:15): the token's bytes."""
+        n = ctypes.c_uint32()
+        status = library().jfh_tokenizer_token_piece(self._h, int(token), None, 0, ctypes.byref(n))
+        if status.code != 0 and n.value == 0:
+            check(status)
+        buf = ctypes.create_string_buffer(max(1, n.value))
+        check(library().jfh_tokenizer_token_piece(self._h, int(token), buf, n.value, ctypes.byref(n)))
+        return buf.raw[:n.value]
+
+    def is_end_token(self, token: int) -> bool:
+        """Tokenizer::is_end_token (tokenizer.hpp:16)."""
+        out = ctypes.c_uint32()
+        check(library().jfh_tokenizer_is_end_token(self._h, int(token), ctypes.byref(out)))
+        return bool(out.value)
+
+    def end_tokens(self) -> list[int]:
+        n = ctypes.c_uint32()
+        out = (ctypes.c_int32 * 64)()
+        check(library().jfh_tokenizer_end_tokens(self._h, out, 64, ctypes.byref(n)))
+        return [int(out[i]) for i in range(n.value)]
+
+    def detokenize(self, tokens: Iterable[int]) -> bytes:
+        return b"".join(self.token_piece(t) for t in tokens)
+
+
 def prompt_lookup_propose(history: Sequence[int], max_tokens: int, max_ngram: int = 4, min_ngram: int = 2) -> list[int]:
     """PromptLookupDraft::propose through the C ABI (prompt_lookup_draft.cpp:15-44)."""
     hist = (ctypes.c_uint32 * max(1, len(history)))(*history)

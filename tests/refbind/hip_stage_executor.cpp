@@ -9,6 +9,60 @@
 #include <utility>
 
 namespace jetsonfabric::runtime::adapters {
+
+namespace {
+[[noreturn]] void tokenizer_fail(const jfh_status& s) {
+    // the messages LlamaCppTokenizer's callers see: invalid input as std::invalid_argument
+    if (s.code == JFH_STATUS_INVALID_ARGUMENT || s.code == JFH_STATUS_NOT_FOUND || s.code == JFH_STATUS_FORMAT_ERROR) {
+        throw std::invalid_argument(s.message);
+    }
+    throw std::runtime_error(s.message);
+}
+}  // namespace
+
+CAbiTokenizer::CAbiTokenizer(const std::string& path) {
+    const jfh_status s = jfh_tokenizer_open(path.c_str(), &handle_);
+    if (s.code != JFH_STATUS_OK) tokenizer_fail(s);
+}
+
+CAbiTokenizer::~CAbiTokenizer() { jfh_tokenizer_destroy(handle_); }
+
+std::vector<std::int32_t> CAbiTokenizer::tokenize(std::string_view text) const {
+    uint32_t n = 0;
+    jfh_status s = jfh_tokenizer_tokenize(handle_, text.data(), text.size(), nullptr, 0, &n);
+    if (s.code != JFH_STATUS_OK && n == 0) tokenizer_fail(s);
+    std::vector<std::int32_t> ids(n);
+    s = jfh_tokenizer_tokenize(handle_, text.data(), text.size(), ids.data(), n, &n);
+    if (s.code != JFH_STATUS_OK) tokenizer_fail(s);
+    return ids;
+}
+
+std::string CAbiTokenizer::token_piece(std::int32_t token) const {
+    uint32_t n = 0;
+    jfh_status s = jfh_tokenizer_token_piece(handle_, token, nullptr, 0, &n);
+    if (s.code != JFH_STATUS_OK && n == 0) tokenizer_fail(s);
+    std::string piece(n, '\0');
+    s = jfh_tokenizer_token_piece(handle_, token, piece.data(), n, &n);
+    if (s.code != JFH_STATUS_OK) tokenizer_fail(s);
+    return piece;
+}
+
+bool CAbiTokenizer::is_end_token(std::int32_t token) const {
+    uint32_t out = 0;
+    const jfh_status s = jfh_tokenizer_is_end_token(handle_, token, &out);
+    if (s.code != JFH_STATUS_OK) tokenizer_fail(s);
+    return out != 0;
+}
+
+std::vector<std::int32_t> CAbiTokenizer::end_tokens() const {
+    uint32_t n = 0;
+    jfh_status s = jfh_tokenizer_end_tokens(handle_, nullptr, 0, &n);
+    if (s.code != JFH_STATUS_OK && n == 0) tokenizer_fail(s);
+    std::vector<std::int32_t> ids(n);
+    s = jfh_tokenizer_end_tokens(handle_, ids.data(), n, &n);
+    if (s.code != JFH_STATUS_OK) tokenizer_fail(s);
+    return ids;
+}
 namespace {
 
 using inference::ExecutionResult;

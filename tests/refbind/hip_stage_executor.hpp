@@ -25,6 +25,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <string_view>
 #include <unordered_map>
 #include <vector>
 
@@ -37,6 +38,27 @@ struct HipStageConfig {
     inference::StagePosition position;
     inference::LayerRange layers;
     int speculative_max_tokens = 8;  // verify width - 1 (worker/config.cpp:105-107)
+};
+
+// The reference's tokenizer interface (runtime/tokenization/tokenizer.hpp:
+// 10-17) over the engine's C-ABI tokenizer: the drop-in for
+// LlamaCppTokenizer (runtime/adapters/llama_cpp_tokenizer.hpp:11-31), from a
+// package directory's metadata.gguf or a GGUF file.
+class CAbiTokenizer final : public tokenization::Tokenizer {
+public:
+    explicit CAbiTokenizer(const std::string& path);
+    ~CAbiTokenizer() override;
+    CAbiTokenizer(const CAbiTokenizer&) = delete;
+    CAbiTokenizer& operator=(const CAbiTokenizer&) = delete;
+
+    std::vector<std::int32_t> tokenize(std::string_view text) const override;
+    std::string token_piece(std::int32_t token) const override;
+    bool is_end_token(std::int32_t token) const override;
+    // the end-of-generation ids, for jfh_engine_set_end_tokens
+    std::vector<std::int32_t> end_tokens() const;
+
+private:
+    jfh_tokenizer* handle_ = nullptr;
 };
 
 class HipStageExecutor final : public inference::Executor {

@@ -11,6 +11,8 @@
 //     same package chained over activation payloads
 //   verify and execute_batch: multi-row decode equals serial decode; a batch
 //     of sessions equals each session alone
+//   text: a text prompt through the executor with the C-ABI tokenizer (the
+//     LlamaCppTokenizer drop-in) on a package with a byte-level BPE vocabulary
 //   continuous batching: continuous_batching_executor_test.cpp:99-133 with
 //     this executor as the delegate: concurrent decode steps coalesce into one
 //     engine step; then two concurrent prompt-lookup-shaped generations on a
@@ -399,7 +401,73 @@ void continuous_batching_cases(Engine& model) {
     expect(coalesced > 0, "concurrent decode steps were coalesced into two-sequence engine steps");
 }
 
+// A text prompt through the executor with the C-ABI tokenizer, on a model
+// whose package carries a byte-level BPE vocabulary
+// (native_stage_executor.cpp:176-210: the prompt text is tokenized, the
+// sampled token's piece and end flag come from the tokenizer): the prompt
+// ids, the sampled tokens, their pieces and end flags equal the C ABI's
+// tokenizer and a direct session on the same ids.
+void text_cases(const char* package) {
+    Engine whole(package, 0, std::numeric_limits<std::uint32_t>::max());
+    jfh_model_params params{};
+    ok(jfh_engine_get_params(whole.engine, &params), "engine params");
+    const int layers = static_cast<int>(params.n_layer);
+    auto tok = std::make_shared<rt::adapters::CAbiTokenizer>(package);
+    const std::vector<std::int32_t> end = tok->end_tokens();
+    expect(!end.empty() && tok->is_end_token(-1), "the vocabulary has end-of-generation ids");
+    ok(jfh_engine_set_end_tokens(whole.engine, end.data(), static_cast<std::uint32_t>(end.size())), "end tokens");
+    const std::string prompt = "<|im_start|>user\nReply with OK only.<|im_end|>\n<|im_start|>assistant\n";
+    const std::vector<std::int32_t> ids = tok->tokenize(prompt);
+
+    jfh_session* direct = nullptr;
+    ok(jfh_session_create(whole.engine, 64, &direct), "session");
+    std::int32_t want = -1;
+    ok(jfh_session_prefill(direct, ids.data(), static_cast<std::uint32_t>(ids.size()), &want, nullptr), "prefill");
+
+    HipStageExecutor executor(stage_config(whole.engine, tok, 64, {0, 1}, {0, layers}));
+    StageInput in = make_input("text-session", Phase::Prefill, 0, {0, 1}, {0, layers}, text_payload(prompt), 4);
+    ExecutionResult r = executor.execute(in);
+    expect(r.ok, "text prefill: " + r.error.message);
+    if (!r.ok) return;
+    std::vector<std::uint32_t> uids(ids.begin(), ids.end());
+    expect(r.output.prompt_token_ids == uids, "prompt ids are the tokenizer's");
+    for (int step = 1; step <= 3; ++step) {
+        const std::int32_t got = rt::inference::decode_single_token(r.output.payload);
+        expect(got == want, "text step " + std::to_string(step) + " samples the direct session's token");
+        expect(r.output.token_text == tok->token_piece(got), "token text is the tokenizer's piece");
+        expect(r.output.end_of_generation == tok->is_end_token(got), "end flag is the tokenizer's");
+        in.phase = Phase::Decode;
+        in.decode_step = step;
+        in.payload = rt::inference::sampled_token_payload(got);
+        r = executor.execute(in);
+        expect(r.ok, "text decode: " + r.error.message);
+        if (!r.ok) break;
+        ok(jfh_session_decode(direct, got, &want, nullptr), "decode");
+    }
+    jfh_session_destroy(direct);
+    executor.close_session(in.session_id);
+    try {
+        (void) tok->tokenize("");
+        expect(false, "an empty prompt tokenized");
+    } catch (const std::invalid_argument& e) {
+        expect(std::string(e.what()) == "native prompt tokenization produced no tokens", e.what());
+    }
+}
+
 }  // namespace
+
+// The text case alone, on a package with a vocabulary.
+extern "C" int jfh_refbind_text_main(const char* package) try {
+    failures = 0;
+    text_cases(package);
+    if (failures == 0) std::printf("refbind text tests passed\n");
+    std::fflush(stdout);
+    return failures;
+} catch (const std::exception& e) {
+    std::printf("FAIL: %s\n", e.what());
+    std::fflush(stdout);
+    return 1;
+}
 
 extern "C" int jfh_refbind_test_main(const char* fixture_package) try {
     failures = 0;

@@ -52,3 +52,36 @@ def test_reference_executor_contract_drives_the_engine(tmp_path, capfd):
     out = capfd.readouterr().out
     assert rc == 0, out
     assert "refbind tests passed" in out
+
+
+def test_reference_executor_serves_text_with_the_tokenizer(tmp_path, capfd):
+    """The text path of the reference contract: tests/refbind's CAbiTokenizer
+    (the reference's Tokenizer over the C ABI, in place of LlamaCppTokenizer)
+    tokenizes a ChatML prompt for the executor on a two-layer model imported
+    from a GGUF file with a byte-level BPE vocabulary; prompt ids, sampled
+    tokens, pieces and end flags equal the tokenizer's and a direct session's."""
+    if not os.path.exists(LIB):
+        pytest.skip("tests/refbind/_ref/librefbind.so is built only where the reference checkout is present "
+                    "(make -C tests/refbind)")
+    newest = max(os.path.getmtime(p) for p in _inputs())
+    assert os.path.getmtime(LIB) >= newest, "tests/refbind/_ref/librefbind.so is stale: make -C tests/refbind"
+    pytest.importorskip("tokenizers")
+    from tests.test_tokenizer import gguf_with_vocab, train_vocab
+    hf = train_vocab()
+    cfg = jf.ModelConfig(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, n_vocab=hf.get_vocab_size(), n_ctx=128)
+    model = jf.Model.synthesize(cfg, seed=9)
+    path = tmp_path / "vocab.gguf"
+    gguf_with_vocab(model, hf, str(path))
+    model.close()
+    imported = jf.Model.open_gguf(str(path))
+    package = tmp_path / "vocab.jfm"
+    imported.write_package(str(package))
+    imported.close()
+    jf.library()
+    main = ctypes.CDLL(LIB).jfh_refbind_text_main
+    main.argtypes = [ctypes.c_char_p]
+    main.restype = ctypes.c_int
+    rc = main(str(package).encode())
+    out = capfd.readouterr().out
+    assert rc == 0, out
+    assert "refbind text tests passed" in out
