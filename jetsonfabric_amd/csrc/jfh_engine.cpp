@@ -17,6 +17,12 @@ namespace {
 #endif
 constexpr int32_t kNormedPrologueRows = JFH_NORMED_PROLOGUE_ROWS;
 
+// Logits rows from which the head runs in the wide matmul (below: token quads).
+#ifndef JFH_WIDE_HEAD_FROM_ROWS
+#define JFH_WIDE_HEAD_FROM_ROWS (gpu::kQuadGroupRows + 1)
+#endif
+constexpr int32_t kWideHeadFromRows = JFH_WIDE_HEAD_FROM_ROWS;
+
 void hip_check(hipError_t e, const char* what) {
     if (e != hipSuccess) throw Error(Status::DeviceError, std::string(what) + ": " + hipGetErrorString(e));
 }
@@ -583,7 +589,7 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
     // the quads' row groups per work-group merge the argmax more cheaply.
     auto matmul = [&](gpu::GemvArgs& a, const char* role) {
         const int32_t min_rows = gpu::wide_min_rows(a.mat.type);
-        const int32_t from = a.mode == gpu::kLogits ? std::max(min_rows, gpu::kQuadGroupRows + 1) : min_rows;
+        const int32_t from = a.mode == gpu::kLogits ? std::max(min_rows, kWideHeadFromRows) : min_rows;
         if (min_rows > 0 && a.n_tok >= from && a.n_tok <= gpu::kWideRows && a.xq.q != nullptr) {
             timed("k_mm_wide<" + std::to_string(a.mat.type) + ">:" + role, gemv_bytes(a),
                   [&] { gpu::launch_gemv_wide(a, s); });

@@ -1024,14 +1024,24 @@ __device__ __forceinline__ void qkv_store(const GemvArgs& a, int t, int gr, floa
 // Row results of a work-group -> bias / residual / SwiGLU / RoPE + cache /
 // greedy argmax. `sum(j, t)` returns the dot of local row j for token t;
 // lv holds nrows * n_tok floats of scratch.
-template <int NTHR, typename Sum>
+#ifndef JFH_ARGMAX_FILTER
+#define JFH_ARGMAX_FILTER 1
+#endif
+// Which modes an instantiation handles: every mode, every mode but kLogits,
+// or kLogits alone (kernels that never see a mode do not carry its code or
+// its registers).
+enum EpilogueModes : int { kAllModes = 0, kNoLogits = 1, kLogitsOnly = 2 };
+
+template <int NTHR, int MODES = kAllModes, typename Sum>
 __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, float* lv,
                               unsigned long long* best_lds = nullptr) {
     constexpr int W = NTHR / kWave;
     const int n = nrows * a.n_tok;
-    switch (a.mode) {
+    const int mode = MODES == kLogitsOnly ? kLogits : (MODES == kNoLogits && a.mode == kLogits ? -1 : a.mode);
+    switch (mode) {
     case kStore:
     case kAdd:
+        if constexpr (MODES == kLogitsOnly) break;
         for (int idx = threadIdx.x; idx < n; idx += NTHR) {
             const int t = idx / nrows, j = idx - t * nrows, gr = row0 + j;
             float* out = a.y + static_cast<size_t>(t) * a.y_stride + gr;
@@ -1040,6 +1050,7 @@ __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, f
         }
         break;
     case kSwiGLU: {
+        if constexpr (MODES == kLogitsOnly) break;
         const int half = nrows / 2;
         for (int idx = threadIdx.x; idx < half * a.n_tok; idx += NTHR) {
             const int t = idx / half, jj = idx - t * half;
@@ -1051,6 +1062,7 @@ __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, f
         break;
     }
     case kQKV: {
+        if constexpr (MODES == kLogitsOnly) break;
         const int Hq = a.qkv.n_head * a.qkv.head_dim, kv = a.qkv.n_head_kv * a.qkv.head_dim;
         for (int idx = threadIdx.x; idx < n; idx += NTHR) {
             const int t = idx / nrows, j = idx - t * nrows, gr = row0 + j;
@@ -1066,6 +1078,7 @@ __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, f
         break;
     }
     case kLogits: {
+        if constexpr (MODES == kNoLogits) break;
         for (int idx = threadIdx.x; idx < n; idx += NTHR) {
             const int t = idx / nrows, j = idx - t * nrows, gr = row0 + j;
             const float v = sum(j, t) + (a.mat.bias ? a.mat.bias[gr] : 0.0F);
@@ -1093,8 +1106,17 @@ __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, f
             }
             // best_lds: a work-group's running best per token, merged into a.best once at its end
             if (lane == 0 && p != 0ull) {
-                if (best_lds != nullptr) best_lds[t] = p > best_lds[t] ? p : best_lds[t];
-                else atomicMax(a.best + t, p);
+                if (best_lds != nullptr) {
+                    best_lds[t] = p > best_lds[t] ? p : best_lds[t];
+                } else {
+#if JFH_ARGMAX_FILTER
+                    // the slot only grows: a best at or below its current value needs no atomic
+                    if (p > __hip_atomic_load(a.best + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+                        atomicMax(a.best + t, p);
+#else
+                    atomicMax(a.best + t, p);
+#endif
+                }
             }
         }
         break;
@@ -1791,8 +1813,8 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide(GemvArgs a, int32_t n_rg
         __syncthreads();
         const int row0 = rg * 16;
         const int nrows = min(16, static_cast<int>(a.mat.rows) - row0);
-        gemv_epilogue<kMmThreads>(out, row0, nrows, [&](int j, int t) { return vals[t][j]; }, lv,
-                                  MERGED ? best : nullptr);
+        gemv_epilogue<kMmThreads, MERGED ? kLogitsOnly : kNoLogits>(
+            out, row0, nrows, [&](int j, int t) { return vals[t][j]; }, lv, MERGED ? best : nullptr);
     }
     if (MERGED) {
         __syncthreads();
@@ -2726,7 +2748,7 @@ void launch_gemv_wide(const GemvArgs& a, hipStream_t stream) {
     const int rpw = a.mode == kLogits ? std::max(1, n_rg / kWideLogitsWgs) : 1;
     const int grid = (n_rg + 8 * rpw - 1) / (8 * rpw) * 8 * ((n_tt + tpw - 1) / tpw);
     const dim3 g(grid), b(kMmThreads);
-    const bool merged = rpw > 1;
+    const bool merged = a.mode == kLogits;  // the head kernel: the only one with the argmax epilogue
     switch (a.mat.type) {
     case 7:
         if (merged) launch(k_mm_wide<7, true>, g, b, 0, stream, a, n_rg, tpw, rpw);
