@@ -1936,9 +1936,21 @@ constexpr int kAttnTile = 16;
 constexpr int kAttnWgKeys = kAttnTile * (kAttnThreads / kWave);
 constexpr int kAttnMaxSplits = 32;
 
-__device__ __forceinline__ int attn_split_len(int n_keys, int splits_max) {
+#ifndef JFH_ATTN_PREFILL_KEYS
+#define JFH_ATTN_PREFILL_KEYS 256
+#endif
+// Keys per split of a sequence with n_keys keys and len rows in the step: the
+// decode rule (about n_keys / splits_max, in whole rounds of the work-group's
+// waves), which depends on the position alone, so a verify or batched step
+// splits every row's keys exactly as serial decode does; a sequence bringing
+// more rows than any verify step (a prefill chunk) takes splits of at least
+// JFH_ATTN_PREFILL_KEYS keys, several tiles per wave. The attention and merge
+// kernels use the same rule.
+__device__ __forceinline__ int attn_split_len(int n_keys, int len, int splits_max) {
     int L = (n_keys + splits_max - 1) / splits_max;
-    return (L + kAttnWgKeys - 1) / kAttnWgKeys * kAttnWgKeys;
+    L = (L + kAttnWgKeys - 1) / kAttnWgKeys * kAttnWgKeys;
+    if (JFH_ATTN_PREFILL_KEYS > 0 && len > kQuadGroupRows) L = max(L, JFH_ATTN_PREFILL_KEYS);
+    return L;
 }
 
 // K quarter of the lane's key (HD > 0) and the lane's V pair of all 16 keys of the tile at t0.
@@ -1986,7 +1998,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
     if (q_begin >= NQ) return;
     const int nq = min(QPW, NQ - q_begin);
     const int n_keys = pos0 + len;
-    const int L = attn_split_len(n_keys, splits_max);
+    const int L = attn_split_len(n_keys, len, splits_max);
     const int n_splits = (n_keys + L - 1) / L;
     const int split = blockIdx.x;
     if (split >= n_splits) return;
@@ -2206,7 +2218,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_mfma(const float* __
     const int q_begin = qg * R;
     if (q_begin >= NQ) return;
     const int n_keys = pos0 + len;
-    const int L = attn_split_len(n_keys, splits_max);
+    const int L = attn_split_len(n_keys, len, splits_max);
     const int n_splits = (n_keys + L - 1) / L;
     const int split = blockIdx.x;
     if (split >= n_splits) return;
@@ -2355,7 +2367,7 @@ __global__ __launch_bounds__(256) void k_attention_merge(const float* __restrict
     const int c = blockIdx.x * 256 + threadIdx.x;
     const SeqDev& sd = step->seqs[step->seq[row]];
     const int n_keys = sd.pos0 + sd.len;
-    const int L = attn_split_len(n_keys, splits_max);
+    const int L = attn_split_len(n_keys, sd.len, splits_max);
     const int n_splits = (n_keys + L - 1) / L;
     float v = 0.0F;
     if (c < H) {
