@@ -1024,9 +1024,6 @@ __device__ __forceinline__ void qkv_store(const GemvArgs& a, int t, int gr, floa
 // Row results of a work-group -> bias / residual / SwiGLU / RoPE + cache /
 // greedy argmax. `sum(j, t)` returns the dot of local row j for token t;
 // lv holds nrows * n_tok floats of scratch.
-#ifndef JFH_ARGMAX_FILTER
-#define JFH_ARGMAX_FILTER 1
-#endif
 // Which modes an instantiation handles: every mode, every mode but kLogits,
 // or kLogits alone (kernels that never see a mode do not carry its code or
 // its registers).
@@ -1109,13 +1106,9 @@ __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, f
                 if (best_lds != nullptr) {
                     best_lds[t] = p > best_lds[t] ? p : best_lds[t];
                 } else {
-#if JFH_ARGMAX_FILTER
                     // the slot only grows: a best at or below its current value needs no atomic
                     if (p > __hip_atomic_load(a.best + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
                         atomicMax(a.best + t, p);
-#else
-                    atomicMax(a.best + t, p);
-#endif
                 }
             }
         }
@@ -1404,8 +1397,6 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
 // and come from v_mfma_f32_16x16x4f32 as exact floats. Sums run over waves,
 // then lane groups, in the decode order: every row equals that row computed
 // alone, bit for bit.
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
 __device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) {
     return static_cast<long>(static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32));
 }
