@@ -985,14 +985,28 @@ __device__ __forceinline__ unsigned long long pack_best(float v, uint32_t idx) {
 }
 
 // ------------------------------------------------------------------ matmul epilogues
+// Step fields the QKV epilogue needs for one token row: its position and its
+// sequence's cache.
+struct QkvRow {
+    int32_t pos;
+    int32_t capacity;
+    uint16_t* k;
+    uint16_t* v;
+};
+
+__device__ __forceinline__ QkvRow qkv_row(const QkvOut& o, int t) {
+    const StepDev* st = o.step;
+    const SeqDev& sd = st->seqs[st->seq[o.row0 + t]];
+    return QkvRow{st->pos[o.row0 + t], sd.capacity, sd.k, sd.v};
+}
+
 #pragma clang fp contract(off)
-__device__ __forceinline__ void qkv_store(const GemvArgs& a, int t, int gr, float va, float vb, bool pair) {
+__device__ __forceinline__ void qkv_store(const GemvArgs& a, int t, int gr, float va, float vb, bool pair,
+                                          const QkvRow& sd) {
     // gr: first fused row of a rotated pair (q or k) or a v row (pair == false)
     const QkvOut& o = a.qkv;
     const int hd = o.head_dim, half = hd / 2, Hq = o.n_head * hd, kv = o.n_head_kv * hd;
-    const StepDev* st = o.step;
-    const int pos = st->pos[o.row0 + t];
-    const SeqDev& sd = st->seqs[st->seq[o.row0 + t]];
+    const int pos = sd.pos;
     if (pair) {
         const int region = gr < Hq ? 0 : 1;
         const int g = region == 0 ? gr : gr - Hq;
@@ -1064,12 +1078,13 @@ __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, f
         for (int idx = threadIdx.x; idx < n; idx += NTHR) {
             const int t = idx / nrows, j = idx - t * nrows, gr = row0 + j;
             const float* bias = a.mat.bias;
+            const QkvRow rw = qkv_row(a.qkv, t);
             if (gr < Hq + kv) {
                 if (gr & 1) continue;
                 qkv_store(a, t, gr, sum(j, t) + (bias ? bias[gr] : 0.0F), sum(j + 1, t) + (bias ? bias[gr + 1] : 0.0F),
-                          true);
+                          true, rw);
             } else {
-                qkv_store(a, t, gr, sum(j, t) + (bias ? bias[gr] : 0.0F), 0.0F, false);
+                qkv_store(a, t, gr, sum(j, t) + (bias ? bias[gr] : 0.0F), 0.0F, false, rw);
             }
         }
         break;
@@ -1944,6 +1959,22 @@ __device__ __forceinline__ int attn_split_len(int n_keys, int len, int splits_ma
     return L;
 }
 
+// A work-group whose key split lies beyond the sequence's last key writes the
+// empty partial (max -inf, sum 0, output 0) for its query rows, so that every
+// split slot below splits_max holds this step's value and the merge reads
+// them without consulting the step descriptor.
+template <int NTHR>
+__device__ __forceinline__ void attn_empty_split(float* partial, int q_begin, int nq, int G, int kvh, int row0,
+                                                 int n_head, int hd, int splits_max, int split) {
+    for (int e = threadIdx.x; e < nq * (hd + 2); e += NTHR) {
+        const int i = e / (hd + 2), c = e - i * (hd + 2);
+        const int qi = q_begin + i;
+        const int t = qi / G, head = kvh * G + qi % G;
+        partial[((static_cast<size_t>(row0 + t) * n_head + head) * splits_max + split) * (hd + 2) + c] =
+            c == 0 ? -INFINITY : 0.0F;
+    }
+}
+
 // K quarter of the lane's key (HD > 0) and the lane's V pair of all 16 keys of the tile at t0.
 template <int HD>
 __device__ __forceinline__ void attn_load_tile(global_ptr<const uint16_t> kc, global_ptr<const uint16_t> vc, int t0,
@@ -1992,7 +2023,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
     const int L = attn_split_len(n_keys, len, splits_max);
     const int n_splits = (n_keys + L - 1) / L;
     const int split = blockIdx.x;
-    if (split >= n_splits) return;
+    if (split >= n_splits) {
+        attn_empty_split<kAttnThreads>(partial, q_begin, nq, G, kvh, row0, n_head, hd, splits_max, split);
+        return;
+    }
     const int k0 = split * L, k1 = min(n_keys, k0 + L);
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int kk = lane >> 2, qq = lane & 3;
@@ -2201,9 +2235,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_mfma(const float* __
     __shared__ float Ms[W][R], Ls[W][R];
     __shared__ float Os[W][HD][R];
     const int seq = blockIdx.z;
-    if (seq >= step->n_seq) return;
+    // the sequence's fields are read together with n_seq (seq < gridDim.z <= kMaxSeq keeps the
+    // read inside the descriptor), not after the check
     const int32_t pos0 = step->seqs[seq].pos0, len = step->seqs[seq].len, row0 = step->seqs[seq].row0;
     const int32_t capacity = step->seqs[seq].capacity;
+    if (seq >= step->n_seq) return;
     const int G = n_head / n_head_kv, NQ = G * len, H = n_head * HD;
     const int kvh = blockIdx.y / qgroups, qg = blockIdx.y % qgroups;
     const int q_begin = qg * R;
@@ -2212,7 +2248,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_mfma(const float* __
     const int L = attn_split_len(n_keys, len, splits_max);
     const int n_splits = (n_keys + L - 1) / L;
     const int split = blockIdx.x;
-    if (split >= n_splits) return;
+    if (split >= n_splits) {
+        attn_empty_split<kAttnThreads>(partial, q_begin, min(R, NQ - q_begin), G, kvh, row0, n_head, HD, splits_max,
+                                       split);
+        return;
+    }
     const int k0 = split * L, k1 = min(n_keys, k0 + L);
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int r = lane & (R - 1), grp = lane >> 4;
@@ -2349,17 +2389,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_mfma(const float* __
 
 // Combines the split partials of every (row, head): one work-group per
 // (row, 256 output values); with xq set the 256 values are quantized into xq.
-__global__ __launch_bounds__(256) void k_attention_merge(const float* __restrict__ partial,
-                                                         const StepDev* __restrict__ step, int32_t n_head,
+// Every split slot below splits_max holds this step's partial (splits past a
+// sequence's last key hold the empty one), so the partials are requested at
+// the kernel's start, with no lookup of the step descriptor before them; an
+// empty split adds exactly zero, as a split beyond the last one did when the
+// merge skipped it.
+__global__ __launch_bounds__(256) void k_attention_merge(const float* __restrict__ partial, int32_t n_head,
                                                          int32_t hd, int32_t splits_max, float* __restrict__ out,
                                                          Act8 xq) {
     __shared__ float vals[256];
     const int row = blockIdx.y, H = n_head * hd;
     const int c = blockIdx.x * 256 + threadIdx.x;
-    const SeqDev& sd = step->seqs[step->seq[row]];
-    const int n_keys = sd.pos0 + sd.len;
-    const int L = attn_split_len(n_keys, sd.len, splits_max);
-    const int n_splits = (n_keys + L - 1) / L;
     float v = 0.0F;
     if (c < H) {
         const int head = c / hd, dcol = c - head * hd;
@@ -2368,14 +2408,14 @@ __global__ __launch_bounds__(256) void k_attention_merge(const float* __restrict
         float pm[kAttnMaxSplits], pl[kAttnMaxSplits], po[kAttnMaxSplits];
 #pragma unroll
         for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
-            const float* p = base + min(sp, n_splits - 1) * (hd + 2);
+            const float* p = base + min(sp, splits_max - 1) * (hd + 2);
             pm[sp] = p[0];
             pl[sp] = p[1];
             po[sp] = p[2 + dcol];
         }
 #pragma unroll
         for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
-            if (sp >= n_splits) pm[sp] = -INFINITY;
+            if (sp >= splits_max) pm[sp] = -INFINITY;
         }
         float M = -INFINITY;
 #pragma unroll
@@ -2801,6 +2841,7 @@ void launch_attention(const float* q, const StepDev* step, int32_t max_len, int3
     if (head_dim > 2 * kWave || head_dim % 4 != 0) {
         throw std::invalid_argument("attention supports head dims that are multiples of 4 up to 128");
     }
+    if (n_seq < 1 || n_seq > kMaxSeq) throw std::invalid_argument("attention step needs 1..kMaxSeq sequences");
     const bool mfma = head_dim == 128 || head_dim == 64;
     const int group_rows = mfma ? kAttnRows : kAttnQPW;
     const int qgroups = (G * max_len + group_rows - 1) / group_rows;
@@ -2826,7 +2867,8 @@ void launch_attention_merge(const float* partial, const StepDev* step, int32_t n
     const int H = n_head * head_dim;
     if (xq.q != nullptr && (H % 256 != 0 || xq.K != H)) throw std::invalid_argument("merge quantization shape mismatch");
     dim3 grid((H + 255) / 256, n_rows);
-    launch(k_attention_merge, grid, dim3(256), 0, stream, partial, step, n_head, head_dim, splits, out, xq);
+    (void) step;
+    launch(k_attention_merge, grid, dim3(256), 0, stream, partial, n_head, head_dim, splits, out, xq);
     check(hipGetLastError(), "attention merge launch");
 }
 
