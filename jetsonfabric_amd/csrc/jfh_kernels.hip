@@ -457,9 +457,11 @@ __device__ __forceinline__ int mul24(int a, int b) { return __mul24(a, b); }
 template <uint32_t TYPE>
 struct Tile;
 
-// A Q4_K tile's share of one lane group (two sub-blocks) for one token:
-// acc + xd * (d * isum - dmin * msum), with the fused products as written.
-// The decode and prefill matmuls both use it, so they round alike.
+// The float step of a K-quant tile for one token: acc + xd * (d * isum -
+// dmin * msum), with the fused products as written. Q4_K applies it once per
+// tile to the integer totals over all eight sub-blocks (GGML's super-block
+// sums, ggml_vec_dot_q4_K_q8_K), Q2_K once per lane group; the decode, token
+// quad and wide matmuls all use it, so they round alike.
 __device__ __forceinline__ float q4k_term(float acc, float xd, float d, float dmin, int isum, int msum) {
     const float t = __builtin_fmaf(d, static_cast<float>(isum), -(dmin * static_cast<float>(msum)));
     return __builtin_fmaf(xd, t, acc);
@@ -520,7 +522,13 @@ struct Tile<11> {
                 const int16_t* s = x.s + tc * x.s_stride + 4 * g;
                 const int isum = mul24(sca, da) + mul24(scb, db);
                 const int msum = mul24(ma, s[0] + s[1]) + mul24(mb, s[2] + s[3]);
-                acc[t] = q4k_term(acc[t], x.d[tc * x.d_stride], d, dmin, isum, msum);
+                // the tile's integer totals over the four lane groups (lanes i, i + 16, i + 32,
+                // i + 48); lane group 0 takes the float step, the others keep exact zeros
+                int it = isum + __shfl_xor(isum, 16);
+                it += __shfl_xor(it, 32);
+                int mt = msum + __shfl_xor(msum, 16);
+                mt += __shfl_xor(mt, 32);
+                if (g == 0) acc[t] = q4k_term(acc[t], x.d[tc * x.d_stride], d, dmin, it, mt);
             }
         }
     }
@@ -680,8 +688,10 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 // values alone — the same integer the decode dot computes for that lane
 // group. Four MFMAs (chunks of 8 values) per sub-block parity give the dots of
 // sub-blocks 2 G' (low nibbles) and 2 G' + 1 (high nibbles). Lane (row i,
-// lane group L) then holds token 4 q + L's dots for all four lane groups and
-// applies q4k_term per lane group in the decode order, keeping acc[4 q + G'].
+// lane group L) then holds token 4 q + L's dots for all four lane groups,
+// sums them with their scales into the tile's integer totals and applies
+// q4k_term once into acc[4 q] (acc[4 q + 1 .. 3] stay exact zeros, so the
+// lane-group reduction ((g0 + g1) + (g2 + g3)) returns the decode dot's sum).
 struct TileQ4Quad {
     struct Regs {
         uint4 w0, w1, hdr;
@@ -734,6 +744,9 @@ struct TileQ4Quad {
             const u32x4* sp = reinterpret_cast<const u32x4*>(x.s + tk * x.s_stride);
             const u32x4 s03 = sp[0], s47 = sp[1];  // the block's 16 code sums (int16 pairs)
             const uint32_t sw[8] = {s03.x, s03.y, s03.z, s03.w, s47.x, s47.y, s47.z, s47.w};
+            // the tile's integer totals over the four lane groups, one float step into
+            // acc[4 q]; acc[4 q + 1 .. 3] keep exact zeros (the decode dot's layout)
+            int isum = 0, msum = 0;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const uint32_t f = F[g];
@@ -741,10 +754,10 @@ struct TileQ4Quad {
                 const uint32_t s01 = sw[2 * g], s23 = sw[2 * g + 1];
                 const int s0 = static_cast<int16_t>(s01 & 0xFFFFu), s1 = static_cast<int16_t>(s01 >> 16);
                 const int s2 = static_cast<int16_t>(s23 & 0xFFFFu), s3 = static_cast<int16_t>(s23 >> 16);
-                const int isum = mul24(sca, dl[g]) + mul24(scb, dh[g]);
-                const int msum = mul24(ma, s0 + s1) + mul24(mb, s2 + s3);
-                acc[4 * q + g] = q4k_term(acc[4 * q + g], xd, d, dmin, isum, msum);
+                isum += mul24(sca, dl[g]) + mul24(scb, dh[g]);
+                msum += mul24(ma, s0 + s1) + mul24(mb, s2 + s3);
             }
+            acc[4 * q] = q4k_term(acc[4 * q], xd, d, dmin, isum, msum);
         }
     }
 };
@@ -1406,12 +1419,13 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
 // product is one GGML block (Q8_0), one sub-block (Q4_K), or, with the lane
 // groups of the other half zeroed, one 16-value sub-block (Q6_K, Q2_K). D
 // gives lane (i, G) the integer dots of row i with tokens 4 G + j for every
-// block, and the lane applies the decode matmul's scale arithmetic per
-// (tile, lane group, token) in the same order (q4k_term, q8_term, the Q6_K
-// scale sum). The min sums Σ m · (code sum) are exact integers below 2^24
-// and come from v_mfma_f32_16x16x4f32 as exact floats. Sums run over waves,
-// then lane groups, in the decode order: every row equals that row computed
-// alone, bit for bit.
+// block, and the lane applies the decode matmul's scale arithmetic in the
+// same order (Q4_K: q4k_term per (tile, token) on the tile's integer totals;
+// Q2_K q4k_term, Q8_0 q8_term and the Q6_K scale sum per (tile, lane group,
+// token)). The min sums Σ m · (code sum) are exact integers below 2^24 and
+// come from v_mfma_f32_16x16x4f32 as exact floats. Sums run over waves, then
+// lane groups, in the decode order: every row equals that row computed alone,
+// bit for bit.
 __device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) {
     return static_cast<long>(static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32));
 }
@@ -1475,6 +1489,11 @@ struct WideTile<11> {
         // row i's 24-bit fields sc 2g | sc 2g+1 | m 2g | m 2g+1 of the four lane groups
         const uint32_t F[4] = {w.hdr.y & 0xFFFFFFu, (w.hdr.y >> 24) | ((w.hdr.z & 0xFFFFu) << 8),
                                (w.hdr.z >> 16) | ((w.hdr.w & 0xFFu) << 16), w.hdr.w >> 8};
+        // the tile's totals over the four lane groups: integer dots, and the min
+        // sums accumulated on the f32 MFMA (exact integers below 2^24); one float
+        // step per token into acc[0], acc[1 .. 3] keep exact zeros (the decode dot's order)
+        int isum[4] = {0, 0, 0, 0};
+        f32x4 ms = {0.0F, 0.0F, 0.0F, 0.0F};
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const uint32_t f = F[g];
@@ -1484,13 +1503,12 @@ struct WideTile<11> {
             const long hi = pack2((c.x >> 4) & 0x0F0F0F0Fu, (c.y >> 4) & 0x0F0F0F0Fu);
             const i32x4 da = mfma_i8(av[2 * g], lo), db = mfma_i8(av[2 * g + 1], hi);
             const float mB = G < 2 ? static_cast<float>((f >> (12 + 6 * G)) & 63u) : 0.0F;
-            const f32x4 ms = mfma_f32k4(x.s[g], mB);
+            ms = __builtin_amdgcn_mfma_f32_16x16x4f32(x.s[g], mB, ms, 0, 0, 0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int isum = mul24(sca, da[j]) + mul24(scb, db[j]);
-                acc[g][j] = q4k_term_f(acc[g][j], xd[j], d, dmin, isum, ms[j]);
-            }
+            for (int j = 0; j < 4; ++j) isum[j] += mul24(sca, da[j]) + mul24(scb, db[j]);
         }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[0][j] = q4k_term_f(acc[0][j], xd[j], d, dmin, isum[j], ms[j]);
     }
 };
 
