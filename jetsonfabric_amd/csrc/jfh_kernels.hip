@@ -457,11 +457,12 @@ __device__ __forceinline__ int mul24(int a, int b) { return __mul24(a, b); }
 template <uint32_t TYPE>
 struct Tile;
 
-// The float step of a K-quant tile for one token: acc + xd * (d * isum -
-// dmin * msum), with the fused products as written. Q4_K applies it once per
-// tile to the integer totals over all eight sub-blocks (GGML's super-block
-// sums, ggml_vec_dot_q4_K_q8_K), Q2_K once per lane group; the decode, token
-// quad and wide matmuls all use it, so they round alike.
+// The float step of a Q4_K / Q2_K tile for one token: acc + xd * (d * isum -
+// dmin * msum), with the fused products as written, applied once per tile to
+// the integer totals over all of the tile's sub-blocks (GGML's super-block
+// sums, ggml_vec_dot_q4_K_q8_K / _q2_K_q8_K; Q6_K likewise sums sc * dot over
+// its sixteen sub-blocks before its one step). The decode, token quad and wide
+// matmuls all use it, so they round alike.
 __device__ __forceinline__ float q4k_term(float acc, float xd, float d, float dmin, int isum, int msum) {
     const float t = __builtin_fmaf(d, static_cast<float>(isum), -(dmin * static_cast<float>(msum)));
     return __builtin_fmaf(xd, t, acc);
@@ -584,7 +585,11 @@ struct Tile<13> {
                     for (int q = 0; q < 4; ++q) dm = sdot4(w[4 * m + q], xw[4 * m + q], dm);
                     isum += mul24(sc[m], dm - 32 * s[m]);
                 }
-                acc[t] = __builtin_fmaf(x.d[tc * x.d_stride], d * static_cast<float>(isum), acc[t]);
+                // the tile's integer total over the four lane groups; lane group 0
+                // takes the float step, the others keep exact zeros
+                isum += __shfl_xor(isum, 16);
+                isum += __shfl_xor(isum, 32);
+                if (g == 0) acc[t] = __builtin_fmaf(x.d[tc * x.d_stride], d * static_cast<float>(isum), acc[t]);
             }
         }
     }
@@ -672,7 +677,13 @@ struct Tile<9> {
                     isum += mul24(sc[m], dm);
                     msum += mul24(mn[m], s[m]);
                 }
-                acc[t] = q4k_term(acc[t], x.d[tc * x.d_stride], d, dmin, isum, msum);
+                // the tile's integer totals over the four lane groups; lane group 0
+                // takes the float step, the others keep exact zeros
+                isum += __shfl_xor(isum, 16);
+                isum += __shfl_xor(isum, 32);
+                msum += __shfl_xor(msum, 16);
+                msum += __shfl_xor(msum, 32);
+                if (g == 0) acc[t] = q4k_term(acc[t], x.d[tc * x.d_stride], d, dmin, isum, msum);
             }
         }
     }
@@ -826,13 +837,14 @@ struct TileQ6Quad {
             }
             const int tk = min(4 * q + L, nt - 1);
             const float xd = x.d[tk * x.d_stride];
+            // the tile's integer total over the four lane groups, one float step into acc[4 q]
+            int isum = 0;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                int isum = 0;
 #pragma unroll
                 for (int m = 0; m < 4; ++m) isum += mul24(sext8(scw[g] >> (8 * m)), D[m][g]);
-                acc[4 * q + g] = __builtin_fmaf(xd, d * static_cast<float>(isum), acc[4 * q + g]);
             }
+            acc[4 * q] = __builtin_fmaf(xd, d * static_cast<float>(isum), acc[4 * q]);
         }
     }
 };
@@ -950,9 +962,10 @@ struct TileQ2Quad {
             const u32x4* sp = reinterpret_cast<const u32x4*>(x.s + tk * x.s_stride);
             const u32x4 s03 = sp[0], s47 = sp[1];
             const uint32_t sw[8] = {s03.x, s03.y, s03.z, s03.w, s47.x, s47.y, s47.z, s47.w};
+            // the tile's integer totals over the four lane groups, one float step into acc[4 q]
+            int isum = 0, msum = 0;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                int isum = 0, msum = 0;
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
                     const int j = 4 * g + m;  // sub-block of the block
@@ -961,8 +974,8 @@ struct TileQ2Quad {
                     isum += mul24(static_cast<int>(byte & 0xF), D[m][g]);
                     msum += mul24(static_cast<int>((byte >> 4) & 0xF), sj);
                 }
-                acc[4 * q + g] = q4k_term(acc[4 * q + g], xd, d, dmin, isum, msum);
             }
+            acc[4 * q] = q4k_term(acc[4 * q], xd, d, dmin, isum, msum);
         }
     }
 };
@@ -1420,9 +1433,9 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
 // groups of the other half zeroed, one 16-value sub-block (Q6_K, Q2_K). D
 // gives lane (i, G) the integer dots of row i with tokens 4 G + j for every
 // block, and the lane applies the decode matmul's scale arithmetic in the
-// same order (Q4_K: q4k_term per (tile, token) on the tile's integer totals;
-// Q2_K q4k_term, Q8_0 q8_term and the Q6_K scale sum per (tile, lane group,
-// token)). The min sums Σ m · (code sum) are exact integers below 2^24 and
+// same order (Q4_K and Q2_K: q4k_term per (tile, token) on the tile's
+// integer totals, Q6_K one step on its integer scale sum; Q8_0 q8_term per
+// (tile, lane group, token)). The min sums Σ m · (code sum) are exact integers below 2^24 and
 // come from v_mfma_f32_16x16x4f32 as exact floats. Sums run over waves, then
 // lane groups, in the decode order: every row equals that row computed alone,
 // bit for bit.
@@ -1434,10 +1447,6 @@ __device__ __forceinline__ i32x4 mfma_i8(long a, long b) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, i32x4{0, 0, 0, 0}, 0, 0, 0);
 }
 
-// D[token][row] = sum over the 4 lane groups k of A[token][k] * B[k][row]
-__device__ __forceinline__ f32x4 mfma_f32k4(float a, float b) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, f32x4{0.0F, 0.0F, 0.0F, 0.0F}, 0, 0, 0);
-}
 
 // q4k_term with the min sum given as the float of that integer
 __device__ __forceinline__ float q4k_term_f(float acc, float xd, float d, float dmin, int isum, float msum) {
@@ -1584,6 +1593,7 @@ struct WideTile<13> {
         const uint32_t SC[4] = {w.sc.x, w.sc.y, w.sc.z, w.sc.w};
         const int hshift = (G & 1) ? 0 : 4;
         const bool low = G < 2;  // lane groups 0, 1: the stretch's first sub-block
+        int isum[4] = {0, 0, 0, 0};  // the tile's integer totals over the lane groups, per token
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             i32x4 dm[4];
@@ -1603,12 +1613,13 @@ struct WideTile<13> {
             for (int m = 0; m < 4; ++m) sc[m] = sext8(SC[g] >> (8 * m));
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                int isum = 0;
 #pragma unroll
-                for (int m = 0; m < 4; ++m) isum += mul24(sc[m], dm[m][j]);
-                acc[g][j] = __builtin_fmaf(xd[j], d * static_cast<float>(isum), acc[g][j]);
+                for (int m = 0; m < 4; ++m) isum[j] += mul24(sc[m], dm[m][j]);
             }
         }
+        // one float step per token into acc[0]; acc[1 .. 3] keep exact zeros
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[0][j] = __builtin_fmaf(xd[j], d * static_cast<float>(isum[j]), acc[0][j]);
     }
 };
 
@@ -1650,6 +1661,10 @@ struct WideTile<9> {
         const uint32_t SC[4] = {w.sc.x, w.sc.y, w.sc.z, w.sc.w};
         const int qshift = 4 * (G & 1);
         const bool low = G < 2;
+        // the tile's totals over the lane groups: integer dots, and the min sums
+        // accumulated on the f32 MFMA (exact integers below 2^24)
+        int isum[4] = {0, 0, 0, 0};
+        f32x4 ms = {0.0F, 0.0F, 0.0F, 0.0F};
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             i32x4 dm[4];
@@ -1660,18 +1675,20 @@ struct WideTile<9> {
                 dm[2 * e] = mfma_i8(av[2 * g + e], low ? B : 0L);
                 dm[2 * e + 1] = mfma_i8(av[2 * g + e], low ? 0L : B);
             }
-            const f32x4 ms = mfma_f32k4(x.s[g], static_cast<float>((SC[g] >> (8 * G + 4)) & 0xFu));
+            ms = __builtin_amdgcn_mfma_f32_16x16x4f32(x.s[g], static_cast<float>((SC[g] >> (8 * G + 4)) & 0xFu), ms, 0,
+                                                      0, 0);
             int sc[4];
 #pragma unroll
             for (int m = 0; m < 4; ++m) sc[m] = (SC[g] >> (8 * m)) & 0xF;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                int isum = 0;
 #pragma unroll
-                for (int m = 0; m < 4; ++m) isum += mul24(sc[m], dm[m][j]);
-                acc[g][j] = q4k_term_f(acc[g][j], xd[j], d, dmin, isum, ms[j]);
+                for (int m = 0; m < 4; ++m) isum[j] += mul24(sc[m], dm[m][j]);
             }
         }
+        // one float step per token into acc[0]; acc[1 .. 3] keep exact zeros
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[0][j] = q4k_term_f(acc[0][j], xd[j], d, dmin, isum[j], ms[j]);
     }
 };
 
