@@ -1863,6 +1863,132 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide(GemvArgs a, int32_t n_rg
     }
 }
 
+// The wide matmul of the K-quant formats (Q4_K, Q6_K, Q2_K, whose tiles keep
+// one accumulator per (row, token): the integer totals of a tile take one
+// float step) over R consecutive 16-row groups per work-group: a wave loads
+// its K tile's activations once for the group's token tiles and runs them
+// against the R row groups' weight tiles (the next row group's tile in flight
+// while the current one is multiplied), so the activation rows are read from
+// L2 once per R row groups instead of once per row group. Per (row, token) the
+// sum is the one-row-group kernel's: each wave's tiles in K order, the waves
+// in order (the lane groups' other accumulators are exact zeros, and adding
+// them to a sum that starts at +0 changes no bit), so rows stay bit-identical
+// to decode rows.
+template <uint32_t TYPE, int R, int TP>
+__global__ __launch_bounds__(kMmThreads) void k_mm_wide_rg(GemvArgs a, int32_t n_rg, int32_t tpw) {
+    using T = WideTile<TYPE>;
+    constexpr int W = kMmWaves;
+    constexpr uint32_t TB = tile_bytes(TYPE);
+    __shared__ float red[W][TP][16][16];  // [wave][token tile][token][row] of one row group
+    __shared__ float vals[kWideRows][16 * R];
+    __shared__ u32x4 stage_s[W][TP][16][2];
+    __shared__ float stage_d[W][TP][16];
+    const int n_tok = a.n_tok, n_tt = (n_tok + 15) / 16, n_grp = (n_tt + tpw - 1) / tpw;
+    // work-group k runs on XCD k % 8: the token groups of one row-group set share an XCD (and its L2)
+    const int q = static_cast<int>(blockIdx.x) >> 3;
+    const int grp = q % n_grp, set = (q / n_grp) * 8 + static_cast<int>(blockIdx.x & 7u);
+    const int rg0 = set * R;
+    if (rg0 >= n_rg) return;
+    const int nrg = min(R, n_rg - rg0);
+    const int K = static_cast<int>(a.mat.cols), nb = K / 256;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+    const int i = lane & 15, G = lane >> 4;
+    const int tt0 = grp * tpw, ntl = min(TP, min(n_tt, tt0 + tpw) - tt0);
+    const int t0 = 16 * tt0, nt = min(16 * (tt0 + ntl), n_tok) - t0;
+    const GemvArgs out = token_slice(a, t0, nt);
+    const Act8 xq = a.xq;
+    auto load_act = [&](int tt, int b) {
+        // token rows past the step repeat its last row; their sums are never stored
+        const size_t tok = static_cast<size_t>(min(16 * tt + i, n_tok - 1));
+        WideAct r;
+        const uint4* xa = reinterpret_cast<const uint4*>(xq.q + tok * K + b * 256 + 64 * G);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) r.xa[u] = xa[u];
+        const int tl = lane < 32 ? lane >> 1 : lane - 32;
+        const size_t tk = static_cast<size_t>(min(16 * tt + (tl & 15), n_tok - 1));
+        if (lane >= 32) r.st.x = __float_as_uint(xq.d[tk * nb + b]);
+        else if (T::kSums) r.st = reinterpret_cast<const u32x4*>(xq.s + tk * (K / 16) + 16 * b)[lane & 1];
+        return r;
+    };
+    const uint8_t* base = a.mat.data + static_cast<size_t>(rg0) * nb * TB;
+    float acc[R][TP][4][4];
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+#pragma unroll
+        for (int tl = 0; tl < TP; ++tl) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[rr][tl][g][j] = 0.0F;
+            }
+        }
+    }
+    for (int b = wave; b < nb; b += W) {
+        // the first row group's tile, then the token tiles' activations (clamped: issued unconditionally)
+        typename T::Wt w = T::load_w(base + static_cast<size_t>(b) * TB, i, G);
+        long av[TP][8];
+        float xd[TP][4];
+        typename T::Xt x[TP];
+#pragma unroll
+        for (int tl = 0; tl < TP; ++tl) {
+            const WideAct r = load_act(tt0 + min(tl, ntl - 1), b);
+            if (lane < 32) {
+                if (T::kSums) stage_s[wave][tl][lane >> 1][lane & 1] = r.st;
+            } else if (lane < 48) {
+                stage_d[wave][tl][lane - 32] = __uint_as_float(r.st.x);
+            }
+            wide_a_operands(r.xa, av[tl]);
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int tl = 0; tl < TP; ++tl) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xd[tl][j] = stage_d[wave][tl][4 * G + j];
+            x[tl] = T::load_x(reinterpret_cast<const uint32_t*>(&stage_s[wave][tl][i][0]), G);
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) {
+            // the next row group's tile (clamped to the group's last) is requested before this one runs
+            const typename T::Wt wn =
+                T::load_w(base + (static_cast<size_t>(min(rr + 1, nrg - 1)) * nb + b) * TB, i, G);
+            if (rr < nrg) {
+#pragma unroll
+                for (int tl = 0; tl < TP; ++tl) {
+                    if (tl < ntl) T::accumulate(w, av[tl], x[tl], xd[tl], G, acc[rr][tl]);
+                }
+            }
+            w = wn;
+        }
+    }
+    // per row group and token tile: the sum over waves in wave order
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+        if (rr < nrg) {
+            __syncthreads();
+#pragma unroll
+            for (int tl = 0; tl < TP; ++tl) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) red[wave][tl][4 * G + j][i] = acc[rr][tl][0][j];
+            }
+            __syncthreads();
+            for (int e = threadIdx.x; e < ntl * 256; e += kMmThreads) {
+                const int tl = e >> 8, tk = (e >> 4) & 15, r = e & 15;
+                float v = 0.0F;
+#pragma unroll
+                for (int w2 = 0; w2 < W; ++w2) v += red[w2][tl][tk][r];
+                vals[16 * tl + tk][16 * rr + r] = v;
+            }
+        }
+    }
+    __syncthreads();
+    const int row0 = rg0 * 16;
+    const int nrows = min(16 * nrg, static_cast<int>(a.mat.rows) - row0);
+    gemv_epilogue<kMmThreads, kNoLogits>(out, row0, nrows, [&](int j, int t) { return vals[t][j]; },
+                                         &red[0][0][0][0]);
+}
+
 // Float weights (F32/F16, small models): one wave per row, lanes over K,
 // float activations (RMS-normalized in the prologue when a gain is given).
 constexpr int kFloatThreads = 256;
@@ -2786,6 +2912,7 @@ void launch_quantize_norm(const float* x, int32_t stride, const int32_t* gather,
 #define JFH_WIDE_MIN_WGS 512
 #endif
 constexpr int kWideMinWgs = JFH_WIDE_MIN_WGS;
+constexpr int kWideRgMinWgs = 256;  // one work-group per CU
 #ifndef JFH_WIDE_LOGITS_WGS
 #define JFH_WIDE_LOGITS_WGS 1024
 #endif
@@ -2822,11 +2949,32 @@ void launch_gemv_wide(const GemvArgs& a, hipStream_t stream) {
     // as many token tiles per work-group as still leave kWideMinWgs work-groups
     int tpw = min(n_tt, kWideTpw);
     while (tpw > 1 && n_rg * ((n_tt + tpw - 1) / tpw) < kWideMinWgs) --tpw;
+    const bool merged = a.mode == kLogits;  // the head kernel: the only one with the argmax epilogue
+    // K-quant layer matrices: one token tile and several row groups per work-group, every
+    // activation load shared by the row groups: four (Q4_K only: the other formats'
+    // operands take the registers) while kWideMinWgs work-groups remain, else two while
+    // one work-group per CU remains (64-row chunks of 7B: gate_up 4, qkv, o and down 2)
+    if (!merged && a.mat.type != 7) {
+        int rgs = 1;
+        if (a.mat.type == 11 && (n_rg + 3) / 4 * n_tt >= kWideMinWgs) rgs = 4;
+        else if ((n_rg + 1) / 2 * n_tt >= kWideRgMinWgs) rgs = 2;
+        if (rgs > 1) {
+            const int tp1 = 1;
+            const dim3 g(((n_rg + rgs - 1) / rgs + 7) / 8 * 8 * n_tt), b(kMmThreads);
+            switch (a.mat.type * 8 + rgs) {
+            case 11 * 8 + 4: launch(k_mm_wide_rg<11, 4, 1>, g, b, 0, stream, a, n_rg, tp1); break;
+            case 11 * 8 + 2: launch(k_mm_wide_rg<11, 2, 1>, g, b, 0, stream, a, n_rg, tp1); break;
+            case 13 * 8 + 2: launch(k_mm_wide_rg<13, 2, 1>, g, b, 0, stream, a, n_rg, tp1); break;
+            default: launch(k_mm_wide_rg<9, 2, 1>, g, b, 0, stream, a, n_rg, tp1); break;
+            }
+            check(hipGetLastError(), "wide matmul launch");
+            return;
+        }
+    }
     // the head: row groups per work-group so that about kWideLogitsWgs work-groups merge their argmax
     const int rpw = a.mode == kLogits ? std::max(1, n_rg / kWideLogitsWgs) : 1;
     const int grid = (n_rg + 8 * rpw - 1) / (8 * rpw) * 8 * ((n_tt + tpw - 1) / tpw);
     const dim3 g(grid), b(kMmThreads);
-    const bool merged = a.mode == kLogits;  // the head kernel: the only one with the argmax epilogue
     switch (a.mat.type) {
     case 7:
         if (merged) launch(k_mm_wide<7, true>, g, b, 0, stream, a, n_rg, tpw, rpw);
