@@ -2120,19 +2120,18 @@ __device__ __forceinline__ int attn_split_len(int n_keys, int len, int splits_ma
     return L;
 }
 
-// A work-group whose key split lies beyond the sequence's last key writes the
-// empty partial (max -inf, sum 0, output 0) for its query rows, so that every
-// split slot below splits_max holds this step's value and the merge reads
-// them without consulting the step descriptor.
+// A work-group whose key split lies beyond the sequence's last key marks the
+// split empty (max -inf) for its query rows, so that every split slot below
+// splits_max holds this step's maximum and the merge reads the slots without
+// consulting the step descriptor (it ignores the sum and output of a split
+// whose maximum is -inf).
 template <int NTHR>
 __device__ __forceinline__ void attn_empty_split(float* partial, int q_begin, int nq, int G, int kvh, int row0,
                                                  int n_head, int hd, int splits_max, int split) {
-    for (int e = threadIdx.x; e < nq * (hd + 2); e += NTHR) {
-        const int i = e / (hd + 2), c = e - i * (hd + 2);
+    for (int i = threadIdx.x; i < nq; i += NTHR) {
         const int qi = q_begin + i;
         const int t = qi / G, head = kvh * G + qi % G;
-        partial[((static_cast<size_t>(row0 + t) * n_head + head) * splits_max + split) * (hd + 2) + c] =
-            c == 0 ? -INFINITY : 0.0F;
+        partial[((static_cast<size_t>(row0 + t) * n_head + head) * splits_max + split) * (hd + 2)] = -INFINITY;
     }
 }
 
@@ -2550,11 +2549,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_mfma(const float* __
 
 // Combines the split partials of every (row, head): one work-group per
 // (row, 256 output values); with xq set the 256 values are quantized into xq.
-// Every split slot below splits_max holds this step's partial (splits past a
-// sequence's last key hold the empty one), so the partials are requested at
-// the kernel's start, with no lookup of the step descriptor before them; an
-// empty split adds exactly zero, as a split beyond the last one did when the
-// merge skipped it.
+// Every split slot below splits_max holds this step's maximum (-inf for a
+// split past the sequence's last key), so the partials are requested at the
+// kernel's start, with no lookup of the step descriptor before them; a split
+// whose maximum is -inf adds exactly zero, as it did when the merge skipped
+// the splits past the last one.
 __global__ __launch_bounds__(256) void k_attention_merge(const float* __restrict__ partial, int32_t n_head,
                                                          int32_t hd, int32_t splits_max, float* __restrict__ out,
                                                          Act8 xq) {
@@ -2585,8 +2584,9 @@ __global__ __launch_bounds__(256) void k_attention_merge(const float* __restrict
 #pragma unroll
         for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
             const float f = pm[sp] == -INFINITY ? 0.0F : expf(pm[sp] - M);
-            total += f * pl[sp];
-            acc += f * po[sp];
+            // a split with maximum -inf adds nothing (its sum and output may be stale)
+            total += pm[sp] == -INFINITY ? 0.0F : f * pl[sp];
+            acc += pm[sp] == -INFINITY ? 0.0F : f * po[sp];
         }
         v = acc / total;
         out[static_cast<size_t>(row) * H + c] = v;
