@@ -3,6 +3,7 @@
 #include "jfh_runtime.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <condition_variable>
 #include <cstring>
@@ -878,12 +879,26 @@ namespace pipeline_parallel {
 // result and wakes everyone. A caller whose ticket is still open afterwards
 // leads or joins the next batch. Steps arriving while a batch runs queue for
 // the next one, so the GPU goes from one batched step to the next.
+// Both waits (an open ticket for its batch, a leader for its batch to fill)
+// first spin for up to kSpin on atomic copies of the state kept under the
+// lock, then block on the condition variable: a batched step is answered
+// within microseconds instead of a thread wake-up later, which the next step
+// of every sequence in the batch would wait for.
 struct ContinuousBatchingExecutor::Impl {
+    static constexpr auto kSpin = std::chrono::microseconds(2000);
     struct Ticket {
         const inference::StageInput* input = nullptr;
         inference::ExecutionResult result;
-        bool answered = false;
+        std::atomic<bool> answered{false};
     };
+
+    // spins until done() or kSpin (or the deadline) has passed; the caller
+    // re-checks its condition under the lock before blocking
+    template <typename Done>
+    static void spin(Done done, std::chrono::steady_clock::time_point deadline) {
+        deadline = std::min(deadline, std::chrono::steady_clock::now() + kSpin);
+        while (!done() && std::chrono::steady_clock::now() < deadline) std::this_thread::yield();
+    }
 
     std::unique_ptr<inference::Executor> delegate;
     ContinuousBatchingConfig config;
@@ -893,6 +908,9 @@ struct ContinuousBatchingExecutor::Impl {
     std::condition_variable changed;
     std::vector<Ticket*> arrived;  // steps no leader has taken yet, oldest first
     bool forming = false;          // a leader is gathering or running a batch
+    // copies of arrived.size() and forming, written under the lock, read while spinning
+    std::atomic<std::size_t> n_arrived{0};
+    std::atomic<bool> forming_now{false};
 
     Impl(std::unique_ptr<inference::Executor> d, ContinuousBatchingConfig c) : delegate(std::move(d)), config(c) {
         if (!delegate) throw std::invalid_argument("a continuous-batching executor needs a delegate executor");
@@ -932,26 +950,40 @@ struct ContinuousBatchingExecutor::Impl {
         mine.input = &input;
         std::unique_lock lock(state);
         arrived.push_back(&mine);
+        n_arrived.store(arrived.size(), std::memory_order_release);
         changed.notify_all();  // a gathering leader may now hold a full batch
-        while (!mine.answered) {
+        while (!mine.answered.load(std::memory_order_acquire)) {
             if (forming) {
-                changed.wait(lock);
+                lock.unlock();
+                spin([&] { return mine.answered.load(std::memory_order_acquire) ||
+                              !forming_now.load(std::memory_order_acquire); },
+                     std::chrono::steady_clock::time_point::max());
+                lock.lock();
+                if (!mine.answered.load(std::memory_order_acquire) && forming) changed.wait(lock);
                 continue;
             }
             forming = true;
-            changed.wait_until(lock, std::chrono::steady_clock::now() + config.max_wait,
-                               [this] { return arrived.size() >= config.max_batch_size; });
+            forming_now.store(true, std::memory_order_release);
+            const auto deadline = std::chrono::steady_clock::now() + config.max_wait;
+            if (arrived.size() < config.max_batch_size) {
+                lock.unlock();
+                spin([&] { return n_arrived.load(std::memory_order_acquire) >= config.max_batch_size; }, deadline);
+                lock.lock();
+            }
+            changed.wait_until(lock, deadline, [this] { return arrived.size() >= config.max_batch_size; });
             const std::size_t n = std::min(arrived.size(), config.max_batch_size);
             std::vector<Ticket*> taken(arrived.begin(), arrived.begin() + static_cast<std::ptrdiff_t>(n));
             arrived.erase(arrived.begin(), arrived.begin() + static_cast<std::ptrdiff_t>(n));
+            n_arrived.store(arrived.size(), std::memory_order_release);
             lock.unlock();
             std::vector<inference::ExecutionResult> results = run_batch(taken);
             lock.lock();
             for (std::size_t i = 0; i < n; ++i) {
                 taken[i]->result = std::move(results[i]);
-                taken[i]->answered = true;
+                taken[i]->answered.store(true, std::memory_order_release);
             }
             forming = false;
+            forming_now.store(false, std::memory_order_release);
             changed.notify_all();
         }
         return std::move(mine.result);
