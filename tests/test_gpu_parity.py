@@ -109,6 +109,45 @@ def test_wide_matmul_rows_equal_single_rows(typed, n_tok):
             assert np.array_equal(wide[r].view(np.uint32), single[0].view(np.uint32)), f"{name} row {r}"
 
 
+# A gate/up matrix of 8192 rows (512 row groups): 64-row steps run the wide
+# K-quant matmul with four row groups per work-group (Q4_K), 9..33-row steps and
+# the other K-quant formats with two.
+WIDE = jf.ModelConfig(n_layer=1, n_embd=512, n_ff=4096, n_head=8, n_head_kv=2, n_vocab=4096, n_ctx=256)
+KQUANTS = [jf.Q4_K, jf.Q6_K, jf.Q2_K]
+
+
+@pytest.fixture(scope="module", params=KQUANTS, ids=[jf.TYPE_NAMES[t] for t in KQUANTS])
+def wide_typed(request):
+    t = request.param
+    model = _model(WIDE, t, t, t, seed=40 + t)
+    engine = jf.NativeEngine(model)
+    yield t, model, engine
+    engine.close()
+
+
+def test_wide_matmul_over_row_group_sets_equals_single_rows(wide_typed):
+    """The wide matmul that shares each activation load between two or four
+    row groups per work-group: every row of a wide step (9, 17, 33 and 64 rows;
+    Q6_K and Q2_K run token quads below 17) equals the same row computed alone
+    (the decode path), bit for bit, and the step matches the oracle's matmul on
+    the same int8 rows."""
+    t, model, engine = wide_typed
+    name = "blk.0.ffn_gate.weight"
+    info = model.tensor(name)
+    cols, rows = info["shape"]
+    for n_tok in ([9] if t == jf.Q4_K else []) + [17, 33, 64]:
+        rng = np.random.default_rng(300 + n_tok)
+        x = rng.standard_normal((n_tok, cols)).astype(np.float32)
+        wide = engine.matmul(name, x, rows)
+        for r in range(n_tok):
+            single = engine.matmul(name, x[r:r + 1], rows)
+            assert np.array_equal(wide[r].view(np.uint32), single[0].view(np.uint32)), f"{n_tok} rows: row {r}"
+        ref = jo.matmul(t, info["data"], cols, rows, x, jo.MODE_Q8)
+        # identical int8 activations and integer dots; only f32 summation order differs
+        scale = np.abs(ref).max()
+        assert np.allclose(wide, ref, rtol=1e-4, atol=2e-5 * scale), f"{n_tok} rows: max err {np.abs(wide - ref).max():.3e}"
+
+
 def test_tiny_fixture_known_answer():
     cfg = jf.ModelConfig(**tiny_fixture.CONFIG)
     model = jf.Model.build(cfg, tiny_fixture.tensors())
