@@ -486,6 +486,7 @@ void Engine::ensure_capacity(uint32_t capacity) {
     hip_check(hipMalloc(&rope_, table.size() * sizeof(float)), "allocate rope table");
     hip_check(hipMemcpy(rope_, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice), "upload rope table");
     splits_ = gpu::attention_splits(static_cast<int32_t>(cap));
+    attn_capacity_ = static_cast<int32_t>(cap);
     const size_t partial_floats = gpu::attention_partial_floats(gpu::kMaxRows, static_cast<int32_t>(p.n_head),
                                                                 static_cast<int32_t>(p.head_dim), splits_);
     if (partial_) (void) hipFree(partial_);
@@ -609,6 +610,8 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
             a.x = {h_, H, nullptr, gain, p.rms_eps};
         }
     };
+    // attention split slots this step shape can fill (a prefill chunk: few long splits)
+    const int32_t slots = gpu::attention_slots(splits_, attn_capacity_, n_rows, n_seq);
     // l: the resident layer (its slot in the sessions' caches)
     for (uint32_t l = 0; l < layers_.size(); ++l) {
         const Layer& L = layers_[l];
@@ -627,11 +630,12 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         matmul(qkv, "qkv");
         timed("k_attention", attn_kv_bytes_ + n * Hq * 4.0, [&] {
             gpu::launch_attention(q_, step_dev_, max_len, n_seq, static_cast<int32_t>(l), static_cast<int32_t>(p.n_head),
-                                  static_cast<int32_t>(p.n_head_kv), static_cast<int32_t>(p.head_dim), splits_, partial_, s);
+                                  static_cast<int32_t>(p.n_head_kv), static_cast<int32_t>(p.head_dim), splits_, partial_, s,
+                                  slots);
         });
-        timed("k_attention_merge", n * Hq * 4.0 * (splits_ + 1.0) + (xq_attn_.q ? n * Hq * 1.1 : 0.0), [&] {
+        timed("k_attention_merge", n * Hq * 4.0 * (slots + 1.0) + (xq_attn_.q ? n * Hq * 1.1 : 0.0), [&] {
             gpu::launch_attention_merge(partial_, step_dev_, n_rows, static_cast<int32_t>(p.n_head),
-                                        static_cast<int32_t>(p.head_dim), splits_, attn_, xq_attn_, s);
+                                        static_cast<int32_t>(p.head_dim), splits_, attn_, xq_attn_, s, slots);
         });
         gpu::GemvArgs o;
         o.mat = L.o->mat;

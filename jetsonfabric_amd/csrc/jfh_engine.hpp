@@ -232,6 +232,7 @@ private:
     float* rope_ = nullptr;
     uint32_t capacity_max_ = 0;
     int32_t splits_ = 0;
+    int32_t attn_capacity_ = 0;  // the positions the rope table and attention splits are sized for
     // int8 staging copies of the attention output and the SwiGLU output
     // (set when the consuming matrix is quantized)
     gpu::Act8 xq_attn_;

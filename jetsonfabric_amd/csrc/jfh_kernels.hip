@@ -2549,14 +2549,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_mfma(const float* __
 
 // Combines the split partials of every (row, head): one work-group per
 // (row, 256 output values); with xq set the 256 values are quantized into xq.
-// Every split slot below splits_max holds this step's maximum (-inf for a
-// split past the sequence's last key), so the partials are requested at the
-// kernel's start, with no lookup of the step descriptor before them; a split
-// whose maximum is -inf adds exactly zero, as it did when the merge skipped
-// the splits past the last one.
+// Every split slot below n_slots (the attention grid's splits) holds this
+// step's maximum (-inf for a split past the sequence's last key), so the
+// partials are requested at the kernel's start, with no lookup of the step
+// descriptor before them; a split whose maximum is -inf adds exactly zero, as
+// it did when the merge skipped the splits past the last one.
+template <int MAXS>
 __global__ __launch_bounds__(256) void k_attention_merge(const float* __restrict__ partial, int32_t n_head,
-                                                         int32_t hd, int32_t splits_max, float* __restrict__ out,
-                                                         Act8 xq) {
+                                                         int32_t hd, int32_t splits_max, int32_t n_slots,
+                                                         float* __restrict__ out, Act8 xq) {
     __shared__ float vals[256];
     const int row = blockIdx.y, H = n_head * hd;
     const int c = blockIdx.x * 256 + threadIdx.x;
@@ -2565,24 +2566,25 @@ __global__ __launch_bounds__(256) void k_attention_merge(const float* __restrict
         const int head = c / hd, dcol = c - head * hd;
         const float* base = partial + (static_cast<size_t>(row) * n_head + head) * splits_max * (hd + 2);
         // every split's (max, sum, value) requested at once
-        float pm[kAttnMaxSplits], pl[kAttnMaxSplits], po[kAttnMaxSplits];
+        float pm[MAXS], pl[MAXS], po[MAXS];
 #pragma unroll
-        for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
-            const float* p = base + min(sp, splits_max - 1) * (hd + 2);
-            pm[sp] = p[0];
-            pl[sp] = p[1];
+        for (int sp = 0; sp < MAXS; ++sp) {
+            const float* p = base + min(sp, n_slots - 1) * (hd + 2);
+            const float2 ml = *reinterpret_cast<const float2*>(p);  // hd + 2 is even: 8-byte aligned
+            pm[sp] = ml.x;
+            pl[sp] = ml.y;
             po[sp] = p[2 + dcol];
         }
 #pragma unroll
-        for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
-            if (sp >= splits_max) pm[sp] = -INFINITY;
+        for (int sp = 0; sp < MAXS; ++sp) {
+            if (sp >= n_slots) pm[sp] = -INFINITY;
         }
         float M = -INFINITY;
 #pragma unroll
-        for (int sp = 0; sp < kAttnMaxSplits; ++sp) M = fmaxf(M, pm[sp]);
+        for (int sp = 0; sp < MAXS; ++sp) M = fmaxf(M, pm[sp]);
         float total = 0.0F, acc = 0.0F;
 #pragma unroll
-        for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
+        for (int sp = 0; sp < MAXS; ++sp) {
             const float f = pm[sp] == -INFINITY ? 0.0F : expf(pm[sp] - M);
             // a split with maximum -inf adds nothing (its sum and output may be stale)
             total += pm[sp] == -INFINITY ? 0.0F : f * pl[sp];
@@ -3017,9 +3019,16 @@ size_t attention_partial_floats(int32_t rows, int32_t n_head, int32_t head_dim, 
     return static_cast<size_t>(rows) * n_head * splits * (head_dim + 2);
 }
 
+int32_t attention_slots(int32_t splits, int32_t capacity, int32_t n_rows, int32_t n_seq) {
+    if (n_seq != 1 || n_rows <= kQuadGroupRows || JFH_ATTN_PREFILL_KEYS <= 0) return splits;
+    return std::max(1, std::min(splits, (capacity + JFH_ATTN_PREFILL_KEYS - 1) / JFH_ATTN_PREFILL_KEYS));
+}
+
 void launch_attention(const float* q, const StepDev* step, int32_t max_len, int32_t n_seq, int32_t layer,
                       int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t splits, float* partial,
-                      hipStream_t stream) {
+                      hipStream_t stream, int32_t slots) {
+    if (slots <= 0) slots = splits;
+    if (slots > splits) throw std::invalid_argument("attention slots exceed the split stride");
     const int G = n_head / n_head_kv;
     if (head_dim > 2 * kWave || head_dim % 4 != 0) {
         throw std::invalid_argument("attention supports head dims that are multiples of 4 up to 128");
@@ -3031,7 +3040,7 @@ void launch_attention(const float* q, const StepDev* step, int32_t max_len, int3
     if (G * max_len > attention_max_rows(head_dim)) {
         throw std::invalid_argument("attention step has too many query rows per kv head");
     }
-    dim3 grid(splits, n_head_kv * qgroups, n_seq), block(kAttnThreads);
+    dim3 grid(slots, n_head_kv * qgroups, n_seq), block(kAttnThreads);
     if (head_dim == 128) {
         launch(k_attention_mfma<128>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, splits, qgroups,
                partial);
@@ -3046,12 +3055,26 @@ void launch_attention(const float* q, const StepDev* step, int32_t max_len, int3
 }
 
 void launch_attention_merge(const float* partial, const StepDev* step, int32_t n_rows, int32_t n_head,
-                            int32_t head_dim, int32_t splits, float* out, const Act8& xq, hipStream_t stream) {
+                            int32_t head_dim, int32_t splits, float* out, const Act8& xq, hipStream_t stream,
+                            int32_t slots) {
+    if (slots <= 0) slots = splits;
+    if (slots > splits) throw std::invalid_argument("attention slots exceed the split stride");
     const int H = n_head * head_dim;
     if (xq.q != nullptr && (H % 256 != 0 || xq.K != H)) throw std::invalid_argument("merge quantization shape mismatch");
     dim3 grid((H + 255) / 256, n_rows);
     (void) step;
-    launch(k_attention_merge, grid, dim3(256), 0, stream, partial, n_head, head_dim, splits, out, xq);
+    // the merge requests MAXS >= slots partials per value at once (MAXS a multiple of 4)
+    static_assert(kAttnMaxSplits == 32, "merge instantiations");
+    switch ((slots + 3) / 4) {
+    case 1: launch(k_attention_merge<4>, grid, dim3(256), 0, stream, partial, n_head, head_dim, splits, slots, out, xq); break;
+    case 2: launch(k_attention_merge<8>, grid, dim3(256), 0, stream, partial, n_head, head_dim, splits, slots, out, xq); break;
+    case 3: launch(k_attention_merge<12>, grid, dim3(256), 0, stream, partial, n_head, head_dim, splits, slots, out, xq); break;
+    case 4: launch(k_attention_merge<16>, grid, dim3(256), 0, stream, partial, n_head, head_dim, splits, slots, out, xq); break;
+    case 5: launch(k_attention_merge<20>, grid, dim3(256), 0, stream, partial, n_head, head_dim, splits, slots, out, xq); break;
+    case 6: launch(k_attention_merge<24>, grid, dim3(256), 0, stream, partial, n_head, head_dim, splits, slots, out, xq); break;
+    case 7: launch(k_attention_merge<28>, grid, dim3(256), 0, stream, partial, n_head, head_dim, splits, slots, out, xq); break;
+    default: launch(k_attention_merge<32>, grid, dim3(256), 0, stream, partial, n_head, head_dim, splits, slots, out, xq); break;
+    }
     check(hipGetLastError(), "attention merge launch");
 }
 

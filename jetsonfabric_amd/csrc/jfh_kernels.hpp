@@ -183,15 +183,26 @@ int32_t wide_min_rows(uint32_t type);
 void launch_gemv_wide(const GemvArgs& a, hipStream_t stream);
 // Split-K causal GQA flash attention over the f16 caches of the step's
 // sequences. Every (row, head, split) writes its (max, sum, unnormalized
-// output) to `partial`; launch_attention_merge combines the splits.
+// output) to `partial` (split stride `splits`); launch_attention_merge
+// combines the splits. `slots` (0: splits) is the number of split slots the
+// step can fill, and the grid's: every split of every sequence must fall below
+// it (attention_slots).
 void launch_attention(const float* q, const StepDev* step, int32_t max_len, int32_t n_seq, int32_t layer,
                       int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t splits, float* partial,
-                      hipStream_t stream);
+                      hipStream_t stream, int32_t slots = 0);
 // Merges the splits of every (row, head) into out[row][n_head * head_dim]
-// and, when xq.q is set, quantizes the rows into xq.
+// and, when xq.q is set, quantizes the rows into xq; reads the first `slots`
+// (0: splits) split slots.
 void launch_attention_merge(const float* partial, const StepDev* step, int32_t n_rows, int32_t n_head,
-                            int32_t head_dim, int32_t splits, float* out, const Act8& xq, hipStream_t stream);
+                            int32_t head_dim, int32_t splits, float* out, const Act8& xq, hipStream_t stream,
+                            int32_t slots = 0);
 int32_t attention_splits(int32_t capacity);
+// Split slots a step can fill: all `splits` when a sequence of the step may
+// bring kQuadGroupRows rows or fewer (the decode rule: about n_keys / splits
+// keys per split); a single sequence of more rows (a prefill chunk) splits
+// its keys into splits of at least the prefill length, so at most
+// ceil(capacity / prefill length) of them.
+int32_t attention_slots(int32_t splits, int32_t capacity, int32_t n_rows, int32_t n_seq);
 // Query rows (G heads x tokens) one sequence may bring to a step per kv head.
 int32_t attention_max_rows(int32_t head_dim);
 // Floats of the attention split scratch for `rows` token rows.
