@@ -343,20 +343,19 @@ __device__ __forceinline__ void stage_f32(const XIn& x, int n_tok, int c0, int n
 
 // After stage_f32 with a gain over the whole row (nb blocks): rs = 1/sqrt(
 // sum(x^2)/K + eps) per token (block sums added in block order) scales the
-// token's block scales (qwen2_architecture.cpp:373-376).
+// token's block scales (qwen2_architecture.cpp:373-376). Every thread that
+// scales a block computes its token's rs itself (the same sums in the same
+// order), so one barrier separates the staging from the scaling and the
+// matmul's own barrier the scaling from the first dot.
 template <int NTHR>
-__device__ void finish_norm(int n_tok, int nb, int K, float eps, const float* ssq, float* sd, float* rs, int chunk) {
-    __syncthreads();
-    if (threadIdx.x < static_cast<unsigned>(n_tok)) {
-        const int t = threadIdx.x;
-        float sum = 0.0F;
-        for (int b = 0; b < nb; ++b) sum += ssq[t * nb + b];
-        rs[t] = 1.0F / sqrtf(sum / static_cast<float>(K) + eps);
-    }
+__device__ void finish_norm(int n_tok, int nb, int K, float eps, const float* ssq, float* sd, int chunk) {
     __syncthreads();
     for (int i = threadIdx.x; i < n_tok * nb; i += NTHR) {
         const int t = i / nb, b = i - t * nb;
-        sd[t * (chunk / 256) + b] = sd[t * (chunk / 256) + b] * rs[t];
+        float sum = 0.0F;
+        for (int c = 0; c < nb; ++c) sum += ssq[t * nb + c];
+        const float rs = 1.0F / sqrtf(sum / static_cast<float>(K) + eps);
+        sd[t * (chunk / 256) + b] = sd[t * (chunk / 256) + b] * rs;
     }
 }
 #pragma clang fp contract(on)
@@ -1298,7 +1297,7 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
         stage_act8<kMmThreads>(a.xq, n_tok, 0, nbcur, sq, sd, ss, chunk, q0);
     } else {
         stage_f32<kMmThreads, NB, GAIN>(a.x, n_tok, 0, nbcur, sq, sd, ss, ssq, chunk, f0);
-        if constexpr (GAIN) finish_norm<kMmThreads>(n_tok, nbcur, K, a.x.eps, ssq, sd, rs, chunk);
+        if constexpr (GAIN) finish_norm<kMmThreads>(n_tok, nbcur, K, a.x.eps, ssq, sd, chunk);
     }
 
     for (int c0b = 0;;) {
