@@ -12,16 +12,10 @@ namespace {
 // Token rows up to which matmuls normalize their input in the prologue (from
 // 3 rows on, the rows are normalized and quantized once, as the token-quad
 // matrix-core path takes int8 rows).
-#ifndef JFH_NORMED_PROLOGUE_ROWS
-#define JFH_NORMED_PROLOGUE_ROWS 2
-#endif
-constexpr int32_t kNormedPrologueRows = JFH_NORMED_PROLOGUE_ROWS;
+constexpr int32_t kNormedPrologueRows = 2;
 
 // Logits rows from which the head runs in the wide matmul (below: token quads).
-#ifndef JFH_WIDE_HEAD_FROM_ROWS
-#define JFH_WIDE_HEAD_FROM_ROWS (gpu::kQuadGroupRows + 1)
-#endif
-constexpr int32_t kWideHeadFromRows = JFH_WIDE_HEAD_FROM_ROWS;
+constexpr int32_t kWideHeadFromRows = gpu::kQuadGroupRows + 1;
 
 void hip_check(hipError_t e, const char* what) {
     if (e != hipSuccess) throw Error(Status::DeviceError, std::string(what) + ": " + hipGetErrorString(e));
@@ -441,18 +435,20 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
     best_ = static_cast<unsigned long long*>(device_alloc(R * sizeof(unsigned long long)));
     // argmax slots start cleared; k_embed and k_finish clear them for every step
     hip_check(hipMemset(best_, 0, R * sizeof(unsigned long long)), "clear argmax slots");
-    auto act8 = [&](int32_t K) {
+    // int8 rows with room for the scales of 32-value blocks (the block size is the consumer's)
+    auto act8 = [&](int32_t K, int32_t blk) {
         gpu::Act8 a;
         a.K = K;
+        a.blk = blk;
         a.q = static_cast<int8_t*>(device_alloc(R * K));
-        a.d = static_cast<float*>(device_alloc(R * (K / 256) * sizeof(float)));
+        a.d = static_cast<float*>(device_alloc(R * (K / gpu::kActBlock32) * sizeof(float)));
         a.s = static_cast<int16_t*>(device_alloc(R * (K / 16) * sizeof(int16_t)));
         return a;
     };
-    if (quantized(layers_[0].o->mat.type) && Hq % 256 == 0) xq_attn_ = act8(Hq);
-    if (quantized(layers_[0].down->mat.type) && F % 256 == 0) xq_ffn_ = act8(F);
+    if (quantized(layers_[0].o->mat.type) && Hq % 256 == 0) xq_attn_ = act8(Hq, gpu::act_block(layers_[0].o->mat.type));
+    if (quantized(layers_[0].down->mat.type) && F % 256 == 0) xq_ffn_ = act8(F, gpu::act_block(layers_[0].down->mat.type));
     if ((quantized(layers_[0].qkv->mat.type) || quantized(layers_[0].gate_up->mat.type)) && H % 256 == 0) {
-        xq_norm_ = act8(H);
+        xq_norm_ = act8(H, gpu::kActBlock);
     }
     step_dev_ = static_cast<gpu::StepDev*>(device_alloc(sizeof(gpu::StepDev)));
     out_dev_ = static_cast<gpu::StepOut*>(device_alloc(sizeof(gpu::StepOut)));
@@ -531,7 +527,7 @@ std::string gemv_label(const gpu::GemvArgs& a) {
 double gemv_bytes(const gpu::GemvArgs& a) {
     const double rows = a.mat.rows, K = a.mat.cols, n = a.n_tok;
     double w = static_cast<double>(mat_bytes(a.mat)) + (a.mat.bias ? 4.0 * rows : 0.0);
-    double in = a.xq.q ? n * K * (1.0 + 4.0 / 256.0 + 2.0 / 16.0) : n * K * 4.0 + (a.x.gain ? K * 4.0 : 0.0);
+    double in = a.xq.q ? n * K * (1.0 + 4.0 / a.xq.blk + 2.0 / 16.0) : n * K * 4.0 + (a.x.gain ? K * 4.0 : 0.0);
     double out = n * rows * 4.0;
     switch (a.mode) {
     case gpu::kAdd: out *= 2.0; break;
@@ -601,13 +597,18 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
     // Normalized rows of multi-row steps are quantized once into xq_norm_
     // (the same codes the matmul prologue would stage): a draft-verify group
     // then stages int8 rows instead of normalizing them in every work-group.
+    // The block size is the consuming matrix's (32 values for Q8_0, else 256).
     auto normed = [&](gpu::GemvArgs& a, const float* gain) {
+        const int32_t blk = gpu::act_block(a.mat.type);
         if (n_rows > kNormedPrologueRows && quantized(a.mat.type) && xq_norm_.q) {
+            gpu::Act8 xq = xq_norm_;
+            xq.blk = blk;
             timed("k_quantize_norm", n * H * 9.1,
-                  [&] { gpu::launch_quantize_norm(h_, H, nullptr, gain, p.rms_eps, n_rows, xq_norm_, s); });
-            a.xq = xq_norm_;
+                  [&] { gpu::launch_quantize_norm(h_, H, nullptr, gain, p.rms_eps, n_rows, xq, s); });
+            a.xq = xq;
         } else {
             a.x = {h_, H, nullptr, gain, p.rms_eps};
+            a.ablk = blk;
         }
     };
     // attention split slots this step shape can fill (a prefill chunk: few long splits)
@@ -670,6 +671,7 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
             dn.xq = xq_ffn_;
         } else {
             dn.x = {ffn_, F, nullptr, nullptr, 0.0F};
+            dn.ablk = gpu::act_block(dn.mat.type);
         }
         dn.y = h_;
         dn.y_stride = H;
@@ -682,14 +684,18 @@ void Engine::record(int32_t n_rows, int32_t max_len, int32_t n_seq, int32_t n_ou
         head.n_tok = n_out;
         const int32_t* out_rows =
             reinterpret_cast<const int32_t*>(reinterpret_cast<const char*>(step_dev_) + offsetof(gpu::StepDev, out_row));
+        const int32_t head_blk = gpu::act_block(head.mat.type);
         if (n_out > kNormedPrologueRows && quantized(head.mat.type) && xq_norm_.q) {
             // several logits rows (draft verify, batches): normalized and quantized once
+            gpu::Act8 xq = xq_norm_;
+            xq.blk = head_blk;
             timed("k_quantize_norm", n_out * H * 9.1, [&] {
-                gpu::launch_quantize_norm(h_, H, out_rows, output_norm_, p.rms_eps, n_out, xq_norm_, s);
+                gpu::launch_quantize_norm(h_, H, out_rows, output_norm_, p.rms_eps, n_out, xq, s);
             });
-            head.xq = xq_norm_;
+            head.xq = xq;
         } else {
             head.x = {h_, H, out_rows, output_norm_, p.rms_eps};
+            head.ablk = head_blk;
         }
         head.y = logits_;
         head.y_stride = static_cast<int32_t>(p.n_vocab);
@@ -1065,16 +1071,19 @@ void Engine::dequantize(const std::string& name, uint32_t row0, uint32_t n_rows,
 
 namespace {
 
-// Bytes of the int8 copy of n_tok rows of K values (codes, one scale per 256
+// Bytes of the int8 copy of n_tok rows of K values (codes, one scale per blk
 // values, one sum per 16).
-size_t act8_bytes(size_t n_tok, size_t K) { return n_tok * K + n_tok * (K / 256) * sizeof(float) + n_tok * (K / 16) * 2; }
+size_t act8_bytes(size_t n_tok, size_t K, size_t blk) {
+    return n_tok * K + n_tok * (K / blk) * sizeof(float) + n_tok * (K / 16) * 2;
+}
 
-gpu::Act8 act8_at(uint8_t* base, size_t n_tok, size_t K) {
+gpu::Act8 act8_at(uint8_t* base, size_t n_tok, size_t K, int32_t blk) {
     gpu::Act8 xq;
     xq.K = static_cast<int32_t>(K);
+    xq.blk = blk;
     xq.q = reinterpret_cast<int8_t*>(base);
     xq.d = reinterpret_cast<float*>(base + n_tok * K);
-    xq.s = reinterpret_cast<int16_t*>(base + n_tok * K + n_tok * (K / 256) * sizeof(float));
+    xq.s = reinterpret_cast<int16_t*>(base + n_tok * K + n_tok * (K / blk) * sizeof(float));
     return xq;
 }
 
@@ -1082,10 +1091,11 @@ size_t round256(size_t n) { return (n + 255) / 256 * 256; }
 
 }  // namespace
 
-// Quantized formats from 3 rows on are quantized once (xq, n_tok x K) and
-// run on the matrix-core paths a step takes (token quads up to 8 rows, the
-// wide kernel beyond, where the format has one); y_full receives the whole
-// device matrix's output rows, n_tok x rows.
+// Quantized formats from 3 rows on are quantized once (xq, n_tok x K, in
+// blocks of the weight type's act_block) and run on the matrix-core paths a
+// step takes (token quads up to 8 rows, the wide kernel beyond, where the
+// format has one); y_full receives the whole device matrix's output rows,
+// n_tok x rows.
 bool Engine::matmul_staged(const gpu::DMat& m, uint32_t n_tok) {
     return n_tok >= 3 && quantized(m.type) && m.cols % 256 == 0;
 }
@@ -1108,6 +1118,7 @@ void Engine::run_matmul(const gpu::DMat& m, const float* x, uint32_t n_tok, floa
         else gpu::launch_gemv(a, stream_);
     } else {
         a.x = {x, static_cast<int32_t>(m.cols), nullptr, nullptr, 0.0F};
+        a.ablk = gpu::act_block(m.type);
         gpu::launch_gemv(a, stream_);
     }
 }
@@ -1138,9 +1149,10 @@ void Engine::matmul(const std::string& name, const float* x_host, uint32_t n_tok
     try {
         hip_check(hipMemcpyAsync(x, x_host, x_bytes, hipMemcpyHostToDevice, stream_), "upload activations");
         gpu::Act8 xq;
+        const int32_t blk = gpu::act_block(m.type);
         if (matmul_staged(m, n_tok)) {
-            hip_check(hipMalloc(&xq_mem, act8_bytes(n_tok, m.cols)), "allocate int8 rows");
-            xq = act8_at(xq_mem, n_tok, m.cols);
+            hip_check(hipMalloc(&xq_mem, act8_bytes(n_tok, m.cols, blk)), "allocate int8 rows");
+            xq = act8_at(xq_mem, n_tok, m.cols, blk);
         }
         run_matmul(m, x, n_tok, y, xq);
         hip_check(hipMemcpyAsync(full.data(), y, y_bytes, hipMemcpyDeviceToHost, stream_), "download matmul");
@@ -1165,7 +1177,8 @@ void Engine::matmul_noalloc(const std::string& name, const float* x_dev, uint32_
         fail(Status::InvalidArgument, "matmul shape is outside the engine workspace");
     }
     // staging in the GPU's static scratch: [int8 rows][the device matrix's output rows]
-    const size_t xq_bytes = matmul_staged(m, n_tok) ? round256(act8_bytes(n_tok, m.cols)) : 0;
+    const int32_t blk = gpu::act_block(m.type);
+    const size_t xq_bytes = matmul_staged(m, n_tok) ? round256(act8_bytes(n_tok, m.cols, blk)) : 0;
     const size_t y_bytes = round256(static_cast<size_t>(n_tok) * m.rows * sizeof(float));
     if (xq_bytes + y_bytes > gpu::kScratchBytes) {
         fail(Status::InvalidArgument, "allocation-free matmul of " + name + " over " + std::to_string(n_tok) +
@@ -1177,7 +1190,7 @@ void Engine::matmul_noalloc(const std::string& name, const float* x_dev, uint32_
     if (base == nullptr) fail(Status::DeviceError, "the device's static scratch was not set up");
     std::lock_guard use(gpu::scratch_lock(options_.device));
     gpu::Act8 xq;
-    if (xq_bytes) xq = act8_at(base, n_tok, m.cols);
+    if (xq_bytes) xq = act8_at(base, n_tok, m.cols, blk);
     float* y_full = reinterpret_cast<float*>(base + xq_bytes);
     run_matmul(m, x_dev, n_tok, y_full, xq);
     gpu::launch_gather_rows(y_full, static_cast<int32_t>(m.rows), y_dev, static_cast<int32_t>(ref.rows),

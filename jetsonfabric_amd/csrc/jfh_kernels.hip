@@ -227,6 +227,43 @@ __device__ __forceinline__ void quant_block_wave(const float v[4], int lane, int
     if ((lane & 3) == 0) s[lane >> 2] = static_cast<int16_t>(sum);
     if (lane == 0) *d = db;
 }
+
+// A float rounded to the nearest f16 value (the stored scale of a 32-value block).
+__device__ __forceinline__ float round_f16(float v) { return static_cast<float>(static_cast<_Float16>(v)); }
+
+// Code of one value of a block given id = 1/d' (d' = amax/127): roundf(x * id),
+// clamped to +-127 (the 256-value rule per block).
+__device__ __forceinline__ int quant_code(float v, float id) {
+    const float r = fminf(127.0F, fmaxf(-127.0F, roundf(v * id)));
+    return static_cast<int>(r);
+}
+
+// The same rule over 32-value blocks: the wave's 256 values (4 per lane) form
+// eight blocks of eight lanes (block k = lanes 8k .. 8k+7). d[k] receives
+// amax/127, rounded to f16 unless RAW (a normalized row's scale is rounded
+// after its rms factor is applied); s the sum of every 16 codes.
+template <bool RAW>
+__device__ __forceinline__ void quant_block_wave32(const float v[4], int lane, int8_t* q, float* d, int16_t* s) {
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = fmaxf(amax, dpp_f<0xB1>(amax));
+    amax = fmaxf(amax, dpp_f<0x4E>(amax));
+    amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror: the other quad of the eight lanes
+    const float db = amax / 127.0F;
+    const float id = db > 0.0F ? 1.0F / db : 0.0F;
+    int qi[4];
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        qi[i] = quant_code(v[i], id);
+        sum += qi[i];
+    }
+    const uint32_t packed = (qi[0] & 0xFF) | ((qi[1] & 0xFF) << 8) | ((qi[2] & 0xFF) << 16) | ((qi[3] & 0xFF) << 24);
+    reinterpret_cast<uint32_t*>(q)[lane] = packed;
+    sum += dpp_i<0xB1>(sum);
+    sum += dpp_i<0x4E>(sum);
+    if ((lane & 3) == 0) s[lane >> 2] = static_cast<int16_t>(sum);
+    if ((lane & 7) == 0) d[lane >> 3] = RAW ? db : round_f16(db);
+}
 #pragma clang fp contract(on)
 
 __device__ __forceinline__ const float* x_row(const XIn& x, int t) {
@@ -266,11 +303,12 @@ __device__ void row_rms(const XIn& x, int n_tok, int K, float* rs, float* red) {
 }
 
 // Quantizes values [c0, c0 + nb*256) of every token row into the LDS chunk
-// (q [t][chunk] permuted per block, d [t][chunk/256], s [t][chunk/16]), one
-// wave per 256-value block, loads issued kStageBatch blocks at a time. With a
-// gain (RMSNorm input) the codes are those of x * gain and ssq[t][b] receives
-// the block's sum of x^2; the block scales are multiplied by the row's
-// 1/rms afterwards (finish_norm), so one pass over x serves both.
+// (q [t][chunk] permuted per block, d [t][chunk/ABLK], s [t][chunk/16]), one
+// wave per 256 values, loads issued kStageBatch blocks at a time; A32 puts the
+// values in 32-value blocks (eight scales per 256 values). With a gain
+// (RMSNorm input) the codes are those of x * gain and ssq[t][b] receives the
+// 256 values' sum of x^2; the block scales are multiplied by the row's 1/rms
+// afterwards (finish_norm), so one pass over x serves both.
 //
 // The first batch of a pass is loaded ahead (stage_f32_load) and handed in:
 // a wave's loads complete in issue order, so activations requested before the
@@ -299,10 +337,11 @@ __device__ __forceinline__ void stage_f32_load(const XIn& x, int n_tok, int c0, 
 }
 
 #pragma clang fp contract(off)
-template <int NTHR, int NB, bool GAIN>
+template <int NTHR, int NB, bool GAIN, bool A32>
 __device__ __forceinline__ void stage_f32_store(int n_tok, int nb, int j0, const f32x4 (&r)[2 * NB], int8_t* sq,
                                                 float* sd, int16_t* ss, float* ssq, int chunk) {
     constexpr int W = NTHR / kWave;
+    constexpr int DB = A32 ? 8 : 1;  // scales per 256 values
     const int lane = threadIdx.x & (kWave - 1);
     const int total = n_tok * nb;
 #pragma unroll
@@ -319,55 +358,64 @@ __device__ __forceinline__ void stage_f32_store(int n_tok, int nb, int j0, const
                 vv[2] = vv[2] * r[NB + u].z;
                 vv[3] = vv[3] * r[NB + u].w;
             }
-            quant_block_wave(vv, lane, sq + t * chunk + b * 256, sd + t * (chunk / 256) + b,
-                             ss + t * (chunk / 16) + b * 16);
+            float* dst_d = sd + t * (chunk / 256 * DB) + b * DB;
+            if constexpr (A32) {
+                quant_block_wave32<GAIN>(vv, lane, sq + t * chunk + b * 256, dst_d, ss + t * (chunk / 16) + b * 16);
+            } else {
+                quant_block_wave(vv, lane, sq + t * chunk + b * 256, dst_d, ss + t * (chunk / 16) + b * 16);
+            }
         }
     }
 }
 #pragma clang fp contract(on)
 
 // Stages a pass whose first batch (blocks wave, wave + W, ...) is already loaded.
-template <int NTHR, int NB, bool GAIN>
+template <int NTHR, int NB, bool GAIN, bool A32>
 __device__ __forceinline__ void stage_f32(const XIn& x, int n_tok, int c0, int nb, int8_t* sq, float* sd, int16_t* ss,
                                           float* ssq, int chunk, const f32x4 (&first)[2 * NB]) {
     constexpr int W = NTHR / kWave;
     const int wave = threadIdx.x / kWave;
     const int total = n_tok * nb;
-    stage_f32_store<NTHR, NB, GAIN>(n_tok, nb, wave, first, sq, sd, ss, ssq, chunk);
+    stage_f32_store<NTHR, NB, GAIN, A32>(n_tok, nb, wave, first, sq, sd, ss, ssq, chunk);
     for (int j0 = wave + NB * W; j0 < total; j0 += NB * W) {
         f32x4 r[2 * NB];
         stage_f32_load<NTHR, NB, GAIN>(x, n_tok, c0, nb, j0, r);
-        stage_f32_store<NTHR, NB, GAIN>(n_tok, nb, j0, r, sq, sd, ss, ssq, chunk);
+        stage_f32_store<NTHR, NB, GAIN, A32>(n_tok, nb, j0, r, sq, sd, ss, ssq, chunk);
     }
 }
 
-// After stage_f32 with a gain over the whole row (nb blocks): rs = 1/sqrt(
-// sum(x^2)/K + eps) per token (block sums added in block order) scales the
-// token's block scales (qwen2_architecture.cpp:373-376). Every thread that
-// scales a block computes its token's rs itself (the same sums in the same
-// order), so one barrier separates the staging from the scaling and the
-// matmul's own barrier the scaling from the first dot.
-template <int NTHR>
+// After stage_f32 with a gain over the whole row (nb 256-value pieces): rs =
+// 1/sqrt(sum(x^2)/K + eps) per token (piece sums added in order) scales the
+// token's block scales (qwen2_architecture.cpp:373-376); 32-value block scales
+// are then rounded to f16. Every thread that scales a block computes its
+// token's rs itself (the same sums in the same order), so one barrier
+// separates the staging from the scaling and the matmul's own barrier the
+// scaling from the first dot.
+#pragma clang fp contract(off)
+template <int NTHR, bool A32>
 __device__ void finish_norm(int n_tok, int nb, int K, float eps, const float* ssq, float* sd, int chunk) {
+    constexpr int DB = A32 ? 8 : 1;
     __syncthreads();
-    for (int i = threadIdx.x; i < n_tok * nb; i += NTHR) {
-        const int t = i / nb, b = i - t * nb;
+    for (int i = threadIdx.x; i < n_tok * nb * DB; i += NTHR) {
+        const int t = i / (nb * DB), b = i - t * (nb * DB);
         float sum = 0.0F;
         for (int c = 0; c < nb; ++c) sum += ssq[t * nb + c];
         const float rs = 1.0F / sqrtf(sum / static_cast<float>(K) + eps);
-        sd[t * (chunk / 256) + b] = sd[t * (chunk / 256) + b] * rs;
+        const float v = sd[t * (chunk / 256 * DB) + b] * rs;
+        sd[t * (chunk / 256 * DB) + b] = A32 ? round_f16(v) : v;
     }
 }
 #pragma clang fp contract(on)
 
 // Copies values [c0, c0 + nb*256) of pre-quantized rows into the LDS chunk.
 // Batch b of a thread holds code pieces tid + (4 b + u) NTHR (uint4, u < 4),
-// sum piece tid + b NTHR (uint4 of 8 int16) and block scale tid + b NTHR;
-// indices are clamped so that every load is issued unconditionally. As with
+// sum piece tid + b NTHR (uint4 of 8 int16) and block scale tid + b NTHR (A32:
+// scale piece tid + b NTHR, a uint4 of four 32-value block scales); indices
+// are clamped so that every load is issued unconditionally. As with
 // stage_f32, the first batch is loaded ahead of the weights.
 using StageA8Regs = u32x4[6];
 
-template <int NTHR>
+template <int NTHR, bool A32>
 __device__ __forceinline__ void stage_act8_load(const Act8& xq, int n_tok, int c0, int nb, int batch, StageA8Regs& r) {
     const int tid = threadIdx.x, n16 = nb * 16, nq = n_tok * n16, ns = n_tok * nb * 2, nd = n_tok * nb;
 #pragma unroll
@@ -380,15 +428,18 @@ __device__ __forceinline__ void stage_act8_load(const Act8& xq, int n_tok, int c
         const int i = min(tid + batch * NTHR, ns - 1);
         const int t = i / (2 * nb), k = i - t * 2 * nb;
         r[4] = *reinterpret_cast<const u32x4*>(xq.s + static_cast<size_t>(t) * (xq.K / 16) + c0 / 16 + 8 * k);
+        if constexpr (A32) {
+            r[5] = *reinterpret_cast<const u32x4*>(xq.d + static_cast<size_t>(t) * (xq.K / 32) + c0 / 32 + 4 * k);
+        }
     }
-    {
+    if constexpr (!A32) {
         const int i = min(tid + batch * NTHR, nd - 1);
         const int t = i / nb, b = i - t * nb;
         r[5].x = __float_as_uint(xq.d[static_cast<size_t>(t) * (xq.K / 256) + c0 / 256 + b]);
     }
 }
 
-template <int NTHR>
+template <int NTHR, bool A32>
 __device__ __forceinline__ void stage_act8_store(int n_tok, int nb, int batch, const StageA8Regs& r, int8_t* sq,
                                                  float* sd, int16_t* ss, int chunk) {
     const int tid = threadIdx.x, n16 = nb * 16, nq = n_tok * n16, ns = n_tok * nb * 2, nd = n_tok * nb;
@@ -404,22 +455,25 @@ __device__ __forceinline__ void stage_act8_store(int n_tok, int nb, int batch, c
     if (i < ns) {
         const int t = i / (2 * nb), k = i - t * 2 * nb;
         reinterpret_cast<u32x4*>(ss + t * (chunk / 16))[k] = r[4];
+        if constexpr (A32) reinterpret_cast<u32x4*>(sd + t * (chunk / 32))[k] = r[5];
     }
-    if (i < nd) {
-        const int t = i / nb, b = i - t * nb;
-        sd[t * (chunk / 256) + b] = __uint_as_float(r[5].x);
+    if constexpr (!A32) {
+        if (i < nd) {
+            const int t = i / nb, b = i - t * nb;
+            sd[t * (chunk / 256) + b] = __uint_as_float(r[5].x);
+        }
     }
 }
 
-template <int NTHR>
+template <int NTHR, bool A32>
 __device__ __forceinline__ void stage_act8(const Act8& xq, int n_tok, int c0, int nb, int8_t* sq, float* sd,
                                            int16_t* ss, int chunk, const StageA8Regs& first) {
     const int nq = n_tok * nb * 16, ns = n_tok * nb * 2;
-    stage_act8_store<NTHR>(n_tok, nb, 0, first, sq, sd, ss, chunk);
+    stage_act8_store<NTHR, A32>(n_tok, nb, 0, first, sq, sd, ss, chunk);
     for (int batch = 1; batch * 4 * NTHR < nq || batch * NTHR < ns; ++batch) {
         StageA8Regs r;
-        stage_act8_load<NTHR>(xq, n_tok, c0, nb, batch, r);
-        stage_act8_store<NTHR>(n_tok, nb, batch, r, sq, sd, ss, chunk);
+        stage_act8_load<NTHR, A32>(xq, n_tok, c0, nb, batch, r);
+        stage_act8_store<NTHR, A32>(n_tok, nb, batch, r, sq, sd, ss, chunk);
     }
 }
 
@@ -467,11 +521,25 @@ __device__ __forceinline__ float q4k_term(float acc, float xd, float d, float dm
     return __builtin_fmaf(xd, t, acc);
 }
 
-// A Q8_0 tile's share of one lane group (two GGML blocks) for one token:
-// acc + xd * (da * ia + db * ib), with the fused products as written.
-__device__ __forceinline__ float q8_term(float acc, float xd, float da, float db, int ia, int ib) {
-    return __builtin_fmaf(xd, __builtin_fmaf(da, static_cast<float>(ia), db * static_cast<float>(ib)), acc);
+
+// The term of one 32-value activation block b of a Q8_0 tile (GGML block b of
+// the row's 256 values) for one (row, token), from its integer dot A:
+// A * (dw * xd) (GGML's q8_0 x q8_0 product). Lane group g's partial is
+// term(2 g) + term(2 g + 1) and the tile's total (p0 + p1) + (p2 + p3), added
+// to the running sum once per tile. Every path (decode dot, token quads,
+// wide) evaluates these expressions as written, so their rows agree bit for
+// bit.
+#pragma clang fp contract(off)
+__device__ __forceinline__ float q8_term32(float xd, float dw, int A) { return static_cast<float>(A) * (dw * xd); }
+__device__ __forceinline__ float pair_sum(float a, float b) { return a + b; }
+__device__ __forceinline__ float tile_total(float p0, float p1, float p2, float p3) { return (p0 + p1) + (p2 + p3); }
+// The decode lane's partial p (lane group g = lane / 16) -> the tile's total
+// in lane group 0's lanes: lanes i, i + 16, i + 32, i + 48 hold p0 .. p3 of row i.
+__device__ __forceinline__ float lane_tile_total(float p) {
+    const float h = p + __shfl_xor(p, 16);  // p0 + p1 (lane groups 0, 1), p2 + p3 (2, 3)
+    return h + __shfl_xor(h, 32);
 }
+#pragma clang fp contract(on)
 
 // Q4_K: header of row i | codes: the lane's 32 qs bytes (sub-blocks 2g, 2g+1).
 // The lane reads d|dmin and the 8 header bytes that hold its 24-bit scale
@@ -492,8 +560,9 @@ struct Tile<11> {
         r.w1 = *reinterpret_cast<const uint4*>(t + 1280 + 16 * lane);
         return r;
     }
-    template <int NT>
+    template <int NT, bool A32>
     static __device__ __forceinline__ void dot(const Regs& r, int g, const XLds& x, int nt, float* acc) {
+        static_assert(!A32, "K-quant matrices take 256-value activation blocks");
         const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
         // the lane group's 24-bit field: sc 2g | sc 2g+1 | m 2g | m 2g+1
         const uint32_t f = __builtin_amdgcn_alignbyte(r.f.y, r.f.x, (3 * g) & 3);
@@ -550,8 +619,9 @@ struct Tile<13> {
         r.d = *reinterpret_cast<const uint16_t*>(t + 2 * (lane & 15));
         return r;
     }
-    template <int NT>
+    template <int NT, bool A32>
     static __device__ __forceinline__ void dot(const Regs& r, int g, const XLds& x, int nt, float* acc) {
+        static_assert(!A32, "K-quant matrices take 256-value activation blocks");
         const float d = h2f(r.d);
         const uint32_t L[8] = {r.c0.x, r.c0.y, r.c0.z, r.c0.w, r.c1.x, r.c1.y, r.c1.z, r.c1.w};
         const uint32_t Hb[4] = {r.c2.x, r.c2.y, r.c2.z, r.c2.w};
@@ -608,9 +678,10 @@ struct Tile<7> {
         r.dd = *reinterpret_cast<const uint32_t*>(t + 16 * (lane & 15) + 4 * (lane >> 4));
         return r;
     }
-    template <int NT>
+    // Q8_0 inputs always come in 32-value blocks (GGML's q8_0 x q8_0 rule)
+    template <int NT, bool A32>
     static __device__ __forceinline__ void dot(const Regs& r, int g, const XLds& x, int nt, float* acc) {
-        (void) g;
+        static_assert(A32, "Q8_0 matrices take 32-value activation blocks");
         const float da = h2f(r.dd), db = h2f(r.dd >> 16);
         const uint32_t w[16] = {r.c[0].x, r.c[0].y, r.c[0].z, r.c[0].w, r.c[1].x, r.c[1].y, r.c[1].z, r.c[1].w,
                                 r.c[2].x, r.c[2].y, r.c[2].z, r.c[2].w, r.c[3].x, r.c[3].y, r.c[3].z, r.c[3].w};
@@ -628,7 +699,10 @@ struct Tile<7> {
                     ia = sdot4(w[k], xw[k], ia);
                     ib = sdot4(w[8 + k], xw[8 + k], ib);
                 }
-                acc[t] = q8_term(acc[t], x.d[tc * x.d_stride], da, db, ia, ib);
+                const float* xd = x.d + tc * x.d_stride + 2 * g;
+                const float p = pair_sum(q8_term32(xd[0], da, ia), q8_term32(xd[1], db, ib));
+                const float tot = lane_tile_total(p);
+                if (g == 0) acc[t] = pair_sum(acc[t], tot);
             }
         }
     }
@@ -648,8 +722,9 @@ struct Tile<9> {
         r.dd = *reinterpret_cast<const uint32_t*>(t + 4 * (lane & 15));
         return r;
     }
-    template <int NT>
+    template <int NT, bool A32>
     static __device__ __forceinline__ void dot(const Regs& r, int g, const XLds& x, int nt, float* acc) {
+        static_assert(!A32, "K-quant matrices take 256-value activation blocks");
         const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
         const uint32_t Q[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
         int sc[4], mn[4];  // scale bytes of sub-blocks 4g .. 4g+3
@@ -715,10 +790,11 @@ struct TileQ4Quad {
     }
     // acc[4 q + G']: running sum of (row lane % 16, token 4 q + lane / 16,
     // lane group G'); zero: 64 zero bytes of LDS (the masked A slots).
-    template <int NT>
+    template <int NT, bool A32>
     static __device__ __forceinline__ void dot(const Regs& r, int L, const XLds& x, int nt, float* acc,
                                                const int8_t* zero) {
         static_assert(NT % 4 == 0, "token quads");
+        static_assert(!A32, "K-quant matrices take 256-value activation blocks");
         constexpr int NQ = NT / 4;
         const int i = threadIdx.x & 15;
         const float d = h2f(r.hdr.x), dmin = h2f(r.hdr.x >> 16);
@@ -750,10 +826,10 @@ struct TileQ4Quad {
                 dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, ah[c]), bh[c], dh, 0, 0, 0);
             }
             const int tk = min(4 * q + L, nt - 1);
-            const float xd = x.d[tk * x.d_stride];
             const u32x4* sp = reinterpret_cast<const u32x4*>(x.s + tk * x.s_stride);
             const u32x4 s03 = sp[0], s47 = sp[1];  // the block's 16 code sums (int16 pairs)
             const uint32_t sw[8] = {s03.x, s03.y, s03.z, s03.w, s47.x, s47.y, s47.z, s47.w};
+            const float xd = x.d[tk * x.d_stride];
             // the tile's integer totals over the four lane groups, one float step into
             // acc[4 q]; acc[4 q + 1 .. 3] keep exact zeros (the decode dot's layout)
             int isum = 0, msum = 0;
@@ -793,10 +869,11 @@ struct TileQ6Quad {
         r.d = *reinterpret_cast<const uint16_t*>(t + 2 * (lane & 15));
         return r;
     }
-    template <int NT>
+    template <int NT, bool A32>
     static __device__ __forceinline__ void dot(const Regs& r, int L, const XLds& x, int nt, float* acc,
                                                const int8_t* zero) {
         static_assert(NT % 4 == 0, "token quads");
+        static_assert(!A32, "K-quant matrices take 256-value activation blocks");
         constexpr int NQ = NT / 4;
         const int i = threadIdx.x & 15;
         const float d = h2f(r.d);
@@ -851,7 +928,7 @@ struct TileQ6Quad {
 // Q8_0 tiles x 4..8 int8 token rows on matrix cores, with the operand layout
 // of TileQ4Quad: the lane group's 64 codes are eight 8-value chunks, chunks
 // 0..3 (GGML block 2 G') accumulate into D0 and chunks 4..7 (block 2 G' + 1)
-// into D1; the float step per lane group is Tile<7>::dot's.
+// into D1; the terms and the tile total are Tile<7>::dot's.
 struct TileQ8Quad {
     struct Regs {
         uint4 c[4];
@@ -864,10 +941,11 @@ struct TileQ8Quad {
         r.sc = *reinterpret_cast<const uint4*>(t + 16 * (lane & 15));
         return r;
     }
-    template <int NT>
+    template <int NT, bool A32>
     static __device__ __forceinline__ void dot(const Regs& r, int L, const XLds& x, int nt, float* acc,
                                                const int8_t* zero) {
         static_assert(NT % 4 == 0, "token quads");
+        static_assert(A32, "Q8_0 matrices take 32-value activation blocks");
         constexpr int NQ = NT / 4;
         const int i = threadIdx.x & 15;
         const uint32_t scw[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};  // (da, db) of lane groups 0..3
@@ -893,12 +971,16 @@ struct TileQ8Quad {
                 D1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a[4 + c]), b[4 + c], D1, 0, 0, 0);
             }
             const int tk = min(4 * q + L, nt - 1);
-            const float xd = x.d[tk * x.d_stride];
+            const float* xd = x.d + tk * x.d_stride;
+            const f32x4 xa = *reinterpret_cast<const f32x4*>(xd), xb = *reinterpret_cast<const f32x4*>(xd + 4);
+            const float x8[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+            float p[4];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const float da = h2f(scw[g]), db = h2f(scw[g] >> 16);
-                acc[4 * q + g] = q8_term(acc[4 * q + g], xd, da, db, D0[g], D1[g]);
+                p[g] = pair_sum(q8_term32(x8[2 * g], da, D0[g]), q8_term32(x8[2 * g + 1], db, D1[g]));
             }
+            acc[4 * q] = pair_sum(acc[4 * q], tile_total(p[0], p[1], p[2], p[3]));
         }
     }
 };
@@ -921,10 +1003,11 @@ struct TileQ2Quad {
         r.dd = *reinterpret_cast<const uint32_t*>(t + 4 * (lane & 15));
         return r;
     }
-    template <int NT>
+    template <int NT, bool A32>
     static __device__ __forceinline__ void dot(const Regs& r, int L, const XLds& x, int nt, float* acc,
                                                const int8_t* zero) {
         static_assert(NT % 4 == 0, "token quads");
+        static_assert(!A32, "K-quant matrices take 256-value activation blocks");
         constexpr int NQ = NT / 4;
         const int i = threadIdx.x & 15;
         const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
@@ -957,10 +1040,10 @@ struct TileQ2Quad {
                                                             0, 0, 0);
             }
             const int tk = min(4 * q + L, nt - 1);
-            const float xd = x.d[tk * x.d_stride];
             const u32x4* sp = reinterpret_cast<const u32x4*>(x.s + tk * x.s_stride);
             const u32x4 s03 = sp[0], s47 = sp[1];
             const uint32_t sw[8] = {s03.x, s03.y, s03.z, s03.w, s47.x, s47.y, s47.z, s47.w};
+            const float xd = x.d[tk * x.d_stride];
             // the tile's integer totals over the four lane groups, one float step into acc[4 q]
             int isum = 0, msum = 0;
 #pragma unroll
@@ -1169,18 +1252,9 @@ __device__ void gemv_epilogue(const GemvArgs& a, int row0, int nrows, Sum sum, f
 // and the wave's partial row sums added to its own LDS slot. Row results are
 // the sum of the waves' slots in wave order, so they do not depend on
 // scheduling.
-#ifndef JFH_MM_WAVES
-#define JFH_MM_WAVES 8
-#endif
-#ifndef JFH_MM_DEPTH
-#define JFH_MM_DEPTH 2
-#endif
-#ifndef JFH_MM_MIN_WGS
-#define JFH_MM_MIN_WGS 1
-#endif
-constexpr int kMmWaves = JFH_MM_WAVES;
+constexpr int kMmWaves = 8;
 constexpr int kMmThreads = kMmWaves * kWave;
-constexpr int kMmDepth = JFH_MM_DEPTH;
+constexpr int kMmDepth = 2;
 
 struct MmGeom {
     int32_t rgw;    // row groups per work-group
@@ -1189,12 +1263,14 @@ struct MmGeom {
 
 // Kinds of matmul input: pre-quantized rows (a.xq), float rows RMS-normalized
 // with a gain in the prologue (a.x with a.x.gain), plain float rows (a.x).
+// A32: the activations are (or are staged) in 32-value blocks.
 enum MmInput : int { kInAct8 = 0, kInNormed = 1, kInFloat = 2 };
 
-template <uint32_t TYPE, int NT, int IN>
-__global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, MmGeom geo) {
+template <uint32_t TYPE, int NT, int IN, bool A32>
+__global__ __launch_bounds__(kMmThreads) void k_mm(GemvArgs a, MmGeom geo) {
     constexpr bool A8 = IN == kInAct8;
     constexpr bool GAIN = IN == kInNormed;
+    constexpr int DB = A32 ? 8 : 1;  // activation scales per 256 values
     constexpr int NB = GAIN ? kStageBatch : kStageBatchFloat;  // blocks per wave of a float staging batch
     // int8 or normalized rows of a format with a token-quad tile, in token quads, run on matrix cores
     constexpr bool QUAD = kHasQuads<TYPE> && (A8 || GAIN) && NT % 4 == 0;
@@ -1209,14 +1285,13 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
     // staging for the step's n_tok rows (token slots past them are never read)
     int8_t* sq = reinterpret_cast<int8_t*>(lds_raw);
     float* sd = reinterpret_cast<float*>(lds_raw + n_tok * chunk);
-    int16_t* ss = reinterpret_cast<int16_t*>(sd + ((n_tok * nbc + 3) & ~3));  // 16-byte aligned
+    int16_t* ss = reinterpret_cast<int16_t*>(sd + ((n_tok * nbc * DB + 3) & ~3));  // 16-byte aligned
     // Row partials. One pass over K: each wave stores its finished row-group
     // sums with the four lane groups already combined, [rgw][W][16 rows][NT].
     // Several passes: every lane keeps running sums, [rgw][W][64 lanes][NT].
     const bool single = NT <= 2 || nbc >= nb;  // one- and two-token groups always run one pass (mm_geom)
     float* part = reinterpret_cast<float*>(ss + n_tok * (chunk / 16));
-    float* rs = part + (single ? rgw * W * 16 * NT : rgw * W * 64 * NT);
-    float* ssq = rs + NT;       // [n_tok][nbc] block sums of squares (normed inputs)
+    float* ssq = part + (single ? rgw * W * 16 * NT : rgw * W * 64 * NT);  // [n_tok][nbc] sums of squares (normed)
     float* lv = ssq + n_tok * nbc;  // [rgw * 16 * NT]
     // 64 zero bytes (16-byte aligned) for the masked operand slots of TileQ4Quad
     int8_t* zero = reinterpret_cast<int8_t*>(lds_raw) +
@@ -1274,7 +1349,7 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
     // in issue order, so the activations do not wait behind weight tiles)
     f32x4 f0[2 * NB];
     StageA8Regs q0;
-    if constexpr (A8) stage_act8_load<kMmThreads>(a.xq, n_tok, 0, nbcur, 0, q0);
+    if constexpr (A8) stage_act8_load<kMmThreads, A32>(a.xq, n_tok, 0, nbcur, 0, q0);
     else stage_f32_load<kMmThreads, NB, GAIN>(a.x, n_tok, 0, nbcur, wave, f0);
     prefetch(0);
     // the residual the epilogue adds to is fetched with the first weights
@@ -1294,10 +1369,10 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
         if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(zero)[threadIdx.x] = 0u;
     }
     if constexpr (A8) {
-        stage_act8<kMmThreads>(a.xq, n_tok, 0, nbcur, sq, sd, ss, chunk, q0);
+        stage_act8<kMmThreads, A32>(a.xq, n_tok, 0, nbcur, sq, sd, ss, chunk, q0);
     } else {
-        stage_f32<kMmThreads, NB, GAIN>(a.x, n_tok, 0, nbcur, sq, sd, ss, ssq, chunk, f0);
-        if constexpr (GAIN) finish_norm<kMmThreads>(n_tok, nbcur, K, a.x.eps, ssq, sd, chunk);
+        stage_f32<kMmThreads, NB, GAIN, A32>(a.x, n_tok, 0, nbcur, sq, sd, ss, ssq, chunk, f0);
+        if constexpr (GAIN) finish_norm<kMmThreads, A32>(n_tok, nbcur, K, a.x.eps, ssq, sd, chunk);
     }
 
     for (int c0b = 0;;) {
@@ -1317,13 +1392,13 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
                 const int bl = wave + W * cm;
                 XLds x;
                 x.q = xq0 + W * 256 * cm;
-                x.d = sd + bl;
+                x.d = sd + bl * DB;
                 x.s = ss + bl * 16;
                 x.q_stride = chunk;
-                x.d_stride = nbc;
+                x.d_stride = nbc * DB;
                 x.s_stride = chunk / 16;
-                if constexpr (QUAD) T::template dot<NT>(tile_regs, grp, x, n_tok, acc, zero);
-                else T::template dot<NT>(tile_regs, grp, x, n_tok, acc);
+                if constexpr (QUAD) T::template dot<NT, A32>(tile_regs, grp, x, n_tok, acc, zero);
+                else T::template dot<NT, A32>(tile_regs, grp, x, n_tok, acc);
                 if (++cm == pr) {
                     cm = 0;
                     if (single) {
@@ -1374,16 +1449,16 @@ __global__ __launch_bounds__(kMmThreads, JFH_MM_MIN_WGS) void k_mm(GemvArgs a, M
         total = pr * rgn;
         if constexpr (A8) {
             StageA8Regs qn;
-            stage_act8_load<kMmThreads>(a.xq, n_tok, c0b * 256, nbcur, 0, qn);
+            stage_act8_load<kMmThreads, A32>(a.xq, n_tok, c0b * 256, nbcur, 0, qn);
             prefetch(c0b);
             __syncthreads();  // every wave is done with the previous pass's activations
-            stage_act8<kMmThreads>(a.xq, n_tok, c0b * 256, nbcur, sq, sd, ss, chunk, qn);
+            stage_act8<kMmThreads, A32>(a.xq, n_tok, c0b * 256, nbcur, sq, sd, ss, chunk, qn);
         } else {
             f32x4 fn[2 * NB];
             stage_f32_load<kMmThreads, NB, GAIN>(a.x, n_tok, c0b * 256, nbcur, wave, fn);
             prefetch(c0b);
             __syncthreads();
-            stage_f32<kMmThreads, NB, GAIN>(a.x, n_tok, c0b * 256, nbcur, sq, sd, ss, ssq, chunk, fn);
+            stage_f32<kMmThreads, NB, GAIN, A32>(a.x, n_tok, c0b * 256, nbcur, sq, sd, ss, ssq, chunk, fn);
         }
     }
     __syncthreads();
@@ -1542,16 +1617,30 @@ struct WideTile<7> {
         return w;
     }
     static __device__ __forceinline__ Xt load_x(const uint32_t*, int) { return {}; }
-    static __device__ __forceinline__ void accumulate(const Wt& w, const long (&av)[8], const Xt&,
-                                                      const float (&xd)[4], int, float (&acc)[4][4]) {
+    // xd holds the token tile's 32-value block scales ([token][8]); the lane's
+    // tokens are 4 G + j. The terms and the tile total are the decode dot's
+    // (q8_term32, tile_total).
+    static __device__ __forceinline__ void accumulate32(const Wt& w, const long (&av)[8], const uint32_t*,
+                                                        const float* xd, int G, float (&acc)[4][4]) {
         const uint32_t D[4] = {w.dd.x, w.dd.y, w.dd.z, w.dd.w};
+        i32x4 I[4][2];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const float da = h2f(D[g]), db = h2f(D[g] >> 16);
-            const i32x4 ia = mfma_i8(av[2 * g], pack2(w.c[2 * g].x, w.c[2 * g].y));
-            const i32x4 ib = mfma_i8(av[2 * g + 1], pack2(w.c[2 * g + 1].x, w.c[2 * g + 1].y));
+            I[g][0] = mfma_i8(av[2 * g], pack2(w.c[2 * g].x, w.c[2 * g].y));
+            I[g][1] = mfma_i8(av[2 * g + 1], pack2(w.c[2 * g + 1].x, w.c[2 * g + 1].y));
+        }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[g][j] = q8_term(acc[g][j], xd[j], da, db, ia[j], ib[j]);
+        for (int j = 0; j < 4; ++j) {
+            const int tok = 4 * G + j;
+            const f32x4 x0 = *reinterpret_cast<const f32x4*>(xd + 8 * tok), x1 = *reinterpret_cast<const f32x4*>(xd + 8 * tok + 4);
+            const float x8[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            float p[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float da = h2f(D[g]), db = h2f(D[g] >> 16);
+                p[g] = pair_sum(q8_term32(x8[2 * g], da, I[g][0][j]), q8_term32(x8[2 * g + 1], db, I[g][1][j]));
+            }
+            acc[0][j] = pair_sum(acc[0][j], tile_total(p[0], p[1], p[2], p[3]));
         }
     }
 };
@@ -1712,6 +1801,43 @@ struct WideAct {
     u32x4 st;
 };
 
+// The loads of one (token tile tt, K tile b) item. Lanes 0..31 bring half
+// lane % 2 of token lane / 2's 16 code sums (SUMS); lanes 32..47 the scale of
+// token lane - 32, or with A32 lanes 32..63 half lane % 2 of token
+// (lane - 32) / 2's eight 32-value block scales. Token rows past the step
+// repeat its last row (their sums are never stored).
+template <bool SUMS, bool A32>
+__device__ __forceinline__ WideAct wide_load_act(const Act8& xq, int tt, int b, int n_tok, int K, int lane) {
+    const int i = lane & 15, G = lane >> 4;
+    const size_t tok = static_cast<size_t>(min(16 * tt + i, n_tok - 1));
+    WideAct r;
+    const uint4* xa = reinterpret_cast<const uint4*>(xq.q + tok * K + b * 256 + 64 * G);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) r.xa[u] = xa[u];
+    const int tl = lane < 32 ? lane >> 1 : (A32 ? (lane - 32) >> 1 : lane - 32);
+    const size_t tk = static_cast<size_t>(min(16 * tt + (tl & 15), n_tok - 1));
+    if (lane >= 32) {
+        if constexpr (A32) r.st = reinterpret_cast<const u32x4*>(xq.d + tk * (K / 32) + 8 * b)[lane & 1];
+        else r.st.x = __float_as_uint(xq.d[tk * (K / 256) + b]);
+    } else if (SUMS) {
+        r.st = reinterpret_cast<const u32x4*>(xq.s + tk * (K / 16) + 16 * b)[lane & 1];
+    }
+    return r;
+}
+
+// Writes a wave's item loads to its LDS slots: sums [token][2] (u32x4),
+// scales [token] or (A32) [token][8].
+template <bool SUMS, bool A32>
+__device__ __forceinline__ void wide_stage(const WideAct& r, int lane, u32x4* sums, float* scales) {
+    if (lane < 32) {
+        if (SUMS) sums[lane] = r.st;
+    } else if (A32) {
+        reinterpret_cast<u32x4*>(scales)[lane - 32] = r.st;
+    } else if (lane < 48) {
+        scales[lane - 32] = __uint_as_float(r.st.x);
+    }
+}
+
 // A operands from natural activation bytes: stretch s = 2 h + e (values
 // 32 s .. 32 s + 31) of lane group G is chunk 4 e + G of lane group h, so
 // for each e and 32-bit half the (chunk, lane group) 4 x 4 block is
@@ -1749,12 +1875,9 @@ __device__ __forceinline__ void wide_a_operands(const uint4 (&xa)[4], long (&av)
 // kWideTpw consecutive 16-token tiles (`tpw`). A wave keeps each of its K
 // tiles' weight operands in registers while it runs that tile for every
 // token tile of the group, with one accumulator set per token tile.
-#ifndef JFH_WIDE_TPW
-#define JFH_WIDE_TPW 2
-#endif
-constexpr int kWideTpw = JFH_WIDE_TPW;
+constexpr int kWideTpw = 2;
 
-template <uint32_t TYPE, bool MERGED>
+template <uint32_t TYPE, bool MERGED, bool A32>
 __global__ __launch_bounds__(kMmThreads) void k_mm_wide(GemvArgs a, int32_t n_rg, int32_t tpw, int32_t rpw) {
     using T = WideTile<TYPE>;
     constexpr int W = kMmWaves;
@@ -1762,7 +1885,7 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide(GemvArgs a, int32_t n_rg
     __shared__ float red[W][4][16][16];  // [wave][lane group][token][row] of one token tile
     __shared__ float vals[kWideRows][16];
     __shared__ u32x4 stage_s[W][16][2];
-    __shared__ float stage_d[W][16];
+    __shared__ float stage_d[W][A32 ? 16 * 8 : 16];  // scales [token] (A32: [token][8])
     __shared__ unsigned long long best[kWideRows];
     float* lv = &red[0][0][0][0];  // the epilogue's scratch (kWideRows x 16 floats) once red is read
     static_assert(sizeof(red) >= sizeof(float) * kWideRows * 16, "epilogue scratch");
@@ -1780,19 +1903,7 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide(GemvArgs a, int32_t n_rg
     const GemvArgs out = token_slice(a, t0, nt);
     if (MERGED && threadIdx.x < kWideRows) best[threadIdx.x] = 0ull;
     const Act8 xq = a.xq;
-    auto load_act = [&](int tt, int b) {
-        // token rows past the step repeat its last row; their sums are never stored
-        const size_t tok = static_cast<size_t>(min(16 * tt + i, n_tok - 1));
-        WideAct r;
-        const uint4* xa = reinterpret_cast<const uint4*>(xq.q + tok * K + b * 256 + 64 * G);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) r.xa[u] = xa[u];
-        const int tl = lane < 32 ? lane >> 1 : lane - 32;
-        const size_t tk = static_cast<size_t>(min(16 * tt + (tl & 15), n_tok - 1));
-        if (lane >= 32) r.st.x = __float_as_uint(xq.d[tk * nb + b]);
-        else if (T::kSums) r.st = reinterpret_cast<const u32x4*>(xq.s + tk * (K / 16) + 16 * b)[lane & 1];
-        return r;
-    };
+    auto load_act = [&](int tt, int b) { return wide_load_act<T::kSums, A32>(xq, tt, b, n_tok, K, lane); };
     for (int rr = 0; rr < (MERGED ? rpw : 1); ++rr) {
         const int rg = rg_first + 8 * rr;
         if (rg >= n_rg) break;
@@ -1812,20 +1923,21 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide(GemvArgs a, int32_t n_rg
             for (int tl = 0; tl < kWideTpw; ++tl) {
                 if (tl < ntl) {
                     const WideAct r = load_act(tt0 + tl, b);
-                    if (lane < 32) {
-                        if (T::kSums) stage_s[wave][lane >> 1][lane & 1] = r.st;
-                    } else if (lane < 48) {
-                        stage_d[wave][lane - 32] = __uint_as_float(r.st.x);
-                    }
-                    __builtin_amdgcn_wave_barrier();
-                    float xd[4];  // scales of tokens 4 G + j
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) xd[j] = stage_d[wave][4 * G + j];
-                    const typename T::Xt x = T::load_x(reinterpret_cast<const uint32_t*>(&stage_s[wave][i][0]), G);
+                    wide_stage<T::kSums, A32>(r, lane, &stage_s[wave][0][0], stage_d[wave]);
                     __builtin_amdgcn_wave_barrier();
                     long av[8];
                     wide_a_operands(r.xa, av);
-                    T::accumulate(w, av, x, xd, G, acc[tl]);
+                    if constexpr (A32) {
+                        T::accumulate32(w, av, reinterpret_cast<const uint32_t*>(&stage_s[wave][0][0]), stage_d[wave],
+                                        G, acc[tl]);
+                    } else {
+                        float xd[4];  // scales of tokens 4 G + j
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) xd[j] = stage_d[wave][4 * G + j];
+                        const typename T::Xt x = T::load_x(reinterpret_cast<const uint32_t*>(&stage_s[wave][i][0]), G);
+                        T::accumulate(w, av, x, xd, G, acc[tl]);
+                    }
+                    __builtin_amdgcn_wave_barrier();
                 }
             }
         }
@@ -1873,7 +1985,7 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide(GemvArgs a, int32_t n_rg
 // in order (the lane groups' other accumulators are exact zeros, and adding
 // them to a sum that starts at +0 changes no bit), so rows stay bit-identical
 // to decode rows.
-template <uint32_t TYPE, int R, int TP>
+template <uint32_t TYPE, int R, int TP, bool A32>
 __global__ __launch_bounds__(kMmThreads) void k_mm_wide_rg(GemvArgs a, int32_t n_rg, int32_t tpw) {
     using T = WideTile<TYPE>;
     constexpr int W = kMmWaves;
@@ -1881,7 +1993,7 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide_rg(GemvArgs a, int32_t n
     __shared__ float red[W][TP][16][16];  // [wave][token tile][token][row] of one row group
     __shared__ float vals[kWideRows][16 * R];
     __shared__ u32x4 stage_s[W][TP][16][2];
-    __shared__ float stage_d[W][TP][16];
+    __shared__ float stage_d[W][TP][A32 ? 16 * 8 : 16];  // scales [token] (A32: [token][8])
     const int n_tok = a.n_tok, n_tt = (n_tok + 15) / 16, n_grp = (n_tt + tpw - 1) / tpw;
     // work-group k runs on XCD k % 8: the token groups of one row-group set share an XCD (and its L2)
     const int q = static_cast<int>(blockIdx.x) >> 3;
@@ -1897,19 +2009,7 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide_rg(GemvArgs a, int32_t n
     const int t0 = 16 * tt0, nt = min(16 * (tt0 + ntl), n_tok) - t0;
     const GemvArgs out = token_slice(a, t0, nt);
     const Act8 xq = a.xq;
-    auto load_act = [&](int tt, int b) {
-        // token rows past the step repeat its last row; their sums are never stored
-        const size_t tok = static_cast<size_t>(min(16 * tt + i, n_tok - 1));
-        WideAct r;
-        const uint4* xa = reinterpret_cast<const uint4*>(xq.q + tok * K + b * 256 + 64 * G);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) r.xa[u] = xa[u];
-        const int tl = lane < 32 ? lane >> 1 : lane - 32;
-        const size_t tk = static_cast<size_t>(min(16 * tt + (tl & 15), n_tok - 1));
-        if (lane >= 32) r.st.x = __float_as_uint(xq.d[tk * nb + b]);
-        else if (T::kSums) r.st = reinterpret_cast<const u32x4*>(xq.s + tk * (K / 16) + 16 * b)[lane & 1];
-        return r;
-    };
+    auto load_act = [&](int tt, int b) { return wide_load_act<T::kSums, A32>(xq, tt, b, n_tok, K, lane); };
     const uint8_t* base = a.mat.data + static_cast<size_t>(rg0) * nb * TB;
     float acc[R][TP][4][4];
 #pragma unroll
@@ -1932,21 +2032,19 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide_rg(GemvArgs a, int32_t n
 #pragma unroll
         for (int tl = 0; tl < TP; ++tl) {
             const WideAct r = load_act(tt0 + min(tl, ntl - 1), b);
-            if (lane < 32) {
-                if (T::kSums) stage_s[wave][tl][lane >> 1][lane & 1] = r.st;
-            } else if (lane < 48) {
-                stage_d[wave][tl][lane - 32] = __uint_as_float(r.st.x);
-            }
+            wide_stage<T::kSums, A32>(r, lane, &stage_s[wave][tl][0][0], stage_d[wave][tl]);
             wide_a_operands(r.xa, av[tl]);
         }
         __builtin_amdgcn_wave_barrier();
+        if constexpr (!A32) {
 #pragma unroll
-        for (int tl = 0; tl < TP; ++tl) {
+            for (int tl = 0; tl < TP; ++tl) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xd[tl][j] = stage_d[wave][tl][4 * G + j];
-            x[tl] = T::load_x(reinterpret_cast<const uint32_t*>(&stage_s[wave][tl][i][0]), G);
+                for (int j = 0; j < 4; ++j) xd[tl][j] = stage_d[wave][tl][4 * G + j];
+                x[tl] = T::load_x(reinterpret_cast<const uint32_t*>(&stage_s[wave][tl][i][0]), G);
+            }
+            __builtin_amdgcn_wave_barrier();
         }
-        __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int rr = 0; rr < R; ++rr) {
             // the next row group's tile (clamped to the group's last) is requested before this one runs
@@ -1955,11 +2053,20 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide_rg(GemvArgs a, int32_t n
             if (rr < nrg) {
 #pragma unroll
                 for (int tl = 0; tl < TP; ++tl) {
-                    if (tl < ntl) T::accumulate(w, av[tl], x[tl], xd[tl], G, acc[rr][tl]);
+                    if (tl < ntl) {
+                        if constexpr (A32) {
+                            T::accumulate32(w, av[tl], reinterpret_cast<const uint32_t*>(&stage_s[wave][tl][0][0]),
+                                            stage_d[wave][tl], G, acc[rr][tl]);
+                        } else {
+                            T::accumulate(w, av[tl], x[tl], xd[tl], G, acc[rr][tl]);
+                        }
+                    }
                 }
             }
             w = wn;
         }
+        // the staged sums and scales are read until the last row group has run
+        if constexpr (A32) __builtin_amdgcn_wave_barrier();
     }
     // per row group and token tile: the sum over waves in wave order
 #pragma unroll
@@ -2036,17 +2143,18 @@ __global__ __launch_bounds__(kFloatThreads) void k_gemv_f(GemvArgs a, int32_t ro
 }
 
 // ------------------------------------------------------------------ activation quantization kernel
-// One wave per 256-value block: rows [0, n_rows) of x (stride floats apart)
-// into the staging layout of `out`.
+// One wave per 256 values: rows [0, n_rows) of x (stride floats apart) into
+// the staging layout of `out` (one 256-value block, or eight 32-value blocks).
 __global__ __launch_bounds__(256) void k_quantize(const float* x, int32_t stride, Act8 out) {
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int b = blockIdx.x * 4 + wave, row = blockIdx.y;
     if (b * 256 >= out.K) return;
     const float4 v4 = *reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * stride + b * 256 + 4 * lane);
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    quant_block_wave(v, lane, out.q + static_cast<size_t>(row) * out.K + b * 256,
-                     out.d + static_cast<size_t>(row) * (out.K / 256) + b,
-                     out.s + static_cast<size_t>(row) * (out.K / 16) + b * 16);
+    int8_t* q = out.q + static_cast<size_t>(row) * out.K + b * 256;
+    int16_t* s = out.s + static_cast<size_t>(row) * (out.K / 16) + b * 16;
+    if (out.blk == kActBlock32) quant_block_wave32<false>(v, lane, q, out.d + static_cast<size_t>(row) * (out.K / 32) + 8 * b, s);
+    else quant_block_wave(v, lane, q, out.d + static_cast<size_t>(row) * (out.K / 256) + b, s);
 }
 
 // RMSNorm x gain + quantization of whole rows, one work-group per row: the
@@ -2057,10 +2165,11 @@ constexpr int kNormThreads = 1024;  // a wave per block for rows up to 4096 valu
 #pragma clang fp contract(off)
 __global__ __launch_bounds__(kNormThreads) void k_quantize_norm(const float* x, int32_t stride, const int32_t* gather,
                                                        const float* gain, float eps, Act8 out) {
-    __shared__ float ssq[kNormMaxBlocks], db[kNormMaxBlocks];
+    __shared__ float ssq[kNormMaxBlocks], db[kNormMaxBlocks * 8];
     __shared__ float rs;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int row = blockIdx.x, nb = out.K / 256;
+    const bool a32 = out.blk == kActBlock32;
     const float* xr = x + static_cast<size_t>(gather ? gather[row] : row) * stride;
     for (int b = wave; b < nb; b += kNormThreads / kWave) {
         const f32x4 v4 = *reinterpret_cast<const f32x4*>(xr + b * 256 + 4 * lane);
@@ -2072,8 +2181,10 @@ __global__ __launch_bounds__(kNormThreads) void k_quantize_norm(const float* x, 
         vv[1] = vv[1] * g4.y;
         vv[2] = vv[2] * g4.z;
         vv[3] = vv[3] * g4.w;
-        quant_block_wave(vv, lane, out.q + static_cast<size_t>(row) * out.K + b * 256, &db[b],
-                         out.s + static_cast<size_t>(row) * (out.K / 16) + b * 16);
+        int8_t* q = out.q + static_cast<size_t>(row) * out.K + b * 256;
+        int16_t* s = out.s + static_cast<size_t>(row) * (out.K / 16) + b * 16;
+        if (a32) quant_block_wave32<true>(vv, lane, q, &db[8 * b], s);
+        else quant_block_wave(vv, lane, q, &db[b], s);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -2082,7 +2193,12 @@ __global__ __launch_bounds__(kNormThreads) void k_quantize_norm(const float* x, 
         rs = 1.0F / sqrtf(sum / static_cast<float>(out.K) + eps);
     }
     __syncthreads();
-    for (int b = threadIdx.x; b < nb; b += kNormThreads) out.d[static_cast<size_t>(row) * nb + b] = db[b] * rs;
+    // the scales times the row's 1/rms (32-value block scales then rounded to f16, as finish_norm)
+    const int nd = a32 ? 8 * nb : nb;
+    for (int b = threadIdx.x; b < nd; b += kNormThreads) {
+        const float v = db[b] * rs;
+        out.d[static_cast<size_t>(row) * nd + b] = a32 ? round_f16(v) : v;
+    }
 }
 #pragma clang fp contract(on)
 
@@ -2102,20 +2218,18 @@ constexpr int kAttnTile = 16;
 constexpr int kAttnWgKeys = kAttnTile * (kAttnThreads / kWave);
 constexpr int kAttnMaxSplits = 32;
 
-#ifndef JFH_ATTN_PREFILL_KEYS
-#define JFH_ATTN_PREFILL_KEYS 256
-#endif
+constexpr int kAttnPrefillKeys = 256;
 // Keys per split of a sequence with n_keys keys and len rows in the step: the
 // decode rule (about n_keys / splits_max, in whole rounds of the work-group's
 // waves), which depends on the position alone, so a verify or batched step
 // splits every row's keys exactly as serial decode does; a sequence bringing
 // more rows than any verify step (a prefill chunk) takes splits of at least
-// JFH_ATTN_PREFILL_KEYS keys, several tiles per wave. The attention and merge
+// kAttnPrefillKeys keys, several tiles per wave. The attention and merge
 // kernels use the same rule.
 __device__ __forceinline__ int attn_split_len(int n_keys, int len, int splits_max) {
     int L = (n_keys + splits_max - 1) / splits_max;
     L = (L + kAttnWgKeys - 1) / kAttnWgKeys * kAttnWgKeys;
-    if (JFH_ATTN_PREFILL_KEYS > 0 && len > kQuadGroupRows) L = max(L, JFH_ATTN_PREFILL_KEYS);
+    if (len > kQuadGroupRows) L = max(L, kAttnPrefillKeys);
     return L;
 }
 
@@ -2599,9 +2713,13 @@ __global__ __launch_bounds__(256) void k_attention_merge(const float* __restrict
         const int lane = threadIdx.x;
         const float4 v4 = *reinterpret_cast<const float4*>(&vals[4 * lane]);
         const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
-        quant_block_wave(vv, lane, xq.q + static_cast<size_t>(row) * xq.K + blockIdx.x * 256,
-                         xq.d + static_cast<size_t>(row) * (xq.K / 256) + blockIdx.x,
-                         xq.s + static_cast<size_t>(row) * (xq.K / 16) + blockIdx.x * 16);
+        int8_t* q = xq.q + static_cast<size_t>(row) * xq.K + blockIdx.x * 256;
+        int16_t* s = xq.s + static_cast<size_t>(row) * (xq.K / 16) + blockIdx.x * 16;
+        if (xq.blk == kActBlock32) {
+            quant_block_wave32<false>(vv, lane, q, xq.d + static_cast<size_t>(row) * (xq.K / 32) + 8 * blockIdx.x, s);
+        } else {
+            quant_block_wave(vv, lane, q, xq.d + static_cast<size_t>(row) * (xq.K / 256) + blockIdx.x, s);
+        }
     }
 }
 
@@ -2692,31 +2810,27 @@ void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStre
 // for 1 and for 8 tokens, so a draft-verify step reproduces serial decode bit
 // for bit. The per-wave row partials take at most kMmPartBytes of LDS, and
 // the row groups per work-group follow from kMmTargetWgs (mm_geom).
-#ifndef JFH_MM_CHUNK
-#define JFH_MM_CHUNK 8192
-#endif
-#ifndef JFH_MM_TARGET_WGS
-#define JFH_MM_TARGET_WGS 256
-#endif
-constexpr int kMmChunk = JFH_MM_CHUNK;
+constexpr int kMmChunk = 8192;
 constexpr int kMmPartBytes = 65536;
-constexpr int kMmTargetWgs = JFH_MM_TARGET_WGS;
+constexpr int kMmTargetWgs = 256;
 constexpr size_t kMmOnePassLds = 64 * 1024;  // largest one-pass staging of a row that is not normalized
 constexpr size_t kMmMaxLds = 160 * 1024;
 
-// LDS of k_mm: staging of n rows, row partials and epilogue values of nt token slots
-size_t mm_lds_bytes(int nt, int n, int chunk, int rgw, int K) {
+// LDS of k_mm: staging of n rows (db activation scales per 256 values), row
+// partials and epilogue values of nt token slots
+size_t mm_lds_bytes(int nt, int n, int chunk, int rgw, int K, int db) {
     const size_t nbc = static_cast<size_t>(chunk) / 256;
     const size_t part_rows = chunk >= K ? 16 : 64;  // one pass: combined lane groups (see k_mm)
-    return static_cast<size_t>(n) * chunk + (n * nbc + 3) / 4 * 16 + static_cast<size_t>(n) * chunk / 8 +
-           static_cast<size_t>(rgw) * kMmWaves * part_rows * nt * 4 + static_cast<size_t>(nt) * 4 + n * nbc * 4 +
+    return static_cast<size_t>(n) * chunk + (n * nbc * db + 3) / 4 * 16 + static_cast<size_t>(n) * chunk / 8 +
+           static_cast<size_t>(rgw) * kMmWaves * part_rows * nt * 4 + n * nbc * 4 +
            static_cast<size_t>(rgw) * 16 * nt * 4 + 16 + 64;  // + the aligned zero bytes
 }
 
-MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds) {
+MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds, bool a32) {
     static_assert(kMmChunk % (256 * kMmWaves) == 0, "a chunk must hold whole rounds of the waves' tiles");
     const int K = static_cast<int>(a.mat.cols);
     const int n_rg = (static_cast<int>(a.mat.rows) + 15) / 16;
+    const int db = a32 ? 8 : 1;
     // Up to 2 x kMmTargetWgs row groups: one work-group per CU (a few CUs
     // with two work-groups would set the kernel's time); larger matrices: two
     // work-groups per CU.
@@ -2738,33 +2852,51 @@ MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds) {
     int rgw = rgw_for(chunk);
     // A grid of at most one work-group per CU may use the whole LDS for one pass.
     const size_t one_pass = (n_rg + rgw - 1) / rgw <= kMmTargetWgs ? kMmMaxLds : kMmOnePassLds;
-    if (!normed && K > kMmChunk && mm_lds_bytes(nt, n, K, rgw, K) > one_pass) chunk = kMmChunk;
+    if (!normed && K > kMmChunk && mm_lds_bytes(nt, n, K, rgw, K, db) > one_pass) chunk = kMmChunk;
     rgw = rgw_for(chunk);
-    if (!normed && mm_lds_bytes(nt, n, chunk, rgw, K) > kMmMaxLds) {
+    if (!normed && mm_lds_bytes(nt, n, chunk, rgw, K, db) > kMmMaxLds) {
         // wide token groups: shorter passes, in whole rounds of the waves' tiles, until the staging fits
         const int round = 256 * kMmWaves;
         chunk = std::min(chunk, kMmChunk) / round * round;
         rgw = rgw_for(chunk);
-        while (chunk > round && mm_lds_bytes(nt, n, chunk, rgw, K) > kMmMaxLds) chunk -= round;
+        while (chunk > round && mm_lds_bytes(nt, n, chunk, rgw, K, db) > kMmMaxLds) chunk -= round;
     }
     if (nt <= 2 && chunk < K) throw std::invalid_argument("one- and two-token matmul rows must fit one pass");
     MmGeom g;
     g.rgw = rgw;
     g.chunk = chunk;
-    lds = mm_lds_bytes(nt, n, chunk, rgw, K);
+    lds = mm_lds_bytes(nt, n, chunk, rgw, K, db);
     if (lds > kMmMaxLds) throw std::invalid_argument("matmul staging does not fit the LDS");
     return g;
 }
 
+// Whether the activations of a matmul come in (or are staged in) 32-value
+// blocks: Q8_0 matrices take nothing else, the K-quants 256-value blocks.
+bool mm_a32(const GemvArgs& a) {
+    const bool a32 = a.xq.q != nullptr ? a.xq.blk == kActBlock32 : a.ablk == kActBlock32;
+    if (a32 != (a.mat.type == 7)) {
+        throw std::invalid_argument("activation block does not fit the weight type (Q8_0: 32 values, K-quants: 256)");
+    }
+    return a32;
+}
+
 template <uint32_t TYPE, int NT>
 void mm(const GemvArgs& a, hipStream_t stream) {
+    const bool a32 = mm_a32(a);
     size_t lds = 0;
-    const MmGeom g = mm_geom(a, NT, lds);
+    const MmGeom g = mm_geom(a, NT, lds, a32);
     const int n_rg = (static_cast<int>(a.mat.rows) + 15) / 16;
     const int grid = (n_rg + g.rgw - 1) / g.rgw;
-    if (a.xq.q != nullptr) launch(k_mm<TYPE, NT, kInAct8>, dim3(grid), dim3(kMmThreads), lds, stream, a, g);
-    else if (a.x.gain != nullptr) launch(k_mm<TYPE, NT, kInNormed>, dim3(grid), dim3(kMmThreads), lds, stream, a, g);
-    else launch(k_mm<TYPE, NT, kInFloat>, dim3(grid), dim3(kMmThreads), lds, stream, a, g);
+    const dim3 gd(grid), bd(kMmThreads);
+    if constexpr (TYPE == 7) {
+        if (a.xq.q != nullptr) launch(k_mm<TYPE, NT, kInAct8, true>, gd, bd, lds, stream, a, g);
+        else if (a.x.gain != nullptr) launch(k_mm<TYPE, NT, kInNormed, true>, gd, bd, lds, stream, a, g);
+        else launch(k_mm<TYPE, NT, kInFloat, true>, gd, bd, lds, stream, a, g);
+    } else {
+        if (a.xq.q != nullptr) launch(k_mm<TYPE, NT, kInAct8, false>, gd, bd, lds, stream, a, g);
+        else if (a.x.gain != nullptr) launch(k_mm<TYPE, NT, kInNormed, false>, gd, bd, lds, stream, a, g);
+        else launch(k_mm<TYPE, NT, kInFloat, false>, gd, bd, lds, stream, a, g);
+    }
     check(hipGetLastError(), "matmul launch");
 }
 
@@ -2861,7 +2993,7 @@ void launch_gemv(const GemvArgs& a_in, hipStream_t stream) {
         a.n_tok = a_in.n_tok - t0 < group ? a_in.n_tok - t0 : group;
         if (a.xq.q) {
             a.xq.q += static_cast<size_t>(t0) * a.xq.K;
-            a.xq.d += static_cast<size_t>(t0) * (a.xq.K / 256);
+            a.xq.d += static_cast<size_t>(t0) * (a.xq.K / a.xq.blk);
             a.xq.s += static_cast<size_t>(t0) * (a.xq.K / 16);
         } else if (a.x.gather) {
             a.x.gather += t0;
@@ -2895,6 +3027,7 @@ void launch_gemv(const GemvArgs& a_in, hipStream_t stream) {
 
 void launch_quantize(const float* x, int32_t stride, int32_t n_rows, const Act8& out, hipStream_t stream) {
     if (out.K % 256 != 0 || stride % 4 != 0) throw std::invalid_argument("quantized rows need multiples of 256 values");
+    if (out.blk != kActBlock && out.blk != kActBlock32) throw std::invalid_argument("activation blocks are 256 or 32 values");
     dim3 grid((out.K / 256 + 3) / 4, n_rows);
     launch(k_quantize, grid, dim3(256), 0, stream, x, stride, out);
     check(hipGetLastError(), "quantize launch");
@@ -2902,50 +3035,45 @@ void launch_quantize(const float* x, int32_t stride, int32_t n_rows, const Act8&
 
 void launch_quantize_norm(const float* x, int32_t stride, const int32_t* gather, const float* gain, float eps,
                           int32_t n_rows, const Act8& out, hipStream_t stream) {
-    if (out.K % 256 != 0 || out.K / 256 > kNormMaxBlocks || stride % 4 != 0 || gain == nullptr) {
+    if (out.K % 256 != 0 || out.K / 256 > kNormMaxBlocks || stride % 4 != 0 || gain == nullptr ||
+        (out.blk != kActBlock && out.blk != kActBlock32)) {
         throw std::invalid_argument("normalized quantization needs rows of a multiple of 256 values and a gain");
     }
     launch(k_quantize_norm, dim3(n_rows), dim3(kNormThreads), 0, stream, x, stride, gather, gain, eps, out);
     check(hipGetLastError(), "normalized quantize launch");
 }
 
-#ifndef JFH_WIDE_MIN_WGS
-#define JFH_WIDE_MIN_WGS 512
-#endif
-constexpr int kWideMinWgs = JFH_WIDE_MIN_WGS;
+constexpr int kWideMinWgs = 512;
 constexpr int kWideRgMinWgs = 256;  // one work-group per CU
-#ifndef JFH_WIDE_LOGITS_WGS
-#define JFH_WIDE_LOGITS_WGS 1024
-#endif
-constexpr int kWideLogitsWgs = JFH_WIDE_LOGITS_WGS;
+constexpr int kWideLogitsWgs = 1024;
 
 bool wide_matmul_supported(uint32_t type) { return type == 7 || type == 9 || type == 11 || type == 13; }
 
 // Measured on 7B-shaped layers: Q4_K and Q8_0 from 9 rows; Q6_K and Q2_K,
 // whose 16-value sub-blocks take two half-masked MFMAs per 32 values, only
 // beyond one 16-slot token-quad group.
-#ifndef JFH_WIDE_FROM_ROWS
-#define JFH_WIDE_FROM_ROWS 9
-#endif
+constexpr int32_t kWideFromRows = 9;
 int32_t wide_min_rows(uint32_t type) {
     switch (type) {
     case 7:
-    case 11: return JFH_WIDE_FROM_ROWS;
+    case 11: return kWideFromRows;
     case 9:
     case 13: return kQuadGroupRows + 1;
     default: return 0;
     }
 }
 
-void launch_gemv_wide(const GemvArgs& a, hipStream_t stream) {
-    if (!wide_matmul_supported(a.mat.type) || a.xq.q == nullptr || a.xq.K != static_cast<int32_t>(a.mat.cols) ||
-        a.mat.cols % kActBlock != 0 || a.n_tok < 1 || a.n_tok > kWideRows) {
+void launch_gemv_wide(const GemvArgs& a_in, hipStream_t stream) {
+    if (!wide_matmul_supported(a_in.mat.type) || a_in.xq.q == nullptr || a_in.xq.K != static_cast<int32_t>(a_in.mat.cols) ||
+        a_in.mat.cols % kActBlock != 0 || a_in.n_tok < 1 || a_in.n_tok > kWideRows) {
         throw std::invalid_argument("wide matmul takes Q4_K / Q6_K / Q8_0 / Q2_K weights and up to 64 pre-quantized token rows");
     }
-    if ((a.mode == kSwiGLU && a.mat.rows % (2 * kGluGroup) != 0) || (a.mode == kQKV && a.mat.rows % 2 != 0) ||
-        (a.mode == kLogits && a.best == nullptr)) {
+    if ((a_in.mode == kSwiGLU && a_in.mat.rows % (2 * kGluGroup) != 0) || (a_in.mode == kQKV && a_in.mat.rows % 2 != 0) ||
+        (a_in.mode == kLogits && a_in.best == nullptr)) {
         throw std::invalid_argument("wide matmul mode or row layout not supported");
     }
+    mm_a32(a_in);  // validates the activation block for the weight type
+    const GemvArgs& a = a_in;
     const int n_rg = (static_cast<int>(a.mat.rows) + 15) / 16, n_tt = (a.n_tok + 15) / 16;
     // as many token tiles per work-group as still leave kWideMinWgs work-groups
     int tpw = min(n_tt, kWideTpw);
@@ -2955,43 +3083,44 @@ void launch_gemv_wide(const GemvArgs& a, hipStream_t stream) {
     // activation load shared by the row groups: four (Q4_K only: the other formats'
     // operands take the registers) while kWideMinWgs work-groups remain, else two while
     // one work-group per CU remains (64-row chunks of 7B: gate_up 4, qkv, o and down 2)
+    int rgs = 1;
     if (!merged && a.mat.type != 7) {
-        int rgs = 1;
         if (a.mat.type == 11 && (n_rg + 3) / 4 * n_tt >= kWideMinWgs) rgs = 4;
         else if ((n_rg + 1) / 2 * n_tt >= kWideRgMinWgs) rgs = 2;
-        if (rgs > 1) {
-            const int tp1 = 1;
-            const dim3 g(((n_rg + rgs - 1) / rgs + 7) / 8 * 8 * n_tt), b(kMmThreads);
-            switch (a.mat.type * 8 + rgs) {
-            case 11 * 8 + 4: launch(k_mm_wide_rg<11, 4, 1>, g, b, 0, stream, a, n_rg, tp1); break;
-            case 11 * 8 + 2: launch(k_mm_wide_rg<11, 2, 1>, g, b, 0, stream, a, n_rg, tp1); break;
-            case 13 * 8 + 2: launch(k_mm_wide_rg<13, 2, 1>, g, b, 0, stream, a, n_rg, tp1); break;
-            default: launch(k_mm_wide_rg<9, 2, 1>, g, b, 0, stream, a, n_rg, tp1); break;
-            }
-            check(hipGetLastError(), "wide matmul launch");
-            return;
+    }
+    if (rgs > 1) {
+        const int tp1 = 1;
+        const dim3 g(((n_rg + rgs - 1) / rgs + 7) / 8 * 8 * n_tt), b(kMmThreads);
+        switch (a.mat.type * 8 + rgs) {
+        case 11 * 8 + 4: launch(k_mm_wide_rg<11, 4, 1, false>, g, b, 0, stream, a, n_rg, tp1); break;
+        case 11 * 8 + 2: launch(k_mm_wide_rg<11, 2, 1, false>, g, b, 0, stream, a, n_rg, tp1); break;
+        case 13 * 8 + 2: launch(k_mm_wide_rg<13, 2, 1, false>, g, b, 0, stream, a, n_rg, tp1); break;
+        default: launch(k_mm_wide_rg<9, 2, 1, false>, g, b, 0, stream, a, n_rg, tp1); break;
         }
+        check(hipGetLastError(), "wide matmul launch");
+        return;
     }
     // the head: row groups per work-group so that about kWideLogitsWgs work-groups merge their argmax
     const int rpw = a.mode == kLogits ? std::max(1, n_rg / kWideLogitsWgs) : 1;
     const int grid = (n_rg + 8 * rpw - 1) / (8 * rpw) * 8 * ((n_tt + tpw - 1) / tpw);
     const dim3 g(grid), b(kMmThreads);
+    auto go = [&](auto kernel) { launch(kernel, g, b, 0, stream, a, n_rg, tpw, rpw); };
     switch (a.mat.type) {
     case 7:
-        if (merged) launch(k_mm_wide<7, true>, g, b, 0, stream, a, n_rg, tpw, rpw);
-        else launch(k_mm_wide<7, false>, g, b, 0, stream, a, n_rg, tpw, rpw);
+        if (merged) go(k_mm_wide<7, true, true>);
+        else go(k_mm_wide<7, false, true>);
         break;
     case 9:
-        if (merged) launch(k_mm_wide<9, true>, g, b, 0, stream, a, n_rg, tpw, rpw);
-        else launch(k_mm_wide<9, false>, g, b, 0, stream, a, n_rg, tpw, rpw);
+        if (merged) go(k_mm_wide<9, true, false>);
+        else go(k_mm_wide<9, false, false>);
         break;
     case 11:
-        if (merged) launch(k_mm_wide<11, true>, g, b, 0, stream, a, n_rg, tpw, rpw);
-        else launch(k_mm_wide<11, false>, g, b, 0, stream, a, n_rg, tpw, rpw);
+        if (merged) go(k_mm_wide<11, true, false>);
+        else go(k_mm_wide<11, false, false>);
         break;
     default:
-        if (merged) launch(k_mm_wide<13, true>, g, b, 0, stream, a, n_rg, tpw, rpw);
-        else launch(k_mm_wide<13, false>, g, b, 0, stream, a, n_rg, tpw, rpw);
+        if (merged) go(k_mm_wide<13, true, false>);
+        else go(k_mm_wide<13, false, false>);
         break;
     }
     check(hipGetLastError(), "wide matmul launch");
@@ -3019,8 +3148,8 @@ size_t attention_partial_floats(int32_t rows, int32_t n_head, int32_t head_dim, 
 }
 
 int32_t attention_slots(int32_t splits, int32_t capacity, int32_t n_rows, int32_t n_seq) {
-    if (n_seq != 1 || n_rows <= kQuadGroupRows || JFH_ATTN_PREFILL_KEYS <= 0) return splits;
-    return std::max(1, std::min(splits, (capacity + JFH_ATTN_PREFILL_KEYS - 1) / JFH_ATTN_PREFILL_KEYS));
+    if (n_seq != 1 || n_rows <= kQuadGroupRows) return splits;
+    return std::max(1, std::min(splits, (capacity + kAttnPrefillKeys - 1) / kAttnPrefillKeys));
 }
 
 void launch_attention(const float* q, const StepDev* step, int32_t max_len, int32_t n_seq, int32_t layer,

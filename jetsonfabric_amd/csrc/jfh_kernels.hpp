@@ -14,18 +14,13 @@ constexpr int kMaxRows = 64;
 // Token groups of at least this many rows (int8 or RMS-normalized input) of
 // the quantized formats (Q4_K, Q6_K, Q8_0, Q2_K) run as token quads on matrix
 // cores.
-#ifndef JFH_QUAD_MIN_ROWS
-#define JFH_QUAD_MIN_ROWS 2
-#endif
-constexpr int kQuadMinRows = JFH_QUAD_MIN_ROWS;        // token rows of one step (sum over sequences)
+constexpr int kQuadMinRows = 2;        // token rows of one step (sum over sequences)
 // Token rows per matrix-core launch of the token-quad matmul (longer steps
 // run in groups of this many rows).
-#ifndef JFH_QUAD_GROUP_ROWS
-#define JFH_QUAD_GROUP_ROWS 16
-#endif
-constexpr int kQuadGroupRows = JFH_QUAD_GROUP_ROWS;
+constexpr int kQuadGroupRows = 16;
 constexpr int kMaxSeq = 16;         // sequences of one batched step
-constexpr int kActBlock = 256;      // activation quantization block (values)
+constexpr int kActBlock = 256;      // activation quantization block of K-quant inputs (values)
+constexpr int kActBlock32 = 32;     // activation block of Q8_0 inputs
 constexpr int kTileRows = 16;       // rows of one weight tile
 constexpr int kMaxAttnQGroups = 8;  // query groups of 8 rows per kv head in one step
 constexpr int kMaxEndTokens = 16;   // end-of-generation ids the on-GPU acceptance stops at
@@ -61,14 +56,21 @@ struct DMat {
     uint32_t row_bytes = 0;  // float types only
 };
 
-// int8 activation rows: per row, q holds the K codes, d one scale per 256
-// values and s the sum of every 16 codes.
+// int8 activation rows: per row, q holds the K codes, d one scale per `blk`
+// values and s the sum of every 16 codes. 256-value blocks keep d in f32
+// (inputs of the K-quant matrices: GGML's q8_K layout); 32-value blocks store
+// d rounded to f16 (inputs of Q8_0 matrices: GGML's q8_0 block).
 struct Act8 {
     int8_t* q = nullptr;
     float* d = nullptr;
     int16_t* s = nullptr;
-    int32_t K = 0;  // values per row (multiple of 256)
+    int32_t K = 0;    // values per row (multiple of 256)
+    int32_t blk = kActBlock;
 };
+
+// Activation block a quantized matrix of `type` takes: 32 values for Q8_0
+// (GGML's q8_0 x q8_0 dot), 256 for the K-quants (GGML's q8_K).
+constexpr int32_t act_block(uint32_t type) { return type == 7 ? kActBlock32 : kActBlock; }
 
 // Per-sequence cache description for a step.
 struct SeqDev {
@@ -141,8 +143,9 @@ struct GemvArgs {
     DMat mat;
     int32_t mode = kStore;
     int32_t n_tok = 1;
-    XIn x;                            // float activations (quantized by the matmul), or
+    XIn x;                            // float activations (quantized by the matmul in blocks of `ablk`), or
     Act8 xq;                          // pre-quantized activations (used when xq.q is set)
+    int32_t ablk = kActBlock;         // activation block of float inputs (act_block of the weight type)
     float* y = nullptr;               // output [tok][y_stride]
     int32_t y_stride = 0;
     unsigned long long* best = nullptr;  // kLogits: packed (value, -index) per token
@@ -162,11 +165,11 @@ void launch_embed(const DMat& table, const StepDev* step, float* h, int32_t n_ro
                   unsigned long long* best, int32_t n_best, hipStream_t stream);
 // Matmul of up to kMaxRows token rows (in groups of 8) against one matrix.
 void launch_gemv(const GemvArgs& a, hipStream_t stream);
-// Quantizes n_rows float rows of K values (K % 256 == 0) into `out`.
+// Quantizes n_rows float rows of K values (K % 256 == 0) into `out` (blocks of out.blk).
 void launch_quantize(const float* x, int32_t stride, int32_t n_rows, const Act8& out, hipStream_t stream);
 // RMS-normalizes n_rows float rows (row gather[r] when gather is set),
-// multiplies them by `gain` and quantizes them into `out`: the codes and
-// scales the matmul's normalized-input prologue would stage.
+// multiplies them by `gain` and quantizes them into `out` (blocks of out.blk):
+// the codes and scales the matmul's normalized-input prologue would stage.
 void launch_quantize_norm(const float* x, int32_t stride, const int32_t* gather, const float* gain, float eps,
                           int32_t n_rows, const Act8& out, hipStream_t stream);
 // Token rows of one matrix-core matmul launch (steps with more rows than the

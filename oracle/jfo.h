@@ -24,11 +24,16 @@
  *
  * Matmul numerics. GGML's backends quantize the activation vector to int8
  * blocks before the integer dot with quantized weights. The HIP engine does
- * the same with one fixed rule (int8 per 256 values, d = amax/127), and the
- * oracle restates that rule so that GPU and CPU see identical integer sums
- * (JFO_MODE_Q8). JFO_MODE_EXACT instead multiplies the exactly dequantized
- * weights with float activations: the mathematically exact product, used to
- * bound the error the activation quantization introduces.
+ * the same with fixed rules and the oracle restates them, so that GPU and CPU
+ * see identical integer sums (JFO_MODE_Q8):
+ *   - inputs of K-quant matrices (Q2_K, Q4_K, Q6_K): int8 per 256 values,
+ *     d = amax/127 kept in f32, 16-value code sums (the layout of GGML's
+ *     q8_K, which its CPU backend pairs with the K-quants);
+ *   - inputs of Q8_0 matrices: int8 per 32 values, d = amax/127 stored as
+ *     f16 (GGML's q8_0 block, the rule of its q8_0 x q8_0 dot).
+ * JFO_MODE_EXACT instead multiplies the exactly dequantized weights with
+ * float activations: the mathematically exact product, used to bound the
+ * error the activation quantization introduces.
  *
  * Parity status of each function is recorded in oracle/README.md.
  */
@@ -52,7 +57,12 @@ enum {
     JFO_Q6_K = 13,
 };
 
+/* JFO_MODE_Q8: activations quantized by the block rule of the weight type
+ * (32 values for Q8_0, 256 for the K-quants). */
 enum { JFO_MODE_EXACT = 0, JFO_MODE_Q8 = 1 };
+
+/* Activation block of a quantized matmul input: 32 for Q8_0 weights, else 256. */
+int jfo_act_block(int type);
 
 float jfo_f16_to_f32(uint16_t h);
 uint16_t jfo_f32_to_f16(float f);
@@ -71,6 +81,13 @@ int jfo_dequantize_row(int type, const void * src, float * dst, int64_t n);
 void jfo_quantize_act(const float * x, int64_t n, int8_t * q, float * d, int16_t * s16);
 
 /*
+ * The same rule over blocks of blk (256 or 32) values, d[n/blk]. For 32-value
+ * blocks the stored scale is d rounded to f16 (the codes use the f32 id), as
+ * GGML's q8_0 / q8_1 blocks store it.
+ */
+void jfo_quantize_act_blk(const float * x, int64_t n, int blk, int8_t * q, float * d, int16_t * s16);
+
+/*
  * Quantization of an RMS-normalized row as the HIP engine stages it: the codes
  * of x[i] * gain[i] per 256-value block (d' = amax/127, q = roundf(v / d')),
  * each block scale multiplied by the row's 1 / sqrtf(mean(x^2) + eps), so
@@ -79,15 +96,33 @@ void jfo_quantize_act(const float * x, int64_t n, int8_t * q, float * d, int16_t
 void jfo_quantize_act_normed(const float * x, const float * gain, int64_t n, float eps, int8_t * q, float * d,
                              int16_t * s16);
 
-/* y[t * rows + r] = W[r] . (q, d, s16)[t]: jfo_matmul's JFO_MODE_Q8 on pre-quantized rows. */
+/* The same over blocks of blk values (256, or 32 for Q8_0 inputs); 32-value
+ * block scales are (d' * rms_scale) rounded to f16. */
+void jfo_quantize_act_normed_blk(const float * x, const float * gain, int64_t n, float eps, int blk, int8_t * q,
+                                 float * d, int16_t * s16);
+
+/* y[t * rows + r] = W[r] . (q, d, s16)[t]: jfo_matmul's JFO_MODE_Q8 on pre-quantized rows
+ * (256-value blocks for the K-quants, 32 for Q8_0). */
 int jfo_matmul_q8(int type, const void * w, int64_t n, int64_t rows, const int8_t * q, const float * d,
                   const int16_t * s16, int64_t tokens, float * y, int threads);
+
+/* The same with activation blocks of blk values (d: n / blk scales per row);
+ * blk must be the weight type's jfo_act_block. */
+int jfo_matmul_q8_blk(int type, const void * w, int64_t n, int64_t rows, const int8_t * q, const float * d,
+                      const int16_t * s16, int64_t tokens, float * y, int blk, int threads);
 
 /* Dot product of one weight row with a quantized activation (n % 256 == 0):
  * integer dot per sub-block scaled by the sub-block scale, one float combine
  * per 256-value block (K-quants) or per 32-value block (Q8_0). */
 double jfo_vec_dot_q8(int type, const void * row, const int8_t * q, const float * d,
                       const int16_t * s16, int64_t n);
+
+/* The same with activation blocks of blk values, which must be the weight
+ * type's jfo_act_block (returns 0 otherwise): the K-quants per 256-value
+ * block as above; Q8_0 per 32-value block b, d[b] * dw * dot, summed in
+ * double (GGML's q8_0 x q8_0 product). */
+double jfo_vec_dot_q8_blk(int type, const void * row, const int8_t * q, const float * d, const int16_t * s16,
+                          int64_t n, int blk);
 
 /* Dot product of one weight row with float activations, exact dequantization. */
 double jfo_vec_dot_f32(int type, const void * row, const float * x, int64_t n);

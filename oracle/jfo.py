@@ -28,7 +28,7 @@ F32, F16, Q8_0, Q2_K, Q4_K, Q6_K = 1, 2, 7, 9, 11, 13
 MODE_EXACT, MODE_Q8 = 0, 1
 
 __all__ = [
-    "F32", "F16", "Q8_0", "Q2_K", "Q4_K", "Q6_K", "MODE_EXACT", "MODE_Q8", "lib", "block", "row_bytes",
+    "F32", "F16", "Q8_0", "Q2_K", "Q4_K", "Q6_K", "MODE_EXACT", "MODE_Q8", "act_block", "lib", "block", "row_bytes",
     "f16_to_f32", "f32_to_f16", "dequantize_row", "quantize_act", "quantize_act_normed", "vec_dot_q8", "vec_dot_f32", "matmul",
     "rope_table", "argmax", "OracleModel", "OracleSession", "prompt_lookup", "speculative_generate",
     "ref_loader", "nrmse", "cosine",
@@ -62,6 +62,13 @@ _SIGS = {
     "jfo_quantize_act_normed": (None, [POINTER(c_float), POINTER(c_float), c_int64, c_float, POINTER(c_int8),
                                        POINTER(c_float), POINTER(c_int16)]),
     "jfo_vec_dot_q8": (c_double, [c_int32, c_void_p, POINTER(c_int8), POINTER(c_float), POINTER(c_int16), c_int64]),
+    "jfo_act_block": (c_int32, [c_int32]),
+    "jfo_quantize_act_blk": (None, [POINTER(c_float), c_int64, c_int32, POINTER(c_int8), POINTER(c_float),
+                                    POINTER(c_int16)]),
+    "jfo_quantize_act_normed_blk": (None, [POINTER(c_float), POINTER(c_float), c_int64, c_float, c_int32,
+                                           POINTER(c_int8), POINTER(c_float), POINTER(c_int16)]),
+    "jfo_vec_dot_q8_blk": (c_double, [c_int32, c_void_p, POINTER(c_int8), POINTER(c_float), POINTER(c_int16), c_int64,
+                                      c_int32]),
     "jfo_vec_dot_f32": (c_double, [c_int32, c_void_p, POINTER(c_float), c_int64]),
     "jfo_matmul": (c_int32, [c_int32, c_void_p, c_int64, c_int64, POINTER(c_float), c_int64, POINTER(c_float), c_int32,
                              c_int32]),
@@ -128,33 +135,43 @@ def dequantize_row(type_id: int, data: bytes, n: int) -> np.ndarray:
     return out
 
 
-def quantize_act(x: np.ndarray):
+def act_block(type_id: int) -> int:
+    """Activation block of a quantized matmul input: 32 for Q8_0 weights, else 256."""
+    return int(lib().jfo_act_block(type_id))
+
+
+def quantize_act(x: np.ndarray, blk: int = 256):
+    """Codes, scales (one per blk values) and 16-value code sums of x."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     n = x.size
     q = np.zeros(n, dtype=np.int8)
-    d = np.zeros(n // 256, dtype=np.float32)
+    d = np.zeros(n // blk, dtype=np.float32)
     s = np.zeros(n // 16, dtype=np.int16)
-    lib().jfo_quantize_act(_fp(x), n, q.ctypes.data_as(POINTER(c_int8)), _fp(d), s.ctypes.data_as(POINTER(c_int16)))
+    lib().jfo_quantize_act_blk(_fp(x), n, blk, q.ctypes.data_as(POINTER(c_int8)), _fp(d),
+                               s.ctypes.data_as(POINTER(c_int16)))
     return q, d, s
 
 
-def quantize_act_normed(x: np.ndarray, gain: np.ndarray, eps: float):
+def quantize_act_normed(x: np.ndarray, gain: np.ndarray, eps: float, blk: int = 256):
     """Codes, block scales and 16-value sums of RMSNorm(x) * gain as the engine stages them."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     g = np.ascontiguousarray(gain, dtype=np.float32)
     n = x.size
     q = np.zeros(n, dtype=np.int8)
-    d = np.zeros(n // 256, dtype=np.float32)
+    d = np.zeros(n // blk, dtype=np.float32)
     s = np.zeros(n // 16, dtype=np.int16)
-    lib().jfo_quantize_act_normed(_fp(x), _fp(g), n, eps, q.ctypes.data_as(POINTER(c_int8)), _fp(d),
-                                  s.ctypes.data_as(POINTER(c_int16)))
+    lib().jfo_quantize_act_normed_blk(_fp(x), _fp(g), n, eps, blk, q.ctypes.data_as(POINTER(c_int8)), _fp(d),
+                                      s.ctypes.data_as(POINTER(c_int16)))
     return q, d, s
 
 
-def vec_dot_q8(type_id: int, row: bytes, q: np.ndarray, d: np.ndarray, s: np.ndarray) -> float:
+def vec_dot_q8(type_id: int, row: bytes, q: np.ndarray, d: np.ndarray, s: np.ndarray, blk: int | None = None) -> float:
+    """Dot of one encoded weight row with quantized activations (blocks of blk
+    values; default: the weight type's rule, act_block(type_id))."""
     buf = ctypes.create_string_buffer(bytes(row), len(row))
-    return lib().jfo_vec_dot_q8(type_id, buf, q.ctypes.data_as(POINTER(c_int8)), _fp(d),
-                                s.ctypes.data_as(POINTER(c_int16)), q.size)
+    b = act_block(type_id) if blk is None else blk
+    return lib().jfo_vec_dot_q8_blk(type_id, buf, q.ctypes.data_as(POINTER(c_int8)), _fp(d),
+                                    s.ctypes.data_as(POINTER(c_int16)), q.size, b)
 
 
 def vec_dot_f32(type_id: int, row: bytes, x: np.ndarray) -> float:
@@ -164,7 +181,8 @@ def vec_dot_f32(type_id: int, row: bytes, x: np.ndarray) -> float:
 
 
 def matmul(type_id: int, w: bytes | int, n: int, rows: int, x: np.ndarray, mode: int = MODE_Q8, threads: int = 8):
-    """y[t, r] = W[r] . x[t]; w may be bytes or a raw address."""
+    """y[t, r] = W[r] . x[t]; w may be bytes or a raw address. MODE_Q8 quantizes
+    the rows by the weight type's block rule (act_block)."""
     x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
     y = np.zeros((x.shape[0], rows), dtype=np.float32)
     keep = None

@@ -60,20 +60,21 @@ int jfo_matmul(int type, const void * w, int64_t n, int64_t rows,
     if (!jfo_type_block(type, &be, &bb) || n % be != 0) return -1;
     const size_t row_bytes = (size_t) (n / be) * bb;
     const int quantized = mode == JFO_MODE_Q8 && type != JFO_F32 && type != JFO_F16;
+    const int blk = jfo_act_block(type);
     int8_t * q = NULL;
     float * d = NULL;
     int16_t * s16 = NULL;
     if (quantized) {
         if (n % 256 != 0) return -1;
         q = malloc((size_t) (tokens * n));
-        d = malloc(sizeof(float) * (size_t) (tokens * n / 256));
+        d = malloc(sizeof(float) * (size_t) (tokens * n / blk));
         s16 = malloc(sizeof(int16_t) * (size_t) (tokens * n / 16));
         if (!q || !d || !s16) {
             free(q); free(d); free(s16);
             return -1;
         }
         for (int64_t t = 0; t < tokens; ++t) {
-            jfo_quantize_act(x + t * n, n, q + t * n, d + t * n / 256, s16 + t * n / 16);
+            jfo_quantize_act_blk(x + t * n, n, blk, q + t * n, d + t * n / blk, s16 + t * n / 16);
         }
     }
 #ifdef _OPENMP
@@ -83,7 +84,7 @@ int jfo_matmul(int type, const void * w, int64_t n, int64_t rows,
         const uint8_t * row = (const uint8_t *) w + (size_t) r * row_bytes;
         for (int64_t t = 0; t < tokens; ++t) {
             const double v = quantized
-                ? jfo_vec_dot_q8(type, row, q + t * n, d + t * n / 256, s16 + t * n / 16, n)
+                ? jfo_vec_dot_q8_blk(type, row, q + t * n, d + t * n / blk, s16 + t * n / 16, n, blk)
                 : jfo_vec_dot_f32(type, row, x + t * n, n);
             y[t * rows + r] = (float) v;
         }
@@ -95,10 +96,11 @@ int jfo_matmul(int type, const void * w, int64_t n, int64_t rows,
     return 0;
 }
 
-int jfo_matmul_q8(int type, const void * w, int64_t n, int64_t rows, const int8_t * q, const float * d,
-                  const int16_t * s16, int64_t tokens, float * y, int threads) {
+int jfo_matmul_q8_blk(int type, const void * w, int64_t n, int64_t rows, const int8_t * q, const float * d,
+                      const int16_t * s16, int64_t tokens, float * y, int blk, int threads) {
     uint32_t be = 0, bb = 0;
     if (!jfo_type_block(type, &be, &bb) || n % 256 != 0 || type == JFO_F32 || type == JFO_F16) return -1;
+    if (blk != jfo_act_block(type)) return -1;
     const size_t row_bytes = (size_t) (n / be) * bb;
 #ifdef _OPENMP
 #pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
@@ -106,11 +108,17 @@ int jfo_matmul_q8(int type, const void * w, int64_t n, int64_t rows, const int8_
     for (int64_t r = 0; r < rows; ++r) {
         const uint8_t * row = (const uint8_t *) w + (size_t) r * row_bytes;
         for (int64_t t = 0; t < tokens; ++t) {
-            y[t * rows + r] = (float) jfo_vec_dot_q8(type, row, q + t * n, d + t * n / 256, s16 + t * n / 16, n);
+            y[t * rows + r] =
+                (float) jfo_vec_dot_q8_blk(type, row, q + t * n, d + t * n / blk, s16 + t * n / 16, n, blk);
         }
     }
     (void) threads;
     return 0;
+}
+
+int jfo_matmul_q8(int type, const void * w, int64_t n, int64_t rows, const int8_t * q, const float * d,
+                  const int16_t * s16, int64_t tokens, float * y, int threads) {
+    return jfo_matmul_q8_blk(type, w, n, rows, q, d, s16, tokens, y, jfo_act_block(type), threads);
 }
 
 static float rms_scale(const float * x, int64_t n, float eps) {
@@ -120,15 +128,45 @@ static float rms_scale(const float * x, int64_t n, float eps) {
     return 1.0f / sqrtf(mean + eps);
 }
 
-void jfo_quantize_act_normed(const float * x, const float * gain, int64_t n, float eps, int8_t * q, float * d,
-                             int16_t * s16) {
+void jfo_quantize_act_normed_blk(const float * x, const float * gain, int64_t n, float eps, int blk, int8_t * q,
+                                 float * d, int16_t * s16) {
     float * v = calloc((size_t) n, sizeof(float));
     if (!v) return;
     for (int64_t i = 0; i < n; ++i) v[i] = x[i] * gain[i];
-    jfo_quantize_act(v, n, q, d, s16);
+    /* the codes of x * gain with the unrounded block scales, then each scale times the row's 1/rms */
     const float scale = rms_scale(x, n, eps);
-    for (int64_t b = 0; b < n / 256; ++b) d[b] = d[b] * scale;
+    if (blk == 32) {
+        for (int64_t b = 0; b < n / 32; ++b) {
+            float amax = 0.0f;
+            for (int i = 0; i < 32; ++i) {
+                const float a = fabsf(v[b * 32 + i]);
+                if (a > amax) amax = a;
+            }
+            const float db = amax / 127.0f;
+            const float id = db > 0.0f ? 1.0f / db : 0.0f;
+            for (int i = 0; i < 32; ++i) {
+                float r = roundf(v[b * 32 + i] * id);
+                if (r > 127.0f) r = 127.0f;
+                if (r < -127.0f) r = -127.0f;
+                q[b * 32 + i] = (int8_t) r;
+            }
+            d[b] = jfo_f16_to_f32(jfo_f32_to_f16(db * scale));
+        }
+        for (int64_t g = 0; g < n / 16; ++g) {
+            int sum = 0;
+            for (int i = 0; i < 16; ++i) sum += q[g * 16 + i];
+            s16[g] = (int16_t) sum;
+        }
+    } else {
+        jfo_quantize_act_blk(v, n, 256, q, d, s16);
+        for (int64_t b = 0; b < n / 256; ++b) d[b] = d[b] * scale;
+    }
     free(v);
+}
+
+void jfo_quantize_act_normed(const float * x, const float * gain, int64_t n, float eps, int8_t * q, float * d,
+                             int16_t * s16) {
+    jfo_quantize_act_normed_blk(x, gain, n, eps, 256, q, d, s16);
 }
 
 static void rms_norm(const float * x, const jfo_tensor * gain, int64_t n, float eps, float * out) {
@@ -158,66 +196,86 @@ static void add_bias(float * y, const jfo_tensor * b, int64_t tokens, int64_t n)
 }
 
 /*
- * Input rows of one or more matmuls. In JFO_MODE_Q8 they are quantized once,
- * the way the HIP engine stages them: plain rows as jfo_quantize_act; rows
- * behind an RMSNorm as jfo_quantize_act_normed (codes of x*gain, block
- * scales times the row's 1/rms). Float weights and JFO_MODE_EXACT use the
- * float rows ((x*rms_scale)*gain for normed inputs, as the reference graph).
+ * Input rows of one or more matmuls. In JFO_MODE_Q8 they are quantized the
+ * way the HIP engine stages them, once per activation block size a consumer
+ * needs (jfo_act_block: 32 values for Q8_0 weights, 256 for the K-quants):
+ * plain rows as jfo_quantize_act_blk; rows behind an RMSNorm as
+ * jfo_quantize_act_normed_blk (codes of x*gain, block scales times the row's
+ * 1/rms). Float weights and JFO_MODE_EXACT use the float rows
+ * ((x*rms_scale)*gain for normed inputs, as the reference graph).
  */
-typedef struct act_rows {
-    const float * x;   /* float rows (normed when a gain was given) */
+typedef struct act_q8 {
     int8_t * q;
     float * d;
     int16_t * s16;
+} act_q8;
+
+typedef struct act_rows {
+    const float * x;    /* float rows (normed when a gain was given) */
+    const float * raw;  /* the rows before the norm */
+    float * gain;       /* dequantized gain, NULL for plain rows */
+    int quantize;       /* JFO_MODE_Q8 session */
+    act_q8 blk256, blk32;
     int64_t n, tokens;
 } act_rows;
 
 static void act_prepare(const jfo_session * s, act_rows * a, const float * x, const jfo_tensor * gain, int64_t n,
                         int64_t tokens, float * xn) {
+    memset(a, 0, sizeof(*a));
     a->n = n;
     a->tokens = tokens;
-    a->q = NULL;
-    a->d = NULL;
-    a->s16 = NULL;
+    a->raw = x;
+    a->quantize = s->mode == JFO_MODE_Q8 && n % 256 == 0;
     if (gain) {
         for (int64_t t = 0; t < tokens; ++t) rms_norm(x + t * n, gain, n, s->m->rms_eps, xn + t * n);
         a->x = xn;
+        a->gain = malloc(sizeof(float) * (size_t) n);
+        jfo_dequantize_row(gain->type, gain->data, a->gain, n);
     } else {
         a->x = x;
     }
-    if (s->mode != JFO_MODE_Q8 || n % 256 != 0) return;
-    a->q = malloc((size_t) (tokens * n));
-    a->d = malloc(sizeof(float) * (size_t) (tokens * n / 256));
-    a->s16 = malloc(sizeof(int16_t) * (size_t) (tokens * n / 16));
-    float * g = NULL;
-    if (gain) {
-        g = malloc(sizeof(float) * (size_t) n);
-        jfo_dequantize_row(gain->type, gain->data, g, n);
-    }
+}
+
+/* The rows quantized in blocks of blk values (computed on first use). */
+static const act_q8 * act_quantized(const jfo_session * s, act_rows * a, int blk) {
+    act_q8 * v = blk == 32 ? &a->blk32 : &a->blk256;
+    if (v->q) return v;
+    const int64_t n = a->n, tokens = a->tokens;
+    v->q = malloc((size_t) (tokens * n));
+    v->d = malloc(sizeof(float) * (size_t) (tokens * n / blk));
+    v->s16 = malloc(sizeof(int16_t) * (size_t) (tokens * n / 16));
     for (int64_t t = 0; t < tokens; ++t) {
-        if (gain) {
-            jfo_quantize_act_normed(x + t * n, g, n, s->m->rms_eps, a->q + t * n, a->d + t * n / 256,
-                                    a->s16 + t * n / 16);
+        if (a->gain) {
+            jfo_quantize_act_normed_blk(a->raw + t * n, a->gain, n, s->m->rms_eps, blk, v->q + t * n,
+                                        v->d + t * n / blk, v->s16 + t * n / 16);
         } else {
-            jfo_quantize_act(x + t * n, n, a->q + t * n, a->d + t * n / 256, a->s16 + t * n / 16);
+            jfo_quantize_act_blk(a->raw + t * n, n, blk, v->q + t * n, v->d + t * n / blk, v->s16 + t * n / 16);
         }
     }
-    free(g);
+    return v;
 }
 
 static void act_release(act_rows * a) {
-    free(a->q);
-    free(a->d);
-    free(a->s16);
-    a->q = NULL;
-    a->d = NULL;
-    a->s16 = NULL;
+    act_q8 * v[2] = {&a->blk256, &a->blk32};
+    for (int i = 0; i < 2; ++i) {
+        free(v[i]->q);
+        free(v[i]->d);
+        free(v[i]->s16);
+        v[i]->q = NULL;
+        v[i]->d = NULL;
+        v[i]->s16 = NULL;
+    }
+    free(a->gain);
+    a->gain = NULL;
 }
 
-static int linear(const jfo_session * s, const jfo_tensor * w, const act_rows * a, float * y) {
+static int linear(const jfo_session * s, const jfo_tensor * w, act_rows * a, float * y) {
     const int float_weights = w->type == JFO_F32 || w->type == JFO_F16;
-    if (a->q && !float_weights) {
-        return jfo_matmul_q8(w->type, w->data, w->ne0, w->ne1, a->q, a->d, a->s16, a->tokens, y, s->threads);
+    if (a->quantize && !float_weights) {
+        const int blk = jfo_act_block(w->type);
+        const act_q8 * v = act_quantized(s, a, blk);
+        return jfo_matmul_q8_blk(w->type, w->data, w->ne0, w->ne1, v->q, v->d, v->s16, a->tokens, y, blk,
+                                 s->threads);
     }
     return jfo_matmul(w->type, w->data, w->ne0, w->ne1, a->x, a->tokens, y, JFO_MODE_EXACT, s->threads);
 }

@@ -202,27 +202,36 @@ int jfo_dequantize_row(int type, const void * src, float * dst, int64_t n) {
     }
 }
 
-void jfo_quantize_act(const float * x, int64_t n, int8_t * q, float * d, int16_t * s16) {
-    for (int64_t b = 0; b < n / 256; ++b) {
-        const float * xb = x + b * 256;
+int jfo_act_block(int type) { return type == JFO_Q8_0 ? 32 : 256; }
+
+void jfo_quantize_act_blk(const float * x, int64_t n, int blk, int8_t * q, float * d, int16_t * s16) {
+    for (int64_t b = 0; b < n / blk; ++b) {
+        const float * xb = x + b * blk;
         float amax = 0.0f;
-        for (int i = 0; i < 256; ++i) {
+        for (int i = 0; i < blk; ++i) {
             const float a = fabsf(xb[i]);
             if (a > amax) amax = a;
         }
         const float db = amax / 127.0f;
         const float id = db > 0.0f ? 1.0f / db : 0.0f;
-        int sums[16] = {0};
-        for (int i = 0; i < 256; ++i) {
+        for (int i = 0; i < blk; ++i) {
             float r = roundf(xb[i] * id);
             if (r > 127.0f) r = 127.0f;
             if (r < -127.0f) r = -127.0f;
-            q[b * 256 + i] = (int8_t) r;
-            sums[i / 16] += (int) r;
+            q[b * blk + i] = (int8_t) r;
         }
-        d[b] = db;
-        for (int g = 0; g < 16; ++g) s16[b * 16 + g] = (int16_t) sums[g];
+        /* 32-value blocks store their scale as f16 (GGML's q8_0 / q8_1 block) */
+        d[b] = blk == 32 ? jfo_f16_to_f32(jfo_f32_to_f16(db)) : db;
     }
+    for (int64_t g = 0; g < n / 16; ++g) {
+        int sum = 0;
+        for (int i = 0; i < 16; ++i) sum += q[g * 16 + i];
+        s16[g] = (int16_t) sum;
+    }
+}
+
+void jfo_quantize_act(const float * x, int64_t n, int8_t * q, float * d, int16_t * s16) {
+    jfo_quantize_act_blk(x, n, 256, q, d, s16);
 }
 
 /*
@@ -241,19 +250,26 @@ static void unpack_kquant(int type, const uint8_t * p, uint8_t * v) {
     }
 }
 
-double jfo_vec_dot_q8(int type, const void * row, const int8_t * q, const float * d,
-                      const int16_t * s16, int64_t n) {
+/* Dot of one Q8_0 row with activation blocks of 32 values (jfo.h). */
+static double vec_dot_q8_32(int type, const uint8_t * p, const int8_t * q, const float * d, int64_t n) {
+    double sum = 0.0;
+    if (type != JFO_Q8_0) return 0.0;
+    for (int64_t b = 0; b < n / 32; ++b, p += 34) {
+        int dot = 0;
+        for (int i = 0; i < 32; ++i) dot += (int) (int8_t) p[2 + i] * q[b * 32 + i];
+        sum += (double) d[b] * (double) f16_at(p) * (double) dot;
+    }
+    return sum;
+}
+
+double jfo_vec_dot_q8_blk(int type, const void * row, const int8_t * q, const float * d, const int16_t * s16,
+                          int64_t n, int blk) {
     const uint8_t * p = (const uint8_t *) row;
+    if (blk != jfo_act_block(type)) return 0.0;
+    if (blk == 32) return vec_dot_q8_32(type, p, q, d, n);
     uint8_t v[256];
     double sum = 0.0;
     switch (type) {
-    case JFO_Q8_0:
-        for (int64_t b = 0; b < n / 32; ++b, p += 34) {
-            int isum = 0;
-            for (int i = 0; i < 32; ++i) isum += (int) (int8_t) p[2 + i] * q[b * 32 + i];
-            sum += (double) d[b / 8] * ((double) f16_at(p) * (double) isum);
-        }
-        return sum;
     case JFO_Q4_K:
         for (int64_t b = 0; b < n / 256; ++b, p += 144) {
             const double dw = f16_at(p), dmin = f16_at(p + 2);
@@ -300,6 +316,11 @@ double jfo_vec_dot_q8(int type, const void * row, const int8_t * q, const float 
     default:
         return 0.0;
     }
+}
+
+
+double jfo_vec_dot_q8(int type, const void * row, const int8_t * q, const float * d, const int16_t * s16, int64_t n) {
+    return jfo_vec_dot_q8_blk(type, row, q, d, s16, n, jfo_act_block(type));
 }
 
 double jfo_vec_dot_f32(int type, const void * row, const float * x, int64_t n) {

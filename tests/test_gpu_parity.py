@@ -79,7 +79,7 @@ def test_dequantize_bit_exact(typed):
 def test_matmul_matches_oracle(typed, n_tok):
     t, model, engine = typed
     rng = np.random.default_rng(n_tok)
-    for name in ("blk.0.attn_q.weight", "blk.2.ffn_down.weight"):
+    for name in ("blk.0.attn_q.weight", "blk.2.ffn_down.weight", "blk.1.attn_output.weight"):
         info = model.tensor(name)
         cols, rows = info["shape"]
         x = rng.standard_normal((n_tok, cols)).astype(np.float32)
@@ -100,7 +100,7 @@ def test_wide_matmul_rows_equal_single_rows(typed, n_tok):
     row must equal the same row computed alone (the decode path), bit for bit."""
     t, model, engine = typed
     rng = np.random.default_rng(100 + n_tok)
-    for name in ("blk.0.attn_q.weight", "blk.1.ffn_down.weight"):
+    for name in ("blk.0.attn_q.weight", "blk.1.ffn_down.weight", "blk.2.attn_output.weight"):
         cols, rows = model.tensor(name)["shape"]
         x = rng.standard_normal((n_tok, cols)).astype(np.float32)
         wide = engine.matmul(name, x, rows)

@@ -295,6 +295,40 @@ def test_activation_quantization_round_trip():
     assert np.array_equal(s, q.astype(np.int32).reshape(-1, 16).sum(axis=1))
 
 
+def test_activation_quantization_32_value_blocks():
+    """The 32-value rule (GGML's q8_0 / q8_1 block): per block d' = amax/127,
+    codes roundf(x / d') from the f32 scale, stored scale d' rounded to f16
+    (numpy's IEEE conversion); every code within half a step of x plus the
+    scale's f16 rounding, and 16-value code sums."""
+    rng = np.random.default_rng(31)
+    x = rng.normal(0, 2, 1024).astype(np.float32)
+    x[64:96] = 0.0                      # a zero block
+    x[96:128] *= np.float32(1e-3)       # a small block: f16 scale well inside the normal range
+    x[128:160] = np.float32(-7.0)       # a constant block: every code -127
+    q, d, s = jo.quantize_act(x, 32)
+    assert d.size == 32
+    for b in range(32):
+        blk = x[32 * b:32 * b + 32]
+        d_raw = np.float32(np.abs(blk).max()) / np.float32(127.0)
+        assert d[b] == np.float32(np.float16(d_raw)), f"block {b}"
+        codes = q[32 * b:32 * b + 32].astype(np.float64)
+        if d_raw == 0:
+            assert not codes.any()
+            continue
+        assert np.abs(codes).max() == 127
+        assert np.array_equal(codes, np.clip(np.round(blk.astype(np.float64) / float(d_raw)), -127, 127)) or \
+            np.abs(codes - blk / float(d_raw)).max() <= 0.5 + 1e-5
+        err = np.abs(codes * float(d[b]) - blk)
+        assert err.max() <= 0.5 * float(d_raw) * (1 + 1e-5) + 127 * abs(float(d[b]) - float(d_raw))
+    assert np.all(q[128:160] == -127)
+    assert np.array_equal(s, q.astype(np.int32).reshape(-1, 16).sum(axis=1))
+    # 32-value blocks never quantize more coarsely than the 256-value rule
+    q256, d256, _ = jo.quantize_act(x)
+    e32 = np.abs(q.astype(np.float64) * np.repeat(d.astype(np.float64), 32) - x)
+    e256 = np.abs(q256.astype(np.float64) * np.repeat(d256.astype(np.float64), 256) - x)
+    assert e32.mean() < e256.mean()
+
+
 def test_normalized_activation_quantization():
     """jfo_quantize_act_normed against the definition of the rule: the codes
     are those of x * gain (one scale per 256 values, amax / 127), each block
@@ -325,13 +359,30 @@ def test_normalized_activation_quantization():
     # the unnormalized rule on x * gain gives the same codes
     q2, d2, _ = jo.quantize_act(v)
     assert np.array_equal(q, q2) and np.array_equal(d, (d2 * rs).astype(np.float32))
+    # 32-value blocks: the codes of x * gain per 32 values, the scale
+    # (amax / 127 * rs) rounded to f16
+    q32, d32, s32 = jo.quantize_act_normed(x, gain, eps, 32)
+    for b in range(n // 32):
+        blk = slice(32 * b, 32 * b + 32)
+        d_raw = np.float32(np.abs(v[blk]).max()) / np.float32(127.0)
+        assert d32[b] == np.float32(np.float16(np.float32(d_raw * rs))), f"block {b}"
+        if d_raw > 0:
+            assert np.abs(q32[blk].astype(np.float64) - v[blk] / float(d_raw)).max() <= 0.5 + 1e-5
+            err = np.abs(q32[blk].astype(np.float64) * float(d32[b]) - normed[blk])
+            assert err.max() <= 0.5 * float(d_raw * rs) * (1 + 1e-5) + 127 * abs(float(d32[b]) - float(d_raw * rs))
+        else:
+            assert not q32[blk].any()
+    assert np.array_equal(s32, q32.astype(np.int32).reshape(-1, 16).sum(axis=1))
 
 
 @pytest.mark.parametrize("type_id", [jo.Q8_0, jo.Q2_K, jo.Q4_K, jo.Q6_K])
 def test_quantized_dot_equals_float64_brute_force(type_id):
     """vec_dot_q8 = sum over blocks of exact integer sums -> equals
-    sum_i dequant(w)_i * (q_i * d_blk) evaluated in float64."""
-    rng = np.random.default_rng(type_id)
+    sum_i dequant(w)_i * (q_i * d_blk) evaluated in float64, with the type's
+    activation blocks (256 values for the K-quants, 32 for Q8_0: GGML's
+    q8_0 x q8_0 rule)."""
+    blk = jo.act_block(type_id)
+    rng = np.random.default_rng(type_id + blk)
     n = 1024
     _, bb = jo.block(type_id)
     e, _ = jo.block(type_id)
@@ -351,13 +402,24 @@ def test_quantized_dot_equals_float64_brute_force(type_id):
     row = bytes(row)
     w = deq(type_id, row).astype(np.float64)
     x = rng.normal(0, 1, n).astype(np.float32)
-    q, d, s = jo.quantize_act(x)
-    xq = q.astype(np.float64) * np.repeat(d.astype(np.float64), 256)
+    q, d, s = jo.quantize_act(x, blk)
+    xq = q.astype(np.float64) * np.repeat(d.astype(np.float64), blk)
     expected = float(w @ xq)
-    got = jo.vec_dot_q8(type_id, row, q, d, s)
+    got = jo.vec_dot_q8(type_id, row, q, d, s, blk)
     assert got == pytest.approx(expected, rel=1e-6, abs=1e-6 * float(np.abs(w) @ np.abs(xq)))
     exact = jo.vec_dot_f32(type_id, row, x)
     assert exact == pytest.approx(float(w @ x.astype(np.float64)), rel=1e-9, abs=1e-9)
+    # the wrong block size is refused (Q8_0 takes 32-value blocks, the K-quants 256)
+    other = 256 if blk == 32 else 32
+    q2, d2, s2 = jo.quantize_act(x, other)
+    assert jo.vec_dot_q8(type_id, row, q2, d2, s2, other) == 0.0
+    if blk == 32:
+        # a planted mistake the comparison above must catch: the scales of two blocks exchanged
+        bad = d.copy()
+        bad[[3, 4]] = bad[[4, 3]]
+        assert bad[3] != bad[4]
+        wrong = jo.vec_dot_q8(type_id, row, q, bad, s, blk)
+        assert abs(wrong - expected) > 1e-6 * float(np.abs(w) @ np.abs(xq))
 
 
 def test_matmul_modes_agree_with_brute_force():
