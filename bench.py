@@ -16,9 +16,11 @@ and `value` = aggregate decode tokens / decode wall time.
 Beside it: greedy decode at batch 1 (one step = one token through all 28
 layers, the head and the on-GPU argmax), draft verification (k = 4) timed
 with forced acceptance 0..k, a 1024-token prefill, the same concurrent run on
-repetitive prompts (drafts proposed and verified), the 1.5B workloads of the
-prompt-lookup configuration (its prompt recipe and forced-acceptance
-verify), and (`--configs all`) the 14B and 32B step shapes.
+repetitive prompts (drafts proposed and verified), end-to-end speculative
+generation at the reference's acceptance rates (68.8 % and 9.5 %, drafts
+from the recorded greedy continuation), the 1.5B workloads of the
+prompt-lookup configuration (its prompt recipe, forced-acceptance verify and
+the same acceptance-rate runs), and the 14B and 32B step shapes.
 
 Prints one JSON line. `roofline` is computed from per-launch HIP-event
 durations of the headline's dominant kernel measured in this run;
@@ -149,6 +151,73 @@ def forced_verify(session, tok, k, vocab, reps):
     return out, cont
 
 
+# The reference's prompt-lookup acceptance rates (docs/benchmarks/2026-07-31-runtime-transport-speculation.md:34-39):
+# 68.8 % on its repetitive fixture, 9.5 % on prose.
+REFERENCE_ACCEPTANCE = (0.688, 0.095)
+
+
+def keep_probability(rate: float, k: int) -> float:
+    """Per-token probability p that a draft token is the true one such that the
+    expected accepted prefix of a k-token draft, sum(p^i, i=1..k), is rate * k."""
+    lo, hi = 0.0, 1.0
+    for _ in range(60):
+        mid = (lo + hi) / 2
+        if sum(mid ** i for i in range(1, k + 1)) < rate * k:
+            lo = mid
+        else:
+            hi = mid
+    return (lo + hi) / 2
+
+
+class RecordedDraft:
+    """A draft strategy for timing speculation at a chosen acceptance rate (the
+    shape of the reference harness's FixedDraft, generation_runner_test.cpp:
+    108-119): it proposes the model's recorded greedy continuation after the
+    history, each draft token kept with a seeded probability p and otherwise
+    replaced by a wrong id, so that acceptance follows p whatever the weights."""
+
+    def __init__(self, prompt_len: int, continuation: list[int], p: float, vocab: int, seed: int):
+        self.prompt_len, self.cont, self.p, self.vocab = prompt_len, continuation, p, vocab
+        self.rng = np.random.default_rng(seed)
+
+    def __call__(self, history, max_tokens):
+        i = len(history) - self.prompt_len  # tokens generated so far
+        truth = self.cont[i:i + max_tokens]
+        return [t if self.rng.random() < self.p else (t + 1 + j) % self.vocab for j, t in enumerate(truth)]
+
+
+def spec_rate_runs(engine, prompt, n_tokens: int, k: int, vocab: int, seed: int) -> dict:
+    """Plain greedy generation of n_tokens, then speculative generation whose
+    drafts are the recorded continuation at the reference's acceptance rates:
+    tok/s, target decode passes and the measured acceptance of each."""
+    engine.generate(prompt, 8)  # graphs of the shapes below
+    plain = engine.generate(prompt, n_tokens)
+    out = {"tokens": n_tokens, "draft_k": k,
+           "plain": {"decode_tok_s": round(plain.decode_tokens_per_second, 1), "passes": plain.target_decode_passes,
+                     "itl_ms": round(plain.inter_token_latency_ms, 4)}}
+    for rate in REFERENCE_ACCEPTANCE:
+        p = keep_probability(rate, k)
+        engine.generate_with_draft(prompt, 16, k, RecordedDraft(len(prompt), plain.sampled_tokens, p, vocab, seed))
+        spec = engine.generate_with_draft(prompt, n_tokens, k,
+                                          RecordedDraft(len(prompt), plain.sampled_tokens, p, vocab, seed))
+        if spec.sampled_tokens != plain.sampled_tokens:
+            raise RuntimeError("speculative generation changed the greedy tokens")
+        measured = spec.speculative_accepted_tokens / max(1, spec.speculative_draft_tokens)
+        out[f"acceptance_{rate:.3f}"] = {
+            "decode_tok_s": round(spec.decode_tokens_per_second, 1),
+            "speedup_vs_plain": round(spec.decode_tokens_per_second / plain.decode_tokens_per_second, 3),
+            "passes": spec.target_decode_passes,
+            "pass_reduction": round(1.0 - spec.target_decode_passes / plain.target_decode_passes, 3),
+            "drafted": spec.speculative_draft_tokens, "accepted": spec.speculative_accepted_tokens,
+            "measured_acceptance": round(measured, 3), "keep_probability": round(p, 4),
+            "same_tokens_as_plain": True,
+        }
+        log(f"speculation at acceptance {rate:.3f} (measured {measured:.3f}): {spec.decode_tokens_per_second:.1f} "
+            f"tok/s vs plain {plain.decode_tokens_per_second:.1f}, passes {spec.target_decode_passes} vs "
+            f"{plain.target_decode_passes}")
+    return out
+
+
 def synthesize(wl, seed):
     t0 = time.perf_counter()
     model = jf.Model.synthesize(wl.model, type_linear=wl.type_linear, type_embd=wl.type_embd,
@@ -176,7 +245,10 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--batch-wait-us", type=int, default=500, help="continuous-batching wait for a batch to fill")
     ap.add_argument("--configs", choices=["default", "all", "none"], default="default",
-                    help="other workloads' legs: default = the 1.5B prompt-lookup legs; all = also 14B and 32B")
+                    help="other workloads' legs: the 1.5B prompt-lookup legs and the 14B and 32B step shapes "
+                         "(all: the same)")
+    ap.add_argument("--spec-tokens", type=int, default=256,
+                    help="tokens of the speculative runs at the reference's acceptance rates")
     ap.add_argument("--copy-probe-mib", type=int, default=256,
                     help="size of the device-to-device copy that calibrates PMC byte counters (0: none)")
     ap.add_argument("--trace-decode", action="store_true",
@@ -293,6 +365,9 @@ def main() -> int:
     log(f"concurrent decode x{conc}, repetitive prompts: {rep['tokens']} tokens in {rep['wall_ms']:.1f} ms = "
         f"{rep_tok_s:.1f} tok/s, {rep['passes']} passes, drafts accepted {rep['accepted']}/{rep['drafted']}")
 
+    # ---- end-to-end speculation at the reference's acceptance rates (drafts from the recorded continuation)
+    spec7 = spec_rate_runs(engine, cprompts[0], args.spec_tokens, k, cfg.n_vocab, args.seed + 500)
+
     parity = parity_sample(engine, model, cfg, args) if not args.no_cpu else None
     cpu = cpu_baseline(model, cfg, context, args) if not args.no_cpu else None
     engine.close()
@@ -301,7 +376,6 @@ def main() -> int:
     legs = {}
     if args.configs in ("default", "all"):
         legs.update(spec_legs(args))
-    if args.configs == "all":
         legs.update(large_legs(args))
 
     g2_roles = {role: {"us_per_launch": round(r["us_per_launch"], 2), "bytes_per_launch": round(r["bytes_per_launch"]),
@@ -343,6 +417,9 @@ def main() -> int:
             "verify_step_rows": f"{conc} sequences x {k + 1} rows",
             "note": "uniform-random prompts and random weights give no n-gram repeats, so no drafts are proposed",
         },
+        "speculation_at_reference_acceptance": dict(spec7, prompt=f"{context} uniform tokens (the headline's first)",
+                                                    reference="docs/benchmarks/2026-07-31-runtime-transport-"
+                                                              "speculation.md:34-39: 68.8% and 9.5% acceptance"),
         "concurrent_repetitive": {
             "prompts": "seeded 64-token segments, each twice in a row, 10% of positions substituted",
             "decode_tok_s": round(rep_tok_s, 2),
@@ -450,7 +527,9 @@ def spec_legs(args) -> dict:
     vb = sum(p["bytes"] for p in vprof)
     s.close()
     vmean = float(np.mean(list(verify_us.values())))
+    rates = spec_rate_runs(engine, prompt, wl2.output_tokens, wl2.draft_max, cfg.n_vocab, args.seed + 600)
     out[wl2.name] = {
+        "speculation_at_reference_acceptance": rates,
         "decode_tok_s": round((len(spec.sampled_tokens) - 1) / (spec.decode_ms * 1e-3), 1),
         "plain_decode_tok_s": round((len(plain.sampled_tokens) - 1) / (plain.decode_ms * 1e-3), 1),
         "same_tokens_as_plain": spec.sampled_tokens == plain.sampled_tokens,

@@ -403,6 +403,23 @@ typedef struct jfh_generation_stats {
     double decode_ms;
     uint32_t stopped;  /* 1: ended at an end-of-generation id (finish reason "stop"), 0: at max_tokens */
     uint32_t reserved;
+    /* GenerationResult's rates (native_inference.hpp:88-96) */
+    double inter_token_latency_ms;        /* decode_ms per token after the first */
+    double decode_tokens_per_second;      /* tokens after the first / decode_ms */
+    double end_to_end_tokens_per_second;  /* sampled tokens / (time to first token + decode_ms) */
+    /* PrefillMetrics (native_inference.hpp:71-78): the prompt's steps */
+    uint32_t prefill_plan_reused;         /* every prefill step shape's captured graph existed already */
+    uint32_t prefill_attention_matrix_cores; /* attention on MFMA (head dim 64 or 128) */
+    double prefill_planning_ms;           /* capturing and instantiating new step graphs */
+    double prefill_allocation_ms;         /* the session's KV cache allocation and clearing */
+    double prefill_host_input_ms;         /* building and uploading the step descriptors */
+    double prefill_compute_ms;            /* device time of the step graphs */
+    double prefill_output_read_ms;        /* device time of the result copies */
+    /* ExecutionBufferMetrics (native_inference.hpp:80-85) */
+    uint64_t kv_cache_bytes;              /* the session's F16 K/V cache */
+    uint64_t prefill_scratch_bytes;       /* engine workspace of one prefill chunk's rows */
+    uint64_t decode_scratch_bytes;        /* engine workspace of one decode row */
+    uint64_t prefill_host_input_bytes;    /* step descriptor bytes uploaded for the prompt */
 } jfh_generation_stats;
 
 /* GenerationRunner::run speculative loop (generation_runner.cpp:398-566) over
@@ -412,6 +429,23 @@ typedef struct jfh_generation_stats {
 jfh_status jfh_generate(jfh_engine * engine, const int32_t * prompt, uint32_t n_prompt, uint32_t max_tokens,
                         uint32_t draft_max, uint32_t max_ngram, uint32_t min_ngram, int32_t * out_tokens,
                         uint32_t * out_count, jfh_generation_stats * stats);
+
+/* A caller's draft strategy (DraftStrategy::propose,
+ * runtime/speculative/draft_strategy.hpp:9-17): given the history (prompt and
+ * generated ids, n of them), writes at most max_tokens proposed ids to out
+ * and returns how many it wrote (0: no draft this pass). */
+typedef uint32_t (*jfh_draft_propose_fn)(void * user, const uint32_t * history, size_t n, uint32_t max_tokens,
+                                         uint32_t * out);
+
+/* jfh_generate with drafts from a caller-supplied strategy: the runner of
+ * GenerationRunner::run (generation_runner.cpp:469-556) with any
+ * DraftStrategy, as the reference's harness installs FixedDraft
+ * (runtime/pipeline_parallel/generation_runner_test.cpp:108-119). propose is
+ * called on the calling thread before each verify pass (not after a rejected
+ * draft: that pass is the single-token recovery pass). */
+jfh_status jfh_generate_draft(jfh_engine * engine, const int32_t * prompt, uint32_t n_prompt, uint32_t max_tokens,
+                              uint32_t draft_max, jfh_draft_propose_fn propose, void * user, int32_t * out_tokens,
+                              uint32_t * out_count, jfh_generation_stats * stats);
 
 /* Continuous-batching generation: n_requests GenerationRunner loops (as
  * jfh_generate, one thread each) over one HIP stage executor wrapped in the

@@ -69,7 +69,18 @@ class GenerationStats(ctypes.Structure):
         ("speculative_draft_tokens", c_uint32), ("speculative_accepted_tokens", c_uint32),
         ("time_to_first_token_ms", c_double), ("decode_ms", c_double),
         ("stopped", c_uint32), ("reserved", c_uint32),
+        ("inter_token_latency_ms", c_double), ("decode_tokens_per_second", c_double),
+        ("end_to_end_tokens_per_second", c_double),
+        ("prefill_plan_reused", c_uint32), ("prefill_attention_matrix_cores", c_uint32),
+        ("prefill_planning_ms", c_double), ("prefill_allocation_ms", c_double), ("prefill_host_input_ms", c_double),
+        ("prefill_compute_ms", c_double), ("prefill_output_read_ms", c_double),
+        ("kv_cache_bytes", c_uint64), ("prefill_scratch_bytes", c_uint64), ("decode_scratch_bytes", c_uint64),
+        ("prefill_host_input_bytes", c_uint64),
     ]
+
+
+# jfh_draft_propose_fn: (user, history, n, max_tokens, out) -> count
+DraftProposeFn = ctypes.CFUNCTYPE(c_uint32, c_void_p, POINTER(c_uint32), c_size_t, c_uint32, POINTER(c_uint32))
 
 
 class PackageStats(ctypes.Structure):
@@ -155,6 +166,8 @@ SIGNATURES = {
     "jfh_tokenizer_vocab_size": (Status, [c_void_p, POINTER(c_uint32)]),
     "jfh_generate": (Status, [c_void_p, POINTER(c_int32), c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
                               POINTER(c_int32), POINTER(c_uint32), POINTER(GenerationStats)]),
+    "jfh_generate_draft": (Status, [c_void_p, POINTER(c_int32), c_uint32, c_uint32, c_uint32, DraftProposeFn, c_void_p,
+                                    POINTER(c_int32), POINTER(c_uint32), POINTER(GenerationStats)]),
     "jfh_generate_concurrent": (Status, [c_void_p, c_uint32, POINTER(c_int32), POINTER(c_uint32), c_uint32, c_uint32,
                                          c_uint32, c_uint32, c_uint32, POINTER(c_int32), POINTER(c_uint32),
                                          POINTER(GenerationStats), POINTER(c_double)]),

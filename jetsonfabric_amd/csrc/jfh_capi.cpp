@@ -106,6 +106,89 @@ jfh::ModelParams to_params(const jfh_model_params& p) {
     return q;
 }
 
+// A DraftStrategy whose proposals come from a caller's C function
+// (jfh_generate_draft); at most max_tokens of them are used.
+class CallbackDraft final : public jfh::runtime::speculative::DraftStrategy {
+public:
+    CallbackDraft(jfh_draft_propose_fn fn, void* user) : fn_(fn), user_(user) {}
+    std::vector<std::uint32_t> propose(const std::vector<std::uint32_t>& history,
+                                       std::size_t max_tokens) const override {
+        std::vector<std::uint32_t> out(max_tokens);
+        const uint32_t n = max_tokens ? fn_(user_, history.data(), history.size(), static_cast<uint32_t>(max_tokens),
+                                            out.data())
+                                      : 0;
+        out.resize(std::min<std::size_t>(n, max_tokens));
+        return out;
+    }
+
+private:
+    jfh_draft_propose_fn fn_;
+    void* user_;
+};
+
+// Generation statistics of one request: the runner's counters and times, the
+// rates of GenerationResult and the prefill / buffer metrics of the engine.
+void fill_stats(const jfh::Engine& engine, const jfh::runtime::GenerationResult& r, const jfh::PrefillMetrics& pm,
+                uint32_t capacity, uint32_t prompt_tokens, jfh_generation_stats& st) {
+    st = jfh_generation_stats{};
+    st.completion_tokens = static_cast<uint32_t>(r.completion_tokens);
+    st.target_decode_passes = static_cast<uint32_t>(r.target_decode_passes);
+    st.speculative_draft_tokens = static_cast<uint32_t>(r.speculative_draft_tokens);
+    st.speculative_accepted_tokens = static_cast<uint32_t>(r.speculative_accepted_tokens);
+    st.time_to_first_token_ms = r.time_to_first_token_ms;
+    st.decode_ms = r.decode_ms;
+    st.stopped = r.finish_reason == "stop" ? 1U : 0U;
+    // the first token comes from the prefill; the decode passes produce the rest
+    const double decoded = r.sampled_tokens.empty() ? 0.0 : static_cast<double>(r.sampled_tokens.size() - 1);
+    st.inter_token_latency_ms = decoded > 0.0 ? r.decode_ms / decoded : 0.0;
+    st.decode_tokens_per_second = decoded > 0.0 && r.decode_ms > 0.0 ? decoded / (r.decode_ms * 1e-3) : 0.0;
+    const double total_ms = r.time_to_first_token_ms + r.decode_ms;
+    st.end_to_end_tokens_per_second = total_ms > 0.0 ? static_cast<double>(r.sampled_tokens.size()) / (total_ms * 1e-3) : 0.0;
+    st.prefill_plan_reused = pm.plan_reused ? 1U : 0U;
+    st.prefill_attention_matrix_cores = pm.attention_matrix_cores ? 1U : 0U;
+    st.prefill_planning_ms = pm.planning_ms;
+    st.prefill_allocation_ms = pm.allocation_ms;
+    st.prefill_host_input_ms = pm.host_input_ms;
+    st.prefill_compute_ms = pm.compute_ms;
+    st.prefill_output_read_ms = pm.output_read_ms;
+    const jfh::BufferMetrics bm = engine.buffer_metrics(capacity, prompt_tokens, pm);
+    st.kv_cache_bytes = bm.kv_cache_bytes;
+    st.prefill_scratch_bytes = bm.prefill_scratch_bytes;
+    st.decode_scratch_bytes = bm.decode_scratch_bytes;
+    st.prefill_host_input_bytes = bm.prefill_host_input_bytes;
+}
+
+// One GenerationRunner loop over a HIP stage executor owning every layer.
+void generate_one(jfh_engine* engine, const int32_t* prompt, uint32_t n_prompt, uint32_t max_tokens,
+                  uint32_t draft_max, const jfh::runtime::speculative::DraftStrategy* draft, int32_t* out_tokens,
+                  uint32_t* out_count, jfh_generation_stats* stats) {
+    require(engine && prompt && n_prompt > 0 && max_tokens > 0 && out_tokens && out_count, "generation arguments are required");
+    require(draft_max <= 8, "draft length must be 0..8");
+    namespace rt = jfh::runtime;
+    const jfh::ModelParams& p = engine->engine->params();
+    rt::adapters::HipStageConfig cfg;
+    cfg.engine = engine->engine;
+    cfg.tokenizer = std::make_shared<rt::tokenization::IdTokenizer>(engine->engine->end_tokens());
+    cfg.ctx_size = static_cast<int>(std::min<uint64_t>(p.n_ctx, static_cast<uint64_t>(n_prompt) + max_tokens));
+    cfg.position = {0, 1};
+    cfg.layers = {0, static_cast<int>(p.n_layer)};
+    cfg.speculative_max_tokens = static_cast<int>(draft_max);
+    rt::adapters::HipStageExecutor executor(cfg);
+    rt::GenerationRequest req;
+    req.prompt.assign(prompt, prompt + n_prompt);
+    req.max_tokens = static_cast<int>(max_tokens);
+    req.layer_count = static_cast<int>(p.n_layer);
+    const rt::GenerationResult r =
+        rt::run_generation(executor, req, draft_max > 0 ? draft : nullptr, static_cast<int>(draft_max));
+    if (!r.ok) throw jfh::Error(jfh::Status::InvalidArgument, r.error_code + ": " + r.error_message);
+    for (size_t i = 0; i < r.sampled_tokens.size(); ++i) out_tokens[i] = static_cast<int32_t>(r.sampled_tokens[i]);
+    *out_count = static_cast<uint32_t>(r.sampled_tokens.size());
+    if (stats) {
+        fill_stats(*engine->engine, r, jfh::Engine::last_prefill_metrics(), static_cast<uint32_t>(cfg.ctx_size),
+                   n_prompt, *stats);
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -758,38 +841,20 @@ jfh_status jfh_generate(jfh_engine* engine, const int32_t* prompt, uint32_t n_pr
                         uint32_t draft_max, uint32_t max_ngram, uint32_t min_ngram, int32_t* out_tokens,
                         uint32_t* out_count, jfh_generation_stats* stats) {
     return guarded([&] {
-        require(engine && prompt && n_prompt > 0 && max_tokens > 0 && out_tokens && out_count, "generation arguments are required");
-        require(draft_max <= 8, "draft length must be 0..8");
-        namespace rt = jfh::runtime;
-        const jfh::ModelParams& p = engine->engine->params();
-        rt::adapters::HipStageConfig cfg;
-        cfg.engine = engine->engine;
-        cfg.tokenizer = std::make_shared<rt::tokenization::IdTokenizer>(engine->engine->end_tokens());
-        cfg.ctx_size = static_cast<int>(std::min<uint64_t>(p.n_ctx, static_cast<uint64_t>(n_prompt) + max_tokens));
-        cfg.position = {0, 1};
-        cfg.layers = {0, static_cast<int>(p.n_layer)};
-        cfg.speculative_max_tokens = static_cast<int>(draft_max);
-        rt::adapters::HipStageExecutor executor(cfg);
-        std::unique_ptr<rt::speculative::PromptLookupDraft> draft;
-        if (draft_max > 0) draft = std::make_unique<rt::speculative::PromptLookupDraft>(max_ngram, min_ngram);
-        rt::GenerationRequest req;
-        req.prompt.assign(prompt, prompt + n_prompt);
-        req.max_tokens = static_cast<int>(max_tokens);
-        req.layer_count = static_cast<int>(p.n_layer);
-        const rt::GenerationResult r = rt::run_generation(executor, req, draft.get(), static_cast<int>(draft_max));
-        if (!r.ok) throw jfh::Error(jfh::Status::InvalidArgument, r.error_code + ": " + r.error_message);
-        for (size_t i = 0; i < r.sampled_tokens.size(); ++i) out_tokens[i] = static_cast<int32_t>(r.sampled_tokens[i]);
-        *out_count = static_cast<uint32_t>(r.sampled_tokens.size());
-        if (stats) {
-            stats->completion_tokens = static_cast<uint32_t>(r.completion_tokens);
-            stats->target_decode_passes = static_cast<uint32_t>(r.target_decode_passes);
-            stats->speculative_draft_tokens = static_cast<uint32_t>(r.speculative_draft_tokens);
-            stats->speculative_accepted_tokens = static_cast<uint32_t>(r.speculative_accepted_tokens);
-            stats->time_to_first_token_ms = r.time_to_first_token_ms;
-            stats->decode_ms = r.decode_ms;
-            stats->stopped = r.finish_reason == "stop" ? 1U : 0U;
-            stats->reserved = 0;
-        }
+        std::unique_ptr<jfh::runtime::speculative::PromptLookupDraft> draft;
+        if (draft_max > 0) draft = std::make_unique<jfh::runtime::speculative::PromptLookupDraft>(max_ngram, min_ngram);
+        generate_one(engine, prompt, n_prompt, max_tokens, draft_max, draft.get(), out_tokens, out_count, stats);
+    });
+}
+
+jfh_status jfh_generate_draft(jfh_engine* engine, const int32_t* prompt, uint32_t n_prompt, uint32_t max_tokens,
+                              uint32_t draft_max, jfh_draft_propose_fn propose, void* user, int32_t* out_tokens,
+                              uint32_t* out_count, jfh_generation_stats* stats) {
+    return guarded([&] {
+        require(propose != nullptr || draft_max == 0, "a draft strategy is required");
+        const CallbackDraft draft(propose, user);
+        generate_one(engine, prompt, n_prompt, max_tokens, draft_max, propose ? &draft : nullptr, out_tokens,
+                     out_count, stats);
     });
 }
 
@@ -847,6 +912,7 @@ jfh_status jfh_generate_concurrent(jfh_engine* engine, uint32_t n_requests, cons
             }
         };
         std::vector<rt::GenerationResult> results(n_requests);
+        std::vector<jfh::PrefillMetrics> prefill(n_requests);
         std::vector<clock::time_point> finished(n_requests);
         std::vector<std::thread> runners;
         for (uint32_t i = 0; i < n_requests; ++i) {
@@ -864,6 +930,7 @@ jfh_status jfh_generate_concurrent(jfh_engine* engine, uint32_t n_requests, cons
                 };
                 try {
                     results[i] = rt::run_generation(*executor, req, draft.get(), static_cast<int>(draft_max));
+                    prefill[i] = jfh::Engine::last_prefill_metrics();  // the prefill ran on this thread
                 } catch (const std::exception& e) {
                     results[i].ok = false;
                     results[i].error_code = "generation_failed";
@@ -883,14 +950,8 @@ jfh_status jfh_generate_concurrent(jfh_engine* engine, uint32_t n_requests, cons
             }
             out_counts[i] = static_cast<uint32_t>(r.sampled_tokens.size());
             if (stats) {
-                stats[i].completion_tokens = static_cast<uint32_t>(r.completion_tokens);
-                stats[i].target_decode_passes = static_cast<uint32_t>(r.target_decode_passes);
-                stats[i].speculative_draft_tokens = static_cast<uint32_t>(r.speculative_draft_tokens);
-                stats[i].speculative_accepted_tokens = static_cast<uint32_t>(r.speculative_accepted_tokens);
-                stats[i].time_to_first_token_ms = r.time_to_first_token_ms;
-                stats[i].decode_ms = r.decode_ms;
-                stats[i].stopped = r.finish_reason == "stop" ? 1U : 0U;
-                stats[i].reserved = 0;
+                fill_stats(*engine->engine, r, prefill[i], static_cast<uint32_t>(cfg.ctx_size), prompt_lengths[i],
+                           stats[i]);
             }
             last = std::max(last, finished[i]);
         }

@@ -2,6 +2,7 @@
 #include "jfh_engine.hpp"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstddef>
 #include <cstring>
@@ -41,6 +42,9 @@ void rope_rows(float base, uint32_t hd, uint32_t begin, uint32_t count, float* o
 bool quantized(uint32_t type) { return type == kQ4_K || type == kQ6_K || type == kQ8_0 || type == kQ2_K; }
 
 }  // namespace
+
+// The last prefill's metrics per calling thread (Engine::last_prefill_metrics).
+thread_local PrefillMetrics t_last_prefill;
 
 // ------------------------------------------------------------------ Session
 Session::Session(Engine* engine, uint32_t capacity)
@@ -325,6 +329,7 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
         fail(Status::DeviceError, "the native engine's kernels are built for gfx950 only; device is " + device_name_);
     }
     hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "create stream");
+    for (hipEvent_t* e : {&ev_begin_, &ev_compute_, &ev_output_}) hip_check(hipEventCreate(e), "create timing event");
     try {
         gpu::scratch_setup(options.device);
     } catch (const std::exception& e) {
@@ -467,6 +472,9 @@ Engine::~Engine() {
     if (rope_) (void) hipFree(rope_);
     if (step_host_) (void) hipHostFree(step_host_);
     if (out_host_) (void) hipHostFree(out_host_);
+    for (hipEvent_t e : {ev_begin_, ev_compute_, ev_output_}) {
+        if (e) (void) hipEventDestroy(e);
+    }
     if (stream_) (void) hipStreamDestroy(stream_);
 }
 
@@ -499,7 +507,10 @@ std::unique_ptr<Session> Engine::create_session(uint32_t capacity) {
     }
     std::lock_guard lock(mutex_);
     ensure_capacity(capacity);
-    return std::unique_ptr<Session>(new Session(this, capacity));
+    const auto t0 = std::chrono::steady_clock::now();
+    std::unique_ptr<Session> s(new Session(this, capacity));
+    s->prefill_metrics_.allocation_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    return s;
 }
 
 namespace {
@@ -833,8 +844,11 @@ std::vector<int32_t> Engine::end_tokens() const {
 }
 
 void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int32_t* accepted, float* logits,
-                     float* act_out) {
+                     float* act_out, PrefillMetrics* metrics) {
+    using clock = std::chrono::steady_clock;
+    const auto ms_since = [](clock::time_point t) { return std::chrono::duration<double, std::milli>(clock::now() - t).count(); };
     std::lock_guard lock(mutex_);
+    const auto t_input = clock::now();
     const ModelParams& p = params_;
     if (!last_stage() && act_out == nullptr) fail(Status::InvalidArgument, "a non-final stage needs an activation output");
     if (steps.empty() || steps.size() > static_cast<size_t>(gpu::kMaxSeq)) {
@@ -906,12 +920,20 @@ void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int
     const bool store = logits != nullptr && outs > 0;
     hip_check(hipMemcpyAsync(step_dev_, step_host_, sizeof(gpu::StepDev), hipMemcpyHostToDevice, stream_), "upload step");
     // input rows of a later stage: the previous stage's residual stream
+    uint64_t input_bytes = sizeof(gpu::StepDev);
     for (size_t si = 0; si < steps.size(); ++si) {
         if (steps[si].activations == nullptr) continue;
-        hip_check(hipMemcpyAsync(h_ + static_cast<size_t>(sd.seqs[si].row0) * p.n_embd, steps[si].activations,
-                                 static_cast<size_t>(steps[si].n) * p.n_embd * sizeof(float), hipMemcpyHostToDevice,
-                                 stream_),
+        const size_t bytes = static_cast<size_t>(steps[si].n) * p.n_embd * sizeof(float);
+        hip_check(hipMemcpyAsync(h_ + static_cast<size_t>(sd.seqs[si].row0) * p.n_embd, steps[si].activations, bytes,
+                                 hipMemcpyHostToDevice, stream_),
                   "upload stage activations");
+        input_bytes += bytes;
+    }
+    if (metrics) {
+        metrics->host_input_ms += ms_since(t_input);
+        metrics->host_input_bytes += input_bytes;
+        metrics->attention_matrix_cores = p.head_dim == 64 || p.head_dim == 128;
+        ++metrics->steps;
     }
     if (options_.use_graphs) {
         const uint64_t key = (static_cast<uint64_t>(rows) << 40) | (static_cast<uint64_t>(max_len) << 32) |
@@ -919,6 +941,7 @@ void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int
                              (store ? 1u : 0u);
         auto it = graphs_.find(key);
         if (it == graphs_.end()) {
+            const auto t_plan = clock::now();
             hipGraph_t graph = nullptr;
             hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
             try {
@@ -934,11 +957,18 @@ void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int
             (void) hipGraphDestroy(graph);
             hip_check(e, "instantiate step graph");
             it = graphs_.emplace(key, exec).first;
+            if (metrics) {
+                metrics->planning_ms += ms_since(t_plan);
+                metrics->plan_reused = false;
+            }
         }
+        if (metrics) hip_check(hipEventRecord(ev_begin_, stream_), "time step");
         hip_check(hipGraphLaunch(it->second, stream_), "launch step graph");
     } else {
+        if (metrics) hip_check(hipEventRecord(ev_begin_, stream_), "time step");
         record(rows, max_len, static_cast<int32_t>(steps.size()), outs, store);
     }
+    if (metrics) hip_check(hipEventRecord(ev_compute_, stream_), "time step");
     if (outs > 0) {
         hip_check(hipMemcpyAsync(out_host_, out_dev_, sizeof(gpu::StepOut), hipMemcpyDeviceToHost, stream_),
                   "download step result");
@@ -953,7 +983,15 @@ void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int
                                  hipMemcpyDeviceToHost, stream_),
                   "download stage activations");
     }
+    if (metrics) hip_check(hipEventRecord(ev_output_, stream_), "time step");
     hip_check(hipStreamSynchronize(stream_), "step");
+    if (metrics) {
+        float compute = 0.0F, output = 0.0F;
+        hip_check(hipEventElapsedTime(&compute, ev_begin_, ev_compute_), "step time");
+        hip_check(hipEventElapsedTime(&output, ev_compute_, ev_output_), "step time");
+        metrics->compute_ms += compute;
+        metrics->output_read_ms += output;
+    }
     for (int32_t i = 0; i < outs; ++i) {
         if (out_tokens) out_tokens[i] = out_host_->token[i];
     }
@@ -966,12 +1004,38 @@ void Engine::forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int
     }
 }
 
+PrefillMetrics Engine::last_prefill_metrics() { return t_last_prefill; }
+
+uint64_t Engine::scratch_bytes_per_row() const {
+    const ModelParams& p = params_;
+    const uint64_t H = p.n_embd, Hq = static_cast<uint64_t>(p.n_head) * p.head_dim, F = p.n_ff;
+    auto act8 = [](const gpu::Act8& a) { return a.q ? a.K + a.K / 32 * 4 + a.K / 16 * 2 : 0; };
+    uint64_t b = (H + 2 * Hq + F) * sizeof(float) + act8(xq_attn_) + act8(xq_ffn_) + act8(xq_norm_);
+    b += gpu::attention_partial_floats(1, static_cast<int32_t>(p.n_head), static_cast<int32_t>(p.head_dim), splits_) *
+         sizeof(float);
+    if (logits_) b += static_cast<uint64_t>(p.n_vocab) * sizeof(float);
+    return b;
+}
+
+BufferMetrics Engine::buffer_metrics(uint32_t capacity, uint32_t prompt_tokens, const PrefillMetrics& prefill) const {
+    const ModelParams& p = params_;
+    BufferMetrics m;
+    const uint64_t stride = (std::max<uint32_t>(capacity, 16) + 15) / 16 * 16;  // as Session allocates
+    m.kv_cache_bytes = 2ull * resident_layers() * p.n_head_kv * stride * p.head_dim * sizeof(uint16_t);
+    m.prefill_scratch_bytes = scratch_bytes_per_row() * std::min<uint64_t>(prefill_chunk_, std::max<uint32_t>(1, prompt_tokens));
+    m.decode_scratch_bytes = scratch_bytes_per_row();
+    m.prefill_host_input_bytes = prefill.host_input_bytes;
+    return m;
+}
+
 int32_t Engine::prefill(Session& s, const int32_t* tokens, uint32_t n, float* logits) {
     require_full_model();
     if (s.position_ != 0 || n == 0 || n > s.capacity_) {
         fail(Status::InvalidArgument, "native Qwen2 prefill is outside session capacity");
     }
     int32_t token = -1;
+    PrefillMetrics m;
+    m.allocation_ms = s.prefill_metrics_.allocation_ms;
     for (uint32_t done = 0; done < n;) {
         const uint32_t len = std::min(prefill_chunk_, n - done);
         const bool last = done + len == n;
@@ -980,10 +1044,12 @@ int32_t Engine::prefill(Session& s, const int32_t* tokens, uint32_t n, float* lo
         st.tokens = tokens + done;
         st.n = len;
         st.logits = last ? 1 : 0;
-        forward({st}, last ? &token : nullptr, nullptr, last ? logits : nullptr);
+        forward({st}, last ? &token : nullptr, nullptr, last ? logits : nullptr, nullptr, &m);
         done += len;
     }
     s.prefill_position_ = n;
+    s.prefill_metrics_ = m;
+    t_last_prefill = m;
     return token;
 }
 
@@ -1003,6 +1069,8 @@ int32_t Engine::stage_prefill(Session& s, const int32_t* tokens, const float* ac
     }
     const size_t H = params_.n_embd;
     int32_t token = -1;
+    PrefillMetrics m;
+    m.allocation_ms = s.prefill_metrics_.allocation_ms;
     for (uint32_t done = 0; done < n;) {
         const uint32_t len = std::min(prefill_chunk_, n - done);
         const bool last = done + len == n;
@@ -1013,10 +1081,12 @@ int32_t Engine::stage_prefill(Session& s, const int32_t* tokens, const float* ac
         st.n = len;
         st.logits = last && last_stage() ? 1 : 0;
         forward({st}, st.logits ? &token : nullptr, nullptr, st.logits ? logits : nullptr,
-                act_out ? act_out + done * H : nullptr);
+                act_out ? act_out + done * H : nullptr, &m);
         done += len;
     }
     s.prefill_position_ = n;
+    s.prefill_metrics_ = m;
+    t_last_prefill = m;
     return token;
 }
 

@@ -33,6 +33,31 @@ class Engine;
 
 // KV-cache owner; position bookkeeping follows Qwen2Session
 // (qwen2_architecture.cpp:800-823, 1040-1054).
+// Host-side breakdown of a prefill (PrefillMetrics, native_inference.hpp:71-78):
+// graph capture and instantiation of step shapes met for the first time
+// (planning), building and uploading the step descriptors (host input), the
+// device time of the step graphs (compute, HIP events around each launch) and
+// of the result copies (output read).
+struct PrefillMetrics {
+    bool plan_reused = true;         // every prefill step shape's graph existed already
+    bool attention_matrix_cores = false;  // attention on MFMA (head dim 64 or 128)
+    double planning_ms = 0.0;
+    double allocation_ms = 0.0;      // the session's KV cache allocation and clearing
+    double host_input_ms = 0.0;
+    double compute_ms = 0.0;
+    double output_read_ms = 0.0;
+    uint64_t host_input_bytes = 0;   // step descriptors and activation rows uploaded
+    uint32_t steps = 0;              // prefill chunks
+};
+
+// Device buffers a generation uses (ExecutionBufferMetrics, native_inference.hpp:80-85).
+struct BufferMetrics {
+    uint64_t kv_cache_bytes = 0;          // the session's F16 K/V cache
+    uint64_t prefill_scratch_bytes = 0;   // workspace rows of one prefill chunk
+    uint64_t decode_scratch_bytes = 0;    // workspace of one decode row
+    uint64_t prefill_host_input_bytes = 0;
+};
+
 class Session {
 public:
     ~Session();
@@ -44,6 +69,8 @@ public:
     uint32_t prefill_position() const { return prefill_position_; }
     void rollback(uint32_t n);
     uint64_t kv_bytes() const { return kv_bytes_; }
+    // Metrics of the session's prefill (zero before it).
+    const PrefillMetrics& prefill_metrics() const { return prefill_metrics_; }
 
 private:
     friend class Engine;
@@ -57,6 +84,7 @@ private:
     uint16_t* k_ = nullptr;  // [resident layer][kv head][stride][head_dim]
     uint16_t* v_ = nullptr;  // [resident layer][kv head][head_dim][stride] (transposed)
     uint64_t kv_bytes_ = 0;
+    PrefillMetrics prefill_metrics_;
 };
 
 // One sequence's share of a batched step.
@@ -115,8 +143,9 @@ public:
     // sequence; logits (optional) n_logits_rows x vocab floats. A stage
     // that is not the last one computes no logits: act_out receives the
     // residual-stream rows after its last layer, f32 [rows][n_embd].
+    // metrics (optional) accumulates the step's host and device times.
     void forward(const std::vector<SeqStep>& steps, int32_t* out_tokens, int32_t* accepted, float* logits,
-                 float* act_out = nullptr);
+                 float* act_out = nullptr, PrefillMetrics* metrics = nullptr);
 
     // Prefill of arbitrary length: runs the prompt in chunks and returns the
     // greedy token of the last row (and its logits if requested).
@@ -154,6 +183,16 @@ public:
     void import_kv(Session& s, uint32_t n, const uint16_t* k, const uint16_t* v);
 
     uint32_t max_prefill_chunk() const { return prefill_chunk_; }
+
+    // Workspace bytes one token row of a step uses (residual, queries,
+    // attention and SwiGLU outputs, their int8 copies, attention partials).
+    uint64_t scratch_bytes_per_row() const;
+    // Buffer metrics of a session of `capacity` positions whose prefill ran
+    // `prompt_tokens` tokens with the given metrics.
+    BufferMetrics buffer_metrics(uint32_t capacity, uint32_t prompt_tokens, const PrefillMetrics& prefill) const;
+    // The prefill metrics of the last prefill the calling thread ran on any
+    // engine (a generation runner's executor closes its session when done).
+    static PrefillMetrics last_prefill_metrics();
 
 private:
     friend class Session;
@@ -199,6 +238,7 @@ private:
         hipEvent_t end = nullptr;
     };
     std::vector<ProfEvent>* prof_ = nullptr;
+    hipEvent_t ev_begin_ = nullptr, ev_compute_ = nullptr, ev_output_ = nullptr;  // prefill step timing
     double attn_kv_bytes_ = 0.0;  // K/V bytes one layer's attention reads in the step being recorded
     void* device_alloc(size_t bytes);
 

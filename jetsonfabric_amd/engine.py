@@ -13,7 +13,7 @@ import ctypes
 import os
 import time
 from dataclasses import dataclass, field
-from typing import Iterable, Sequence
+from typing import Callable, Iterable, Sequence
 
 import numpy as np
 
@@ -260,7 +260,36 @@ class GenerationResult:
     speculative_draft_tokens: int = 0
     speculative_accepted_tokens: int = 0
     finish_reason: str = "length"  # "stop": ended at an end-of-generation id
+    inter_token_latency_ms: float = 0.0
+    decode_tokens_per_second: float = 0.0
+    end_to_end_tokens_per_second: float = 0.0
+    # PrefillMetrics / ExecutionBufferMetrics (native_inference.hpp:71-85)
+    prefill: dict = field(default_factory=dict)
+    buffers: dict = field(default_factory=dict)
     extra: dict = field(default_factory=dict)
+
+    @classmethod
+    def from_stats(cls, tokens: list[int], st) -> "GenerationResult":
+        return cls(
+            sampled_tokens=tokens,
+            time_to_first_token_ms=st.time_to_first_token_ms,
+            decode_ms=st.decode_ms,
+            target_decode_passes=int(st.target_decode_passes),
+            speculative_draft_tokens=int(st.speculative_draft_tokens),
+            speculative_accepted_tokens=int(st.speculative_accepted_tokens),
+            finish_reason="stop" if st.stopped else "length",
+            inter_token_latency_ms=st.inter_token_latency_ms,
+            decode_tokens_per_second=st.decode_tokens_per_second,
+            end_to_end_tokens_per_second=st.end_to_end_tokens_per_second,
+            prefill={"plan_reused": bool(st.prefill_plan_reused),
+                     "attention_matrix_cores": bool(st.prefill_attention_matrix_cores),
+                     "planning_ms": st.prefill_planning_ms, "allocation_ms": st.prefill_allocation_ms,
+                     "host_input_preparation_ms": st.prefill_host_input_ms, "compute_ms": st.prefill_compute_ms,
+                     "output_read_ms": st.prefill_output_read_ms},
+            buffers={"kv_cache_bytes": int(st.kv_cache_bytes), "prefill_scratch_bytes": int(st.prefill_scratch_bytes),
+                     "decode_scratch_bytes": int(st.decode_scratch_bytes),
+                     "prefill_host_input_bytes": int(st.prefill_host_input_bytes)},
+        )
 
 
 def _i32(values: Sequence[int]):
@@ -550,15 +579,28 @@ class NativeEngine:
         stats = _capi.GenerationStats()
         check(library().jfh_generate(self._h, _i32(prompt), len(prompt), max_tokens, draft_max, max_ngram, min_ngram,
                                      out, ctypes.byref(count), ctypes.byref(stats)))
-        return GenerationResult(
-            sampled_tokens=[int(x) for x in out[:count.value]],
-            time_to_first_token_ms=stats.time_to_first_token_ms,
-            decode_ms=stats.decode_ms,
-            target_decode_passes=int(stats.target_decode_passes),
-            speculative_draft_tokens=int(stats.speculative_draft_tokens),
-            speculative_accepted_tokens=int(stats.speculative_accepted_tokens),
-            finish_reason="stop" if stats.stopped else "length",
-        )
+        return GenerationResult.from_stats([int(x) for x in out[:count.value]], stats)
+
+    def generate_with_draft(self, prompt: Sequence[int], max_tokens: int, draft_max: int,
+                            propose: Callable[[list[int], int], Sequence[int]]) -> GenerationResult:
+        """The same runner with a caller's draft strategy (jfh_generate_draft):
+        propose(history, max_tokens) returns the draft for the history."""
+        def thunk(_user, history, n, limit, out_ptr):
+            try:
+                draft = list(propose([history[i] for i in range(n)], int(limit)))[:limit]
+            except Exception:  # a failing strategy proposes nothing
+                return 0
+            for i, t in enumerate(draft):
+                out_ptr[i] = int(t)
+            return len(draft)
+
+        fn = _capi.DraftProposeFn(thunk)
+        out = (ctypes.c_int32 * max_tokens)()
+        count = ctypes.c_uint32()
+        stats = _capi.GenerationStats()
+        check(library().jfh_generate_draft(self._h, _i32(prompt), len(prompt), max_tokens, draft_max, fn, None, out,
+                                           ctypes.byref(count), ctypes.byref(stats)))
+        return GenerationResult.from_stats([int(x) for x in out[:count.value]], stats)
 
 
     def generate_concurrent(self, prompts: Sequence[Sequence[int]], max_tokens: int, draft_max: int = 0,
@@ -577,16 +619,8 @@ class NativeEngine:
                                                 min_ngram, batch_wait_us, out, counts, stats, ctypes.byref(wall)))
         results = []
         for i in range(n):
-            st = stats[i]
-            results.append(GenerationResult(
-                sampled_tokens=[int(x) for x in out[i * max_tokens:i * max_tokens + counts[i]]],
-                time_to_first_token_ms=st.time_to_first_token_ms,
-                decode_ms=st.decode_ms,
-                target_decode_passes=int(st.target_decode_passes),
-                speculative_draft_tokens=int(st.speculative_draft_tokens),
-                speculative_accepted_tokens=int(st.speculative_accepted_tokens),
-                finish_reason="stop" if st.stopped else "length",
-            ))
+            results.append(GenerationResult.from_stats(
+                [int(x) for x in out[i * max_tokens:i * max_tokens + counts[i]]], stats[i]))
         return results, wall.value
 
 
