@@ -304,18 +304,22 @@ jfh_status jfh_engine_dequantize(jfh_engine * engine, const char * tensor, uint3
 jfh_status jfh_engine_matmul(jfh_engine * engine, const char * tensor, const float * x, uint32_t n_tok, float * y);
 
 /* Allocation-free variant of jfh_engine_matmul. No counterpart in the
- * reference: it is for callers that cannot allocate device memory (code
- * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). x and y are DEVICE buffers, x f32 [n_tok][cols] and y f32
- * [n_tok][rows] of the tensor; the result equals jfh_engine_matmul's bit for
- * bit. The staging (int8 copies of the rows, the fused device matrix's full
- * output rows) lives in the library's static device scratch, one 16 MiB
- * array per GPU held until the process ends; calls whose staging exceeds it
- * fail with JFH_STATUS_INVALID_ARGUMENT before any work. Calls on one GPU
- * share that array: the library serializes them, so a caller must not expect
- * two of them to overlap. The call returns after the result is in y. */
+ * reference: it is for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc). x and y are DEVICE
+ * buffers, x f32 [n_tok][cols] and y f32 [n_tok][rows] of the tensor; the
+ * result equals jfh_engine_matmul's bit for bit. stream is the caller's HIP
+ * stream (hipStream_t; NULL: the null stream): the matmul reads x only after
+ * the work already enqueued there, so x may still be in flight on it. The
+ * kernels run on the engine's own stream and the call returns after the
+ * result is in y; it cannot be recorded into the caller's graph capture. The
+ * staging (int8 copies of the rows, the fused device matrix's full output
+ * rows) lives in the library's static device scratch, one 16 MiB array per
+ * GPU held until the process ends; calls whose staging exceeds it fail with
+ * JFH_STATUS_INVALID_ARGUMENT before any work. Calls on one GPU share that
+ * array: the library serializes them, so a caller must not expect two of them
+ * to overlap. */
 jfh_status jfh_engine_matmul_noalloc(jfh_engine * engine, const char * tensor, const float * x, uint32_t n_tok,
-                                     float * y);
+                                     float * y, void * stream);
 
 /* Parity entry points for the F16 KV cache (no reference counterpart: the
  * reference's cache lives in GGML tensors, qwen2_architecture.cpp:1056-1092).

@@ -653,10 +653,10 @@ jfh_status jfh_engine_matmul(jfh_engine* engine, const char* tensor, const float
 }
 
 jfh_status jfh_engine_matmul_noalloc(jfh_engine* engine, const char* tensor, const float* x, uint32_t n_tok,
-                                     float* y) {
+                                     float* y, void* stream) {
     return guarded([&] {
         require(engine && tensor && x && y, "engine, tensor and device buffers are required");
-        engine->engine->matmul_noalloc(tensor, x, n_tok, y);
+        engine->engine->matmul_noalloc(tensor, x, n_tok, y, static_cast<hipStream_t>(stream));
     });
 }
 

@@ -330,6 +330,7 @@ Engine::Engine(const HostModel& model, const EngineOptions& options) : params_(m
     }
     hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "create stream");
     for (hipEvent_t* e : {&ev_begin_, &ev_compute_, &ev_output_}) hip_check(hipEventCreate(e), "create timing event");
+    hip_check(hipEventCreateWithFlags(&ev_order_, hipEventDisableTiming), "create ordering event");
     try {
         gpu::scratch_setup(options.device);
     } catch (const std::exception& e) {
@@ -472,7 +473,7 @@ Engine::~Engine() {
     if (rope_) (void) hipFree(rope_);
     if (step_host_) (void) hipHostFree(step_host_);
     if (out_host_) (void) hipHostFree(out_host_);
-    for (hipEvent_t e : {ev_begin_, ev_compute_, ev_output_}) {
+    for (hipEvent_t e : {ev_begin_, ev_compute_, ev_output_, ev_order_}) {
         if (e) (void) hipEventDestroy(e);
     }
     if (stream_) (void) hipStreamDestroy(stream_);
@@ -1239,7 +1240,8 @@ void Engine::matmul(const std::string& name, const float* x_host, uint32_t n_tok
     }
 }
 
-void Engine::matmul_noalloc(const std::string& name, const float* x_dev, uint32_t n_tok, float* y_dev) {
+void Engine::matmul_noalloc(const std::string& name, const float* x_dev, uint32_t n_tok, float* y_dev,
+                            hipStream_t after) {
     std::lock_guard lock(mutex_);
     const TensorRef& ref = find_ref(name);
     const gpu::DMat& m = ref.dev->mat;
@@ -1259,6 +1261,9 @@ void Engine::matmul_noalloc(const std::string& name, const float* x_dev, uint32_
     uint8_t* base = static_cast<uint8_t*>(gpu::scratch_address(options_.device));
     if (base == nullptr) fail(Status::DeviceError, "the device's static scratch was not set up");
     std::lock_guard use(gpu::scratch_lock(options_.device));
+    // x may still be written by work on the caller's stream
+    hip_check(hipEventRecord(ev_order_, after), "order after the caller's stream");
+    hip_check(hipStreamWaitEvent(stream_, ev_order_, 0), "order after the caller's stream");
     gpu::Act8 xq;
     if (xq_bytes) xq = act8_at(base, n_tok, m.cols, blk);
     float* y_full = reinterpret_cast<float*>(base + xq_bytes);

@@ -168,8 +168,10 @@ public:
     void dequantize(const std::string& name, uint32_t row0, uint32_t n_rows, float* out_host);
     void matmul(const std::string& name, const float* x_host, uint32_t n_tok, float* y_host);
     // The same matmul on device rows (x_dev [n_tok][cols], y_dev [n_tok][rows])
-    // with its staging in the GPU's static scratch: no device allocation.
-    void matmul_noalloc(const std::string& name, const float* x_dev, uint32_t n_tok, float* y_dev);
+    // with its staging in the GPU's static scratch: no device allocation. It
+    // runs after the work enqueued on `after` (the caller's stream) and
+    // returns with y_dev written.
+    void matmul_noalloc(const std::string& name, const float* x_dev, uint32_t n_tok, float* y_dev, hipStream_t after);
 
     // Runs the step `iterations` times without graphs, timing every kernel
     // launch; sessions are restored to their starting positions.
@@ -239,6 +241,7 @@ private:
     };
     std::vector<ProfEvent>* prof_ = nullptr;
     hipEvent_t ev_begin_ = nullptr, ev_compute_ = nullptr, ev_output_ = nullptr;  // prefill step timing
+    hipEvent_t ev_order_ = nullptr;  // orders the allocation-free matmul after the caller's stream
     double attn_kv_bytes_ = 0.0;  // K/V bytes one layer's attention reads in the step being recorded
     void* device_alloc(size_t bytes);
 

@@ -922,19 +922,23 @@ struct ContinuousBatchingExecutor::Impl {
         }
     }
 
-    // Runs the taken steps on the delegate; failures become per-step results
-    // with the reference's error codes.
+    // Runs the taken steps on the delegate; failures, whatever the delegate
+    // throws, become per-step results with the reference's error codes.
     std::vector<inference::ExecutionResult> run_batch(const std::vector<Ticket*>& taken) {
-        std::vector<inference::StageInput> inputs;
-        inputs.reserve(taken.size());
-        for (const Ticket* t : taken) inputs.push_back(*t->input);
         std::vector<inference::ExecutionResult> out;
         try {
+            std::vector<inference::StageInput> inputs;
+            inputs.reserve(taken.size());
+            for (const Ticket* t : taken) inputs.push_back(*t->input);
             std::lock_guard turn(delegate_turn);
             out = delegate->execute_batch(inputs);
         } catch (const std::exception& e) {
             return std::vector<inference::ExecutionResult>(
                 taken.size(), inference::ExecutionResult::failure("continuous_batch_failed", e.what()));
+        } catch (...) {
+            return std::vector<inference::ExecutionResult>(
+                taken.size(), inference::ExecutionResult::failure("continuous_batch_failed",
+                                                                   "the delegate threw a non-standard exception"));
         }
         if (out.size() != taken.size()) {
             const std::string why = "the delegate answered " + std::to_string(out.size()) + " of " +
@@ -964,23 +968,47 @@ struct ContinuousBatchingExecutor::Impl {
             }
             forming = true;
             forming_now.store(true, std::memory_order_release);
-            const auto deadline = std::chrono::steady_clock::now() + config.max_wait;
-            if (arrived.size() < config.max_batch_size) {
+            std::vector<Ticket*> taken;
+            try {
+                const auto deadline = std::chrono::steady_clock::now() + config.max_wait;
+                if (arrived.size() < config.max_batch_size) {
+                    lock.unlock();
+                    spin([&] { return n_arrived.load(std::memory_order_acquire) >= config.max_batch_size; }, deadline);
+                    lock.lock();
+                }
+                changed.wait_until(lock, deadline, [this] { return arrived.size() >= config.max_batch_size; });
+                const std::size_t n = std::min(arrived.size(), config.max_batch_size);
+                taken.assign(arrived.begin(), arrived.begin() + static_cast<std::ptrdiff_t>(n));
+                arrived.erase(arrived.begin(), arrived.begin() + static_cast<std::ptrdiff_t>(n));
+                n_arrived.store(arrived.size(), std::memory_order_release);
                 lock.unlock();
-                spin([&] { return n_arrived.load(std::memory_order_acquire) >= config.max_batch_size; }, deadline);
+                std::vector<inference::ExecutionResult> results = run_batch(taken);
                 lock.lock();
-            }
-            changed.wait_until(lock, deadline, [this] { return arrived.size() >= config.max_batch_size; });
-            const std::size_t n = std::min(arrived.size(), config.max_batch_size);
-            std::vector<Ticket*> taken(arrived.begin(), arrived.begin() + static_cast<std::ptrdiff_t>(n));
-            arrived.erase(arrived.begin(), arrived.begin() + static_cast<std::ptrdiff_t>(n));
-            n_arrived.store(arrived.size(), std::memory_order_release);
-            lock.unlock();
-            std::vector<inference::ExecutionResult> results = run_batch(taken);
-            lock.lock();
-            for (std::size_t i = 0; i < n; ++i) {
-                taken[i]->result = std::move(results[i]);
-                taken[i]->answered.store(true, std::memory_order_release);
+                for (std::size_t i = 0; i < n; ++i) {
+                    taken[i]->result = std::move(results[i]);
+                    taken[i]->answered.store(true, std::memory_order_release);
+                }
+            } catch (...) {
+                // Whatever escaped, no ticket is left waiting for this leader: the
+                // steps it took and its own step (still queued or not) are answered
+                // with the batch failure, and the next caller leads.
+                if (!lock.owns_lock()) lock.lock();
+                const auto failed = [] {
+                    return inference::ExecutionResult::failure("continuous_batch_failed", "the batch leader failed");
+                };
+                for (Ticket* t : taken) {
+                    if (!t->answered.load(std::memory_order_acquire)) {
+                        t->result = failed();
+                        t->answered.store(true, std::memory_order_release);
+                    }
+                }
+                const auto it = std::find(arrived.begin(), arrived.end(), &mine);
+                if (it != arrived.end()) {
+                    arrived.erase(it);
+                    n_arrived.store(arrived.size(), std::memory_order_release);
+                    mine.result = failed();
+                    mine.answered.store(true, std::memory_order_release);
+                }
             }
             forming = false;
             forming_now.store(false, std::memory_order_release);

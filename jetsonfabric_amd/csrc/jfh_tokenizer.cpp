@@ -209,8 +209,13 @@ std::shared_ptr<const BpeTokenizer> BpeTokenizer::from_gguf(const uint8_t* data,
         if (types->ints.size() != n) throw Error(Status::FormatError, "tokenizer.ggml.token_type does not match the vocabulary");
         t->types_ = types->ints;
     }
+    // llama.cpp's vocabulary load: an empty text is spelled "[EMPTY_<id>]", and
+    // a text listed twice maps to its last id
     t->text_to_id_.reserve(n);
-    for (size_t id = 0; id < n; ++id) t->text_to_id_.emplace(t->tokens_[id], static_cast<int32_t>(id));
+    for (size_t id = 0; id < n; ++id) {
+        if (t->tokens_[id].empty()) t->tokens_[id] = "[EMPTY_" + std::to_string(id) + "]";
+        t->text_to_id_[t->tokens_[id]] = static_cast<int32_t>(id);
+    }
     t->merge_rank_.reserve(merges->strs.size());
     for (size_t r = 0; r < merges->strs.size(); ++r) {
         const std::string& m = merges->strs[r];

@@ -186,6 +186,7 @@ public:
     mutable std::vector<std::size_t> batches;
     mutable int prefills = 0, closes = 0, rollbacks = 0;
     bool fail_batches = false;
+    bool throw_non_standard = false;  // execute_batch throws an int
     bool short_batches = false;  // answers one step fewer than it is handed
 
     inference::ExecutionResult execute(const inference::StageInput& in) const override {
@@ -206,6 +207,7 @@ public:
             batches.push_back(inputs.size());
         }
         if (fail_batches) throw std::runtime_error("injected batch failure");
+        if (throw_non_standard) throw 42;
         std::vector<inference::ExecutionResult> out;
         for (const auto& in : inputs) out.push_back(execute(in));
         if (short_batches) out.pop_back();
@@ -273,6 +275,28 @@ void test_continuous_batching() {
         ContinuousBatchingExecutor ex(std::move(rec), ContinuousBatchingConfig{2, microseconds(0)});
         const inference::ExecutionResult a = ex.execute(step_input(inference::Phase::Decode, "a", 5));
         expect(!a.ok && a.error.code == "continuous_batch_failed", "batch failure is reported per step");
+    }
+    // a delegate that throws something that is no std::exception: every step of
+    // every batch gets the batch failure, nobody waits forever, and the
+    // executor keeps serving (later steps lead new batches)
+    {
+        auto rec = std::make_unique<BatchRecorder>();
+        rec->throw_non_standard = true;
+        BatchRecorder* r = rec.get();
+        ContinuousBatchingExecutor ex(std::move(rec), ContinuousBatchingConfig{2, microseconds(1000)});
+        std::vector<inference::ExecutionResult> res(5);
+        std::vector<std::thread> ts;
+        for (int i = 0; i < 5; ++i) {
+            ts.emplace_back([&, i] { res[i] = ex.execute(step_input(inference::Phase::Decode, std::to_string(i), i)); });
+        }
+        for (auto& t : ts) t.join();
+        for (const auto& x : res) {
+            expect(!x.ok && x.error.code == "continuous_batch_failed", "a non-standard delegate exception fails the step");
+        }
+        r->throw_non_standard = false;
+        const inference::ExecutionResult after = ex.execute(step_input(inference::Phase::Decode, "z", 9));
+        expect(after.ok && inference::decode_token_ids(after.output.payload) == std::vector<std::int32_t>{10},
+               "the executor serves steps after a failed batch");
     }
     // a delegate that answers the wrong number of steps fails every step of the batch
     {

@@ -194,6 +194,32 @@ def test_bos_eos_from_metadata(hf, tmp_path):
     t.close()
 
 
+def test_duplicate_and_empty_token_texts(hf, tmp_path):
+    """As llama.cpp loads a vocabulary: a text listed twice maps to its last id
+    (the merges and byte tokens then produce that id), and an empty text is
+    spelled "[EMPTY_<id>]". Parity with llama.cpp itself is unpinned (no
+    llama.cpp in this environment); this pins the rule as restated."""
+    kv, vocab = _vocab_kv(hf)
+    tokens = list(dict(kv)["tokenizer.ggml.tokens"][1])
+    types = list(dict(kv)["tokenizer.ggml.token_type"][1])
+    h_id = vocab["h"]
+    tokens += ["h", ""]  # a second "h" and an empty text at the end
+    types += [1, 1]
+    kv = [(k, ("str", tokens) if k == "tokenizer.ggml.tokens" else ("i32", types) if k == "tokenizer.ggml.token_type"
+           else v) for k, v in kv]
+    (tmp_path / "metadata.gguf").write_bytes(_metadata(kv))
+    t = jf.Tokenizer(str(tmp_path))
+    dup, empty = len(tokens) - 2, len(tokens) - 1
+    try:
+        assert t.vocab_size == len(tokens)
+        ids = t.tokenize("h")
+        assert ids == [dup] and h_id != dup
+        assert t.token_piece(dup) == b"h" and t.token_piece(h_id) == b"h"
+        assert t.token_piece(empty) == f"[EMPTY_{empty}]".encode()
+    finally:
+        t.close()
+
+
 def test_open_errors(tmp_path):
     with pytest.raises(jf.JfhError) as e:
         jf.Tokenizer(str(tmp_path))

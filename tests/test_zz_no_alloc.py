@@ -5,7 +5,9 @@ the fused device matrix's output rows in the library's static scratch; its
 rows must equal the allocating entry point's bit for bit, on consecutive
 calls that reuse the scratch (the second with fewer rows, so stale staging
 from the first call would show), for a fused tensor of each layout kind, and
-it rejects a call whose staging exceeds the scratch before doing any work.
+it rejects a call whose staging exceeds the scratch before doing any work. It
+reads x after the work enqueued on the caller's stream: an input still being
+copied there asynchronously is read complete.
 """
 from __future__ import annotations
 
@@ -67,7 +69,7 @@ def _noalloc(hip, engine, tensor, x, rows):
     xd = hip.upload(x)
     yd = hip.alloc(x.shape[0] * rows * 4)
     try:
-        check(jf.library().jfh_engine_matmul_noalloc(engine.handle, tensor.encode(), xd, x.shape[0], yd))
+        check(jf.library().jfh_engine_matmul_noalloc(engine.handle, tensor.encode(), xd, x.shape[0], yd, None))
         return hip.download(yd, (x.shape[0], rows))
     finally:
         hip.free(xd)
@@ -131,3 +133,37 @@ def test_noalloc_rejects_a_call_larger_than_the_scratch():
         assert np.array_equal(_noalloc(hip, e, "output.weight", x8, 70000), e.matmul("output.weight", x8, 70000))
     finally:
         e.close()
+
+
+def test_noalloc_reads_x_after_the_callers_stream(engine):
+    """x is written by an asynchronous copy from pinned memory on the caller's
+    non-blocking stream and the matmul is called at once with that stream: the
+    result equals the allocating matmul's on the same rows, bit for bit."""
+    hip = _Hip()
+    lib = hip.lib
+    tensor = "blk.0.ffn_down.weight"
+    rows, cols = TENSORS[tensor]
+    stream = ctypes.c_void_p()
+    hip._ok(lib.hipStreamCreateWithFlags(ctypes.byref(stream), 1), "hipStreamCreateWithFlags")
+    n_tok = 16
+    nbytes = n_tok * cols * 4
+    pinned = ctypes.c_void_p()
+    hip._ok(lib.hipHostMalloc(ctypes.byref(pinned), ctypes.c_size_t(nbytes), 0), "hipHostMalloc")
+    xd = hip.alloc(nbytes)  # NaN-filled: a matmul that ran ahead of the copy would read them
+    yd = hip.alloc(n_tok * rows * 4)
+    try:
+        rng = np.random.default_rng(77)
+        for it in range(3):
+            x = rng.normal(0, 1, (n_tok, cols)).astype(np.float32)
+            ctypes.memmove(pinned, x.ctypes.data, nbytes)
+            hip._ok(lib.hipMemsetAsync(xd, 0xFF, ctypes.c_size_t(nbytes), stream), "hipMemsetAsync")
+            hip._ok(lib.hipMemcpyAsync(xd, pinned, ctypes.c_size_t(nbytes), 1, stream), "hipMemcpyAsync")
+            check(jf.library().jfh_engine_matmul_noalloc(engine.handle, tensor.encode(), xd, n_tok, yd, stream))
+            got = hip.download(yd, (n_tok, rows))
+            assert np.array_equal(got, engine.matmul(tensor, x, rows)), f"call {it}"
+    finally:
+        hip._ok(lib.hipStreamSynchronize(stream), "hipStreamSynchronize")
+        hip.free(xd)
+        hip.free(yd)
+        lib.hipHostFree(pinned)
+        lib.hipStreamDestroy(stream)
