@@ -297,6 +297,20 @@ jfh_status jfh_engine_step_batch(jfh_engine * engine, jfh_session * const * sess
                                  const int32_t * tokens, const uint32_t * lengths, int32_t * out_tokens,
                                  uint32_t * out_accepted, float * logits);
 
+/* Several sessions' rows through one pipeline stage in one pass: the stage
+ * form of jfh_engine_step_batch, for draft verification and batched decode in
+ * stages (the reference verifies through its llama.cpp stage adapter,
+ * llama_cpp_stage_adapter.cpp:350-475, 703-823; its native stage decodes one
+ * row per pass, native_stage_executor.cpp:285-306). lengths[i] rows of
+ * sessions[i] at its position, every session prefilled; token ids
+ * (concatenated) into the first stage, f32 [rows][n_embd] activations into
+ * later ones. The last stage writes every row's greedy id to out_tokens and,
+ * when logits is set, every row's logits (rows x vocab); the others write
+ * every row's output activations to out_activations. */
+jfh_status jfh_engine_stage_step_batch(jfh_engine * engine, jfh_session * const * sessions, uint32_t count,
+                                       const int32_t * tokens, const float * activations, const uint32_t * lengths,
+                                       int32_t * out_tokens, float * out_activations, float * logits);
+
 /* Parity entry points: GPU dequantization of tensor rows (bit-exact with the
  * GGML layouts) and a matmul through the engine's kernels. */
 jfh_status jfh_engine_dequantize(jfh_engine * engine, const char * tensor, uint32_t row0, uint32_t n_rows,

@@ -149,6 +149,8 @@ SIGNATURES = {
     "jfh_engine_step_batch": (Status, [c_void_p, POINTER(c_void_p), c_uint32, POINTER(c_int32), POINTER(c_uint32),
                                        POINTER(c_int32), POINTER(c_uint32), POINTER(c_float)]),
     "jfh_engine_dequantize": (Status, [c_void_p, c_char_p, c_uint32, c_uint32, POINTER(c_float)]),
+    "jfh_engine_stage_step_batch": (Status, [c_void_p, POINTER(c_void_p), c_uint32, POINTER(c_int32), POINTER(c_float),
+                                             POINTER(c_uint32), POINTER(c_int32), POINTER(c_float), POINTER(c_float)]),
     "jfh_engine_matmul_noalloc": (Status, [c_void_p, c_char_p, c_void_p, c_uint32, c_void_p, c_void_p]),
     "jfh_engine_matmul": (Status, [c_void_p, c_char_p, POINTER(c_float), c_uint32, POINTER(c_float)]),
     "jfh_session_read_kv": (Status, [c_void_p, c_uint32, c_uint32, POINTER(c_uint16), POINTER(c_uint16)]),

@@ -638,6 +638,36 @@ jfh_status jfh_engine_step_batch(jfh_engine* engine, jfh_session* const* session
     });
 }
 
+jfh_status jfh_engine_stage_step_batch(jfh_engine* engine, jfh_session* const* sessions, uint32_t count,
+                                       const int32_t* tokens, const float* activations, const uint32_t* lengths,
+                                       int32_t* out_tokens, float* out_activations, float* logits) {
+    return guarded([&] {
+        require(engine && sessions && lengths && count > 0, "batch arguments are required");
+        jfh::Engine& e = *engine->engine;
+        require(e.first_stage() ? tokens != nullptr && activations == nullptr : tokens == nullptr && activations != nullptr,
+                "the first stage takes token ids, later stages activation rows");
+        require(e.last_stage() ? out_tokens != nullptr : out_activations != nullptr && logits == nullptr,
+                "the last stage writes token ids (and logits), the others activation rows");
+        const size_t H = e.params().n_embd;
+        std::vector<jfh::SeqStep> steps;
+        size_t offset = 0;
+        for (uint32_t i = 0; i < count; ++i) {
+            require(sessions[i] && sessions[i]->owner == engine, "session does not belong to this engine");
+            require(sessions[i]->session->position() > 0, "batched steps require prefilled sessions");
+            require(lengths[i] > 0, "every session brings at least one row");
+            jfh::SeqStep st;
+            st.session = sessions[i]->session.get();
+            st.tokens = tokens ? tokens + offset : nullptr;
+            st.activations = activations ? activations + offset * H : nullptr;
+            st.n = lengths[i];
+            st.logits = e.last_stage() ? 2 : 0;
+            offset += lengths[i];
+            steps.push_back(st);
+        }
+        e.forward(steps, out_tokens, nullptr, logits, e.last_stage() ? nullptr : out_activations);
+    });
+}
+
 jfh_status jfh_engine_dequantize(jfh_engine* engine, const char* tensor, uint32_t row0, uint32_t n_rows, float* out) {
     return guarded([&] {
         require(engine && tensor && out, "engine, tensor and output are required");

@@ -520,6 +520,36 @@ class NativeEngine:
             o += len(row)
         return (ids, [int(a) for a in acc], rows) if logits else (ids, [int(a) for a in acc])
 
+    def stage_step_batch(self, sessions: Sequence[NativeSession], tokens: Sequence[Sequence[int]] | None = None,
+                         activations: Sequence[np.ndarray] | None = None, logits: bool = False):
+        """Several sessions' rows through this pipeline stage in one pass (jfh_engine_stage_step_batch):
+        token ids per session into the first stage, f32 [rows, n_embd] activations into later ones.
+        The last stage returns every row's greedy id per session (and, when asked, [rows, vocab]
+        logits per session); the others return every row's output activations per session."""
+        count = len(sessions)
+        handles = (ctypes.c_void_p * count)(*[s.handle.value for s in sessions])
+        rows = [len(t) for t in tokens] if tokens is not None else [len(a) for a in activations]
+        total = sum(rows)
+        lengths = (ctypes.c_uint32 * count)(*rows)
+        f32p = ctypes.POINTER(ctypes.c_float)
+        toks = _i32([t for row in tokens for t in row]) if tokens is not None else None
+        acts = None
+        if activations is not None:
+            acts = np.ascontiguousarray(np.concatenate([np.asarray(a, dtype=np.float32) for a in activations]))
+        out_ids = (ctypes.c_int32 * total)() if self.last_stage else None
+        out_act = None if self.last_stage else np.zeros((total, self._config.n_embd), dtype=np.float32)
+        lg = np.zeros((total, self.vocab), dtype=np.float32) if logits and self.last_stage else None
+        check(library().jfh_engine_stage_step_batch(
+            self._h, handles, count, toks, acts.ctypes.data_as(f32p) if acts is not None else None, lengths, out_ids,
+            out_act.ctypes.data_as(f32p) if out_act is not None else None, lg.ctypes.data_as(f32p) if lg is not None else None))
+        split = np.cumsum([0] + rows)
+        if not self.last_stage:
+            return [out_act[split[i]:split[i + 1]] for i in range(count)]
+        ids = [[int(out_ids[j]) for j in range(split[i], split[i + 1])] for i in range(count)]
+        if logits:
+            return ids, [lg[split[i]:split[i + 1]] for i in range(count)]
+        return ids
+
     def profile_batch(self, sessions: Sequence[NativeSession], token_rows: Sequence[Sequence[int]],
                       iterations: int = 3, all_logits: bool = False) -> list[dict]:
         """Per-kernel device time and algorithmic bytes of one batched step (as step_batch) over
