@@ -368,8 +368,9 @@ def main() -> int:
     # ---- end-to-end speculation at the reference's acceptance rates (drafts from the recorded continuation)
     spec7 = spec_rate_runs(engine, cprompts[0], args.spec_tokens, k, cfg.n_vocab, args.seed + 500)
 
+    oracle_build = host_oracle() if not args.no_cpu else None
     parity = parity_sample(engine, model, cfg, args) if not args.no_cpu else None
-    cpu = cpu_baseline(model, cfg, context, args) if not args.no_cpu else None
+    cpu = cpu_baseline(model, cfg, context, args, oracle_build) if not args.no_cpu else None
     engine.close()
     model.close()
 
@@ -765,7 +766,23 @@ def parity_sample(engine, model, cfg, args, prompt_len: int = 12, steps: int = 3
     return out
 
 
-def cpu_baseline(model, cfg, context, args):
+def host_oracle() -> str:
+    """Build the oracle for this host's CPU (-march=native; results equal the
+    portable build's: no FP contraction, no reassociation) and use it for the
+    parity sample and the CPU baseline. Falls back to the portable build."""
+    import subprocess
+    import tempfile
+    import oracle as jo
+    flags = "-O3 -ffp-contract=off -fopenmp"
+    try:
+        jo.use_library(jo.build_native(tempfile.mkdtemp(prefix="jfo_native_")))
+        return f"gcc {flags} -march=native"
+    except (OSError, subprocess.CalledProcessError) as e:
+        log(f"host-tuned oracle build failed ({e}); timing the portable build")
+        return f"gcc {flags} -march=x86-64-v3"
+
+
+def cpu_baseline(model, cfg, context, args, build: str):
     """The oracle's multithreaded C forward timed on the host cores over a bounded sample."""
     import oracle as jo
 
@@ -794,6 +811,7 @@ def cpu_baseline(model, cfg, context, args):
                   f"(KV filled with seeded values), CPU oracle (OpenMP C), {threads} threads",
         "host": topo,
         "threads_note": f"{threads} threads: the host CPU share of one GPU on this machine",
+        "build": build,
     }
 
 

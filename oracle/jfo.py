@@ -31,7 +31,7 @@ __all__ = [
     "F32", "F16", "Q8_0", "Q2_K", "Q4_K", "Q6_K", "MODE_EXACT", "MODE_Q8", "act_block", "lib", "block", "row_bytes",
     "f16_to_f32", "f32_to_f16", "dequantize_row", "quantize_act", "quantize_act_normed", "vec_dot_q8", "vec_dot_f32", "matmul",
     "rope_table", "argmax", "OracleModel", "OracleSession", "prompt_lookup", "speculative_generate",
-    "ref_loader", "nrmse", "cosine",
+    "ref_loader", "nrmse", "cosine", "use_library", "build_native",
 ]
 
 
@@ -87,6 +87,24 @@ _SIGS = {
 }
 
 _lib = None
+
+
+def use_library(path: str) -> None:
+    """Load the oracle from another build of the same sources (e.g. one tuned
+    with -march=native for timing) instead of libjfo.so. Only before the
+    first call into the oracle: handles from one build mean nothing to another."""
+    global LIB_PATH
+    if _lib is not None and os.path.abspath(path) != os.path.abspath(LIB_PATH):
+        raise RuntimeError("the oracle library is already loaded")
+    LIB_PATH = path
+
+
+def build_native(out_dir: str) -> str:
+    """Build the oracle for this host's CPU (make -C oracle native) into out_dir."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", HERE, "native", f"OUT={os.path.abspath(out_dir)}"], check=True,
+                   stdout=subprocess.DEVNULL)
+    return os.path.join(out_dir, "libjfo_native.so")
 
 
 def lib() -> ctypes.CDLL:

@@ -405,3 +405,39 @@ def test_rope_table_closed_form():
     assert np.allclose(t[:, 0::2] ** 2 + t[:, 1::2] ** 2, 1.0, atol=1e-6)  # rotations preserve norms
     tail = jo.rope_table(base, hd, 1000, 8)
     assert np.array_equal(tail, t[1000:1008])
+
+
+_HOST_BUILD_SCRIPT = """
+import sys
+import numpy as np
+import oracle as jo
+jo.use_library(sys.argv[1])
+from tests.test_oracle_forward import _q4k_model
+model = _q4k_model()
+om = jo.OracleModel.from_model(model)
+out = []
+for mode in (jo.MODE_Q8, jo.MODE_EXACT):
+    s = om.session(64, mode, 2)
+    out.append(s.forward([5, 17, 99, 3, 250, 7, 7, 12], 8)[1])
+np.save(sys.argv[2], np.stack(out))
+"""
+
+
+def test_host_tuned_build_gives_the_same_logits(tmp_path):
+    """The -march=native build that bench.py times computes exactly what the portable build does."""
+    import os
+    import subprocess
+    import sys
+    lib = jo.build_native(str(tmp_path))
+    out = tmp_path / "logits.npy"
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    subprocess.run([sys.executable, "-c", _HOST_BUILD_SCRIPT, lib, str(out)], check=True, cwd=root)
+    model = _q4k_model()
+    om = jo.OracleModel.from_model(model)
+    want = []
+    for mode in (jo.MODE_Q8, jo.MODE_EXACT):
+        s = om.session(64, mode, 2)
+        want.append(s.forward([5, 17, 99, 3, 250, 7, 7, 12], 8)[1])
+    want = np.stack(want)
+    assert np.isfinite(want).all()
+    assert np.array_equal(np.load(out), want)
