@@ -2219,6 +2219,9 @@ constexpr int kAttnWgKeys = kAttnTile * (kAttnThreads / kWave);
 constexpr int kAttnMaxSplits = 32;
 
 constexpr int kAttnPrefillKeys = 256;
+// Work-groups of the matrix-core attention resident at once: two per CU
+// (four waves each at its two waves per SIMD) on 256 CUs.
+constexpr int kAttnResidentWgs = 512;
 // Keys per split of a sequence with n_keys keys and len rows in the step: the
 // decode rule (about n_keys / splits_max, in whole rounds of the work-group's
 // waves), which depends on the position alone, so a verify or batched step
@@ -2502,8 +2505,8 @@ template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void k_attention_mfma(const float* __restrict__ q,
                                                                  const StepDev* __restrict__ step, int32_t layer,
                                                                  int32_t n_head, int32_t n_head_kv,
-                                                                 int32_t splits_max, int32_t qgroups,
-                                                                 float* __restrict__ partial) {
+                                                                 int32_t splits_max, int32_t qgroups, int32_t slots,
+                                                                 int32_t spw, float* __restrict__ partial) {
     constexpr int W = kAttnThreads / kWave, KS = HD / 32, DB = HD / 16, R = kAttnRows;
     __shared__ float Ms[W][R], Ls[W][R];
     __shared__ float Os[W][HD][R];
@@ -2520,13 +2523,16 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_mfma(const float* __
     const int n_keys = pos0 + len;
     const int L = attn_split_len(n_keys, len, splits_max);
     const int n_splits = (n_keys + L - 1) / L;
-    const int split = blockIdx.x;
-    if (split >= n_splits) {
+    // the work-group's splits [s_first, s_end) of the slots; those past the sequence's last key are marked empty
+    const int s_first = blockIdx.x * spw, s_end = min(s_first + spw, slots);
+    for (int sp = max(s_first, n_splits); sp < s_end; ++sp) {
         attn_empty_split<kAttnThreads>(partial, q_begin, min(R, NQ - q_begin), G, kvh, row0, n_head, HD, splits_max,
-                                       split);
-        return;
+                                       sp);
     }
-    const int k0 = split * L, k1 = min(n_keys, k0 + L);
+    const int s_stop = min(s_end, n_splits);
+    if (s_first >= s_stop) return;
+    int split = s_first;
+    int k0 = split * L, k1 = min(n_keys, k0 + L);
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int r = lane & (R - 1), grp = lane >> 4;
     const size_t head_base = static_cast<size_t>(layer) * n_head_kv + kvh;
@@ -2562,10 +2568,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_mfma(const float* __
         }
     }
 
-    float m = -INFINITY, l = 0.0F;
+    float m, l;
     f32x4 o[DB];
-#pragma unroll
-    for (int d = 0; d < DB; ++d) o[d] = f32x4{0.0F, 0.0F, 0.0F, 0.0F};
     // one 16-key tile of the wave at t0 from kr / vr
     auto tile = [&](int t0) {
         f32x4 sc = {0.0F, 0.0F, 0.0F, 0.0F};
@@ -2609,54 +2613,76 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_mfma(const float* __
             o[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, plo, o[d], 0, 0, 0);
         }
     };
-    // a wave with several tiles keeps the next one in flight; its last tile requests nothing more
-    for (; t0 + W * R < k1; t0 += W * R) {
+    const int nq = min(R, NQ - q_begin);
+    // The splits of the work-group one after another, each with its own
+    // (max, sum, output) state and partial: a wave keeps its next tile in
+    // flight, across a split boundary too (the next split's first tile is
+    // requested before the current split's last tile and its merge).
+    for (;;) {
+        m = -INFINITY;
+        l = 0.0F;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) o[d] = f32x4{0.0F, 0.0F, 0.0F, 0.0F};
         u32x4 krn[KS];
         u32x2 vrn[DB];
-        attn_mfma_load<HD>(kc, vt, t0 + W * R, capacity, r, grp, krn, vrn);
-        tile(t0);
+        for (; t0 + W * R < k1; t0 += W * R) {
+            attn_mfma_load<HD>(kc, vt, t0 + W * R, capacity, r, grp, krn, vrn);
+            tile(t0);
+#pragma unroll
+            for (int s = 0; s < KS; ++s) kr[s] = krn[s];
+#pragma unroll
+            for (int d = 0; d < DB; ++d) vr[d] = vrn[d];
+        }
+        const bool more = split + 1 < s_stop;
+        const int t_next = (split + 1) * L + R * wave;
+        if (more) attn_mfma_load<HD>(kc, vt, t_next, capacity, r, grp, krn, vrn);
+        if (t0 < k1) tile(t0);
+        // the row's sum over its four lanes, then the waves merged in LDS
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        if (grp == 0) {
+            Ms[wave][r] = m;
+            Ls[wave][r] = l;
+        }
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) Os[wave][16 * d + 4 * grp + j][r] = o[d][j];
+        }
+        __syncthreads();
+        for (int e = threadIdx.x; e < nq * HD; e += kAttnThreads) {
+            const int i = e / HD, dim = e - i * HD;
+            float M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < W; ++w) M = fmaxf(M, Ms[w][i]);
+            float Lsum = 0.0F, acc = 0.0F;
+            if (M != -INFINITY) {
+#pragma unroll
+                for (int w = 0; w < W; ++w) {
+                    const float f = Ms[w][i] == -INFINITY ? 0.0F : expf(Ms[w][i] - M);
+                    Lsum += f * Ls[w][i];
+                    acc += f * Os[w][dim][i];
+                }
+            }
+            const int qrow_i = q_begin + i;
+            const int t = qrow_i / G, hh = kvh * G + qrow_i % G;
+            float* dst = partial + ((static_cast<size_t>(row0 + t) * n_head + hh) * splits_max + split) * (HD + 2);
+            if (dim == 0) {
+                dst[0] = M;
+                dst[1] = Lsum;
+            }
+            dst[2 + dim] = acc;
+        }
+        if (!more) break;
+        __syncthreads();  // the merge above has read the waves' states before the next split overwrites them
+        ++split;
+        k0 = split * L;
+        k1 = min(n_keys, k0 + L);
+        t0 = t_next;
 #pragma unroll
         for (int s = 0; s < KS; ++s) kr[s] = krn[s];
 #pragma unroll
         for (int d = 0; d < DB; ++d) vr[d] = vrn[d];
-    }
-    if (t0 < k1) tile(t0);
-    // the row's sum over its four lanes, then the waves merged in LDS
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    if (grp == 0) {
-        Ms[wave][r] = m;
-        Ls[wave][r] = l;
-    }
-#pragma unroll
-    for (int d = 0; d < DB; ++d) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) Os[wave][16 * d + 4 * grp + j][r] = o[d][j];
-    }
-    __syncthreads();
-    const int nq = min(R, NQ - q_begin);
-    for (int e = threadIdx.x; e < nq * HD; e += kAttnThreads) {
-        const int i = e / HD, dim = e - i * HD;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < W; ++w) M = fmaxf(M, Ms[w][i]);
-        float Lsum = 0.0F, acc = 0.0F;
-        if (M != -INFINITY) {
-#pragma unroll
-            for (int w = 0; w < W; ++w) {
-                const float f = Ms[w][i] == -INFINITY ? 0.0F : expf(Ms[w][i] - M);
-                Lsum += f * Ls[w][i];
-                acc += f * Os[w][dim][i];
-            }
-        }
-        const int qrow_i = q_begin + i;
-        const int t = qrow_i / G, hh = kvh * G + qrow_i % G;
-        float* dst = partial + ((static_cast<size_t>(row0 + t) * n_head + hh) * splits_max + split) * (HD + 2);
-        if (dim == 0) {
-            dst[0] = M;
-            dst[1] = Lsum;
-        }
-        dst[2 + dim] = acc;
     }
 }
 
@@ -3169,12 +3195,22 @@ void launch_attention(const float* q, const StepDev* step, int32_t max_len, int3
         throw std::invalid_argument("attention step has too many query rows per kv head");
     }
     dim3 grid(slots, n_head_kv * qgroups, n_seq), block(kAttnThreads);
+    // On matrix cores a work-group walks spw consecutive splits when the
+    // step's (split, kv head x query group, sequence) work-groups would
+    // exceed one resident round: every split keeps its own partial, so the
+    // results do not depend on spw.
+    int spw = 1;
+    if (mfma) {
+        const int cols = n_head_kv * qgroups * n_seq;
+        spw = std::min(slots, (slots * cols + kAttnResidentWgs - 1) / kAttnResidentWgs);
+        grid.x = (slots + spw - 1) / spw;
+    }
     if (head_dim == 128) {
         launch(k_attention_mfma<128>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, splits, qgroups,
-               partial);
+               slots, spw, partial);
     } else if (head_dim == 64) {
         launch(k_attention_mfma<64>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, splits, qgroups,
-               partial);
+               slots, spw, partial);
     } else {
         launch(k_attention<0>, grid, block, 0, stream, q, step, layer, n_head, n_head_kv, head_dim, splits, qgroups,
                partial);
