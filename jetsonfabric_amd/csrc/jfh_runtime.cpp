@@ -10,6 +10,7 @@
 #include <limits>
 #include <map>
 #include <stdexcept>
+#include <stop_token>
 #include <thread>
 
 namespace jfh::runtime {
@@ -373,9 +374,12 @@ using inference::StageOutput;
 
 class HipStageExecutor::Impl {
 public:
+    using Clock = std::chrono::steady_clock;
+
     struct SessionState {
         std::unique_ptr<Session> session;
         int expected_decode_step = 1;
+        Clock::time_point last_used = Clock::now();
     };
 
     explicit Impl(HipStageConfig c) : config(std::move(c)) {
@@ -399,11 +403,38 @@ public:
         if (config.speculative_max_tokens < 0 || config.speculative_max_tokens > 8) {
             throw std::invalid_argument("speculative width must be 0..8");
         }
+        if (config.session_idle_ttl <= std::chrono::milliseconds::zero() ||
+            config.session_reap_interval <= std::chrono::milliseconds::zero()) {
+            throw std::invalid_argument("native session expiration intervals must be greater than zero");
+        }
+        reaper = std::jthread([this](std::stop_token stop) { reap_sessions(stop); });
+    }
+
+    // llama_cpp_stage_adapter.cpp:939-967: sessions idle for the TTL are closed
+    void prune_expired_locked(Clock::time_point now) {
+        for (auto it = sessions.begin(); it != sessions.end();) {
+            it = now - it->second.last_used >= config.session_idle_ttl ? sessions.erase(it) : std::next(it);
+        }
+    }
+
+    void reap_sessions(std::stop_token stop) {
+        std::mutex wait_mutex;
+        std::condition_variable_any wake;
+        while (!stop.stop_requested()) {
+            {
+                std::unique_lock wait_lock(wait_mutex);
+                wake.wait_for(wait_lock, stop, config.session_reap_interval, [] { return false; });
+            }
+            if (stop.stop_requested()) return;
+            std::lock_guard lock(mutex);
+            prune_expired_locked(Clock::now());
+        }
     }
 
     // native_stage_executor.cpp:110-140
     ExecutionResult execute(const StageInput& input) {
         std::lock_guard lock(mutex);
+        prune_expired_locked(Clock::now());
         return execute_locked(input);
     }
 
@@ -430,6 +461,7 @@ public:
     // engine step; everything else falls back to execute (executor.hpp:20-28).
     std::vector<ExecutionResult> execute_batch(const std::vector<StageInput>& inputs) {
         std::lock_guard lock(mutex);
+        prune_expired_locked(Clock::now());
         std::vector<ExecutionResult> results(inputs.size());
         std::vector<std::size_t> batch;
         std::vector<std::vector<std::int32_t>> batch_tokens;
@@ -479,6 +511,7 @@ public:
                 const std::size_t n = batch_tokens[k].size();
                 SessionState& state = sessions.at(inputs[batch[k]].session_id);
                 state.expected_decode_step += static_cast<int>(n);
+                state.last_used = Clock::now();
                 std::vector<std::int32_t> mine(ids.begin() + static_cast<std::ptrdiff_t>(o),
                                                ids.begin() + static_cast<std::ptrdiff_t>(o + n));
                 StageOutput out = n > 1 ? rows_output(mine) : token_output(mine[0]);
@@ -507,10 +540,12 @@ public:
         if (n >= state.expected_decode_step) throw std::invalid_argument("rollback exceeds the decoded native suffix");
         state.session->rollback(static_cast<std::uint32_t>(n));
         state.expected_decode_step -= n;
+        state.last_used = Clock::now();
     }
 
-    std::size_t count() const {
+    std::size_t count() {
         std::lock_guard lock(mutex);
+        prune_expired_locked(Clock::now());
         return sessions.size();
     }
 
@@ -656,6 +691,7 @@ private:
             config.engine->stage_decode(*state.session, tokens.empty() ? nullptr : tokens.data(),
                                         act.empty() ? nullptr : act.data(), out_rows.empty() ? nullptr : out_rows.data());
         ++state.expected_decode_step;
+        state.last_used = Clock::now();
         return ExecutionResult::success(config.position.is_last() ? token_output(token) : activation_output(out_rows));
     }
 
@@ -704,12 +740,14 @@ private:
         std::vector<std::int32_t> ids(tokens.size());
         config.engine->forward({st}, ids.data(), nullptr, nullptr);
         state.expected_decode_step += static_cast<int>(tokens.size());
+        state.last_used = Clock::now();
         return ExecutionResult::success(tokens.size() > 1 ? rows_output(ids) : token_output(ids[0]));
     }
 
     HipStageConfig config;
     mutable std::mutex mutex;
     std::unordered_map<std::string, SessionState> sessions;
+    std::jthread reaper;  // last: stopped and joined before the sessions go
 };
 
 HipStageExecutor::HipStageExecutor(HipStageConfig config) : impl_(std::make_unique<Impl>(std::move(config))) {}

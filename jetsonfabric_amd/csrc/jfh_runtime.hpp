@@ -224,6 +224,12 @@ struct HipStageConfig {
     inference::StagePosition position;
     inference::LayerRange layers;
     int speculative_max_tokens = 8;  // verify width limit - 1 (worker/config.cpp:105-107)
+    // A session unused for session_idle_ttl is closed (its KV cache freed), checked
+    // every session_reap_interval and at every call, so that a caller that fails
+    // between steps cannot hold device memory forever (the reference's stage
+    // adapter, llama_cpp_stage_adapter.hpp:26-33, .cpp:151-153, 193-196, 939-967).
+    std::chrono::milliseconds session_idle_ttl = std::chrono::minutes(5);
+    std::chrono::milliseconds session_reap_interval = std::chrono::seconds(1);
 };
 
 class HipStageExecutor final : public inference::Executor {

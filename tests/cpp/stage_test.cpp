@@ -8,12 +8,14 @@
 // jfh_stage_test_main tests/test_gpu_stages.py calls in its own process.
 #include "jfh_runtime.hpp"
 
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <filesystem>
 #include <memory>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include <unistd.h>
@@ -146,6 +148,33 @@ extern "C" int jfh_stage_test_main() try {
     expect(!mismatch.ok && mismatch.error.code == "native_stage_assignment_mismatch", "assignment mismatch");
     const ExecutionResult missing = last.execute(input("nope", Phase::Decode, 1, 1, 2, 2, 4, a.output.payload));
     expect(!missing.ok && missing.error.code == "stage_session_not_found", "decode without a session");
+
+    // idle sessions are closed after their TTL (llama_cpp_stage_adapter_test.cpp:410-437)
+    {
+        adapters::HipStageConfig c = config(whole_engine, 0, 1, 0, 4);
+        c.session_idle_ttl = std::chrono::milliseconds(30);
+        c.session_reap_interval = std::chrono::milliseconds(5);
+        adapters::HipStageExecutor expiring(c);
+        const ExecutionResult p = expiring.execute(input("expiring", Phase::Prefill, 0, 0, 1, 0, 4, tokens(prompt)));
+        expect(p.ok, "expiring stage prefill");
+        expect(expiring.session_count() == 1U, "expiring stage retains its new session");
+        const auto deadline = std::chrono::steady_clock::now() + std::chrono::seconds(2);
+        while (expiring.session_count() != 0U && std::chrono::steady_clock::now() < deadline) {
+            std::this_thread::sleep_for(std::chrono::milliseconds(5));
+        }
+        expect(expiring.session_count() == 0U, "idle stage session is reaped after its TTL");
+        const ExecutionResult gone = expiring.execute(input("expiring", Phase::Decode, 1, 0, 1, 0, 4, tokens({want})));
+        expect(!gone.ok && gone.error.code == "stage_session_not_found", "a reaped session is gone");
+        c.session_idle_ttl = std::chrono::milliseconds(0);
+        try {
+            adapters::HipStageExecutor bad(c);
+            expect(false, "accepted a zero session TTL");
+        } catch (const std::invalid_argument& ex) {
+            expect(std::string(ex.what()) == "native session expiration intervals must be greater than zero",
+                   std::string("message: ") + ex.what());
+        }
+    }
+    expect(whole.session_count() == 1U, "sessions in use are not reaped");
 
     if (failures) {
         std::printf("%d stage check(s) failed\n", failures);
