@@ -3195,12 +3195,14 @@ void launch_attention(const float* q, const StepDev* step, int32_t max_len, int3
         throw std::invalid_argument("attention step has too many query rows per kv head");
     }
     dim3 grid(slots, n_head_kv * qgroups, n_seq), block(kAttnThreads);
-    // On matrix cores a work-group walks spw consecutive splits when the
-    // step's (split, kv head x query group, sequence) work-groups would
-    // exceed one resident round: every split keeps its own partial, so the
-    // results do not depend on spw.
+    // On matrix cores a work-group of a decode or verify step walks spw
+    // consecutive splits when the step's (split, kv head x query group,
+    // sequence) work-groups would exceed one resident round: every split keeps
+    // its own partial, so the results do not depend on spw. (Prefill chunks,
+    // whose splits already hold 256 keys or more, run one split per
+    // work-group: two per work-group made 64-row chunks 16 -> 20 us.)
     int spw = 1;
-    if (mfma) {
+    if (mfma && max_len <= kQuadGroupRows) {
         const int cols = n_head_kv * qgroups * n_seq;
         spw = std::min(slots, (slots * cols + kAttnResidentWgs - 1) / kAttnResidentWgs);
         grid.x = (slots + spw - 1) / spw;
