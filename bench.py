@@ -11,7 +11,9 @@ executor, which coalesces their decode steps into one multi-sequence
 forward. A step is one such batched pass; after `--warmup` untimed passes
 (a run that also captures the step graphs) exactly `--steps` passes are
 timed (each runner generates steps + 1 tokens, the first from its prefill),
-and `value` = aggregate decode tokens / decode wall time.
+and `value` = aggregate decode tokens / decode wall time (from the runners'
+common decode start to the last runner's last token; closing the sessions
+afterwards is not decode work).
 
 Beside it: greedy decode at batch 1 (one step = one token through all 28
 layers, the head and the on-GPU argmax), draft verification (k = 4) timed

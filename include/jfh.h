@@ -476,7 +476,8 @@ jfh_status jfh_generate_draft(jfh_engine * engine, const int32_t * prompt, uint3
  * each); out_tokens receives max_tokens slots per request, out_counts and
  * stats (optional) one entry per request. The runners' decode phases start
  * together once every prefill is done; decode_wall_ms (optional) is the time
- * from that start until the last runner finishes. n_requests 1..8. */
+ * from that start until the last runner has read its last token (its session
+ * is closed afterwards, outside that time). n_requests 1..8. */
 jfh_status jfh_generate_concurrent(jfh_engine * engine, uint32_t n_requests, const int32_t * prompts,
                                    const uint32_t * prompt_lengths, uint32_t max_tokens, uint32_t draft_max,
                                    uint32_t max_ngram, uint32_t min_ngram, uint32_t batch_wait_us,

@@ -943,7 +943,6 @@ jfh_status jfh_generate_concurrent(jfh_engine* engine, uint32_t n_requests, cons
         };
         std::vector<rt::GenerationResult> results(n_requests);
         std::vector<jfh::PrefillMetrics> prefill(n_requests);
-        std::vector<clock::time_point> finished(n_requests);
         std::vector<std::thread> runners;
         for (uint32_t i = 0; i < n_requests; ++i) {
             runners.emplace_back([&, i] {
@@ -967,7 +966,6 @@ jfh_status jfh_generate_concurrent(jfh_engine* engine, uint32_t n_requests, cons
                     results[i].error_message = e.what();
                 }
                 if (!arrived) arrive();  // a runner that failed before decoding must not hold the others
-                finished[i] = clock::now();
             });
         }
         for (std::thread& t : runners) t.join();
@@ -983,7 +981,9 @@ jfh_status jfh_generate_concurrent(jfh_engine* engine, uint32_t n_requests, cons
                 fill_stats(*engine->engine, r, prefill[i], static_cast<uint32_t>(cfg.ctx_size), prompt_lengths[i],
                            stats[i]);
             }
-            last = std::max(last, finished[i]);
+            // the decode ends with a runner's last token; closing its session (freeing the
+            // KV cache) follows and is not decode work, as in the runner's own decode_ms
+            last = std::max(last, r.decode_end);
         }
         if (decode_wall_ms) *decode_wall_ms = std::chrono::duration<double, std::milli>(last - decode_start).count();
     });

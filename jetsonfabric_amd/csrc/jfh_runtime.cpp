@@ -897,7 +897,8 @@ GenerationResult run_generation(const inference::Executor& executor, const Gener
             emit(target.tokens[i]);
         }
     }
-    result.decode_ms = std::chrono::duration<double, std::milli>(clock::now() - t1).count();
+    result.decode_end = clock::now();
+    result.decode_ms = std::chrono::duration<double, std::milli>(result.decode_end - t1).count();
     executor.close_session(request.session_id);
     result.ok = true;
     result.finish_reason = eog ? "stop" : "length";

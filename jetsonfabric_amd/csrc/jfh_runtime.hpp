@@ -275,6 +275,8 @@ struct GenerationResult {
     std::string error_message;
     double time_to_first_token_ms = 0.0;
     double decode_ms = 0.0;
+    // when the last token was read (before the session is closed)
+    std::chrono::steady_clock::time_point decode_end{};
 };
 
 // GenerationRunner::run restricted to one local stage that owns every layer.

@@ -637,7 +637,7 @@ class NativeEngine:
                             max_ngram: int = 4, min_ngram: int = 2, batch_wait_us: int = 500):
         """Concurrent GenerationRunner loops over a continuous-batching executor
         (continuous_batching_executor.cpp:14-200); returns (results per prompt,
-        decode wall ms from the common decode start to the last finish)."""
+        decode wall ms from the common decode start to the last runner's last token)."""
         n = len(prompts)
         flat = [t for p in prompts for t in p]
         lengths = (ctypes.c_uint32 * n)(*[len(p) for p in prompts])
