@@ -38,6 +38,7 @@ __device__ __forceinline__ global_ptr<T> as_global(T* p) {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint4 load_u4(global_ptr<const uint16_t> p) {
     const u32x4 v = *(global_ptr<const u32x4>) p;
@@ -518,6 +519,12 @@ struct Tile;
 // matmuls all use it, so they round alike.
 __device__ __forceinline__ float q4k_term(float acc, float xd, float d, float dmin, int isum, int msum) {
     const float t = __builtin_fmaf(d, static_cast<float>(isum), -(dmin * static_cast<float>(msum)));
+    return __builtin_fmaf(xd, t, acc);
+}
+
+// q4k_term with the min sum given as the float of that integer
+__device__ __forceinline__ float q4k_term_f(float acc, float xd, float d, float dmin, int isum, float msum) {
+    const float t = __builtin_fmaf(d, static_cast<float>(isum), -(dmin * msum));
     return __builtin_fmaf(xd, t, acc);
 }
 
@@ -1062,6 +1069,65 @@ struct TileQ2Quad {
     }
 };
 
+// Q2_K tiles x 4..16 int8 token rows on matrix cores with the sub-block
+// scales folded into the weight operand: a Q2_K scale (4 bits) times a code
+// (2 bits) is at most 45, an int8, so one v_mfma_i32_16x16x64_i8 per 64
+// values contracts sc * code against the tokens' codes and four of them give
+// every (token, row) the tile's integer total sum_j sc_j dot_j over all
+// sixteen sub-blocks, with no per-sub-block arithmetic. Lane (i, G) brings
+// token i's codes of lane group G's chunk c (activation words 4 c .. 4 c + 3
+// of its slice) and row i's codes of sub-block 4 G + c at the same positions
+// (the 2-bit fields at shift 2 q of Q[c] pair with word 4 c + q, as in the
+// decode dot), times that sub-block's scale. The min sums sum_j m_j S_j are
+// exact integers below 2^24 from four v_mfma_f32_16x16x4f32 (K = lane group
+// G: sub-block 4 c + G). D gives lane (i, G) tokens 4 G + r, r < 4, of row
+// i: the lane keeps them in acc[0..3] (token-major, one lane group per
+// token) and takes the decode dot's one float step per tile on the same
+// integers, so rows equal the decode rows bit for bit.
+struct TileQ2Fold {
+    using Regs = TileQ2Quad::Regs;
+    static __device__ __forceinline__ Regs load(const uint8_t* t, int lane) { return TileQ2Quad::load(t, lane); }
+    template <int NT, bool A32>
+    static __device__ __forceinline__ void dot(const Regs& r, int G, const XLds& x, int nt, float* acc) {
+        static_assert(NT % 4 == 0 && NT <= 16, "token groups of up to 16 rows");
+        static_assert(!A32, "K-quant matrices take 256-value activation blocks");
+        const int i = threadIdx.x & 15;
+        const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
+        const uint32_t Q[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
+        const uint32_t scw[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};  // row i's scale bytes, sub-blocks 4 g + m
+        const uint32_t own = G == 0 ? scw[0] : G == 1 ? scw[1] : G == 2 ? scw[2] : scw[3];
+        constexpr uint32_t M2 = 0x03030303u;
+        const int ta = min(i, nt - 1);  // token rows past the step repeat its last row (never stored)
+        const u32x4* src = reinterpret_cast<const u32x4*>(x.q + ta * x.q_stride);
+        i32x4 D = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const u32x4 av = src[c];
+            const uint16_t sc = static_cast<uint16_t>((own >> (8 * c)) & 0xFu);
+            const u16x2 sv = {sc, sc};
+            u32x4 bv;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                bv[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, (Q[c] >> (2 * q)) & M2) * sv);
+            D = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, av), __builtin_bit_cast(i32x4, bv), D,
+                                                      0, 0, 0);
+        }
+        f32x4 ms = {0.0F, 0.0F, 0.0F, 0.0F};
+        const int16_t* srow = x.s + ta * x.s_stride;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float sa = static_cast<float>(srow[4 * c + G]);
+            const float mb = static_cast<float>((scw[c] >> (8 * G + 4)) & 0xFu);
+            ms = __builtin_amdgcn_mfma_f32_16x16x4f32(sa, mb, ms, 0, 0, 0);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int t = min(4 * G + q, nt - 1);
+            acc[q] = q4k_term_f(acc[q], x.d[t * x.d_stride], d, dmin, D[q], ms[q]);
+        }
+    }
+};
+
 // The token-quad tile of a weight format (void: none).
 template <uint32_t TYPE>
 struct QuadTile {
@@ -1272,9 +1338,12 @@ __global__ __launch_bounds__(kMmThreads) void k_mm(GemvArgs a, MmGeom geo) {
     constexpr bool GAIN = IN == kInNormed;
     constexpr int DB = A32 ? 8 : 1;  // activation scales per 256 values
     constexpr int NB = GAIN ? kStageBatch : kStageBatchFloat;  // blocks per wave of a float staging batch
-    // int8 or normalized rows of a format with a token-quad tile, in token quads, run on matrix cores
-    constexpr bool QUAD = kHasQuads<TYPE> && (A8 || GAIN) && NT % 4 == 0;
-    using T = std::conditional_t<QUAD, typename QuadTile<TYPE>::type, Tile<TYPE>>;
+    // int8 or normalized rows of a format with a token-quad tile, in token quads, run on matrix cores;
+    // Q2_K token groups on the folded-scale tile (token-major: lane group G holds tokens 4 G .. 4 G + 3)
+    constexpr bool FOLD = TYPE == 9 && (A8 || GAIN) && NT % 4 == 0;
+    constexpr bool QUAD = kHasQuads<TYPE> && (A8 || GAIN) && NT % 4 == 0 && !FOLD;
+    using T = std::conditional_t<FOLD, TileQ2Fold,
+                                 std::conditional_t<QUAD, typename QuadTile<TYPE>::type, Tile<TYPE>>>;
     using Regs = typename T::Regs;
     constexpr int W = kMmWaves;
     constexpr uint32_t TB = tile_bytes(TYPE);
@@ -1403,7 +1472,13 @@ __global__ __launch_bounds__(kMmThreads) void k_mm(GemvArgs a, MmGeom geo) {
                     cm = 0;
                     if (single) {
                         // (g0 + g1) + (g2 + g3) of the row's four lane-group sums
-                        if constexpr (QUAD) {
+                        if constexpr (FOLD) {
+                            // one lane group per token: its value is the sum
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                if (4 * grp + q < NT) done[4 * grp + q] = acc[q];
+                            }
+                        } else if constexpr (QUAD) {
 #pragma unroll
                             for (int q = 0; q < NT / 4; ++q) {
                                 done[4 * q + grp] =
@@ -1474,6 +1549,11 @@ __global__ __launch_bounds__(kMmThreads) void k_mm(GemvArgs a, MmGeom geo) {
 #pragma unroll
         for (int w = 0; w < W; ++w) {
             float p[4];
+            if constexpr (FOLD) {
+                // token t's running sum sits in lane group t / 4, slot t % 4 alone
+                v += part[((r * W + w) * 64 + i + 16 * (t >> 2)) * NT + (t & 3)];
+                continue;
+            }
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 p[g] = QUAD ? part[((r * W + w) * 64 + i + 16 * (t & 3)) * NT + 4 * (t >> 2) + g]
@@ -1521,12 +1601,6 @@ __device__ __forceinline__ i32x4 mfma_i8(long a, long b) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, i32x4{0, 0, 0, 0}, 0, 0, 0);
 }
 
-
-// q4k_term with the min sum given as the float of that integer
-__device__ __forceinline__ float q4k_term_f(float acc, float xd, float d, float dmin, int isum, float msum) {
-    const float t = __builtin_fmaf(d, static_cast<float>(isum), -(dmin * msum));
-    return __builtin_fmaf(xd, t, acc);
-}
 
 // Per-format operands of one tile for lane (row i, lane group G) and the
 // scale arithmetic of its 16 (lane group g, token 4 G + j) terms.
