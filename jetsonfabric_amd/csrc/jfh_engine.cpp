@@ -727,15 +727,15 @@ void Engine::read_kv(const Session& s, uint32_t layer, uint32_t n, uint16_t* k, 
     layer -= layer_start_;  // the resident layer
     hip_check(hipStreamSynchronize(stream_), "synchronize before cache read");
     const size_t hd = p.head_dim, rows = static_cast<size_t>(n) * hd, stride = s.stride_;
-    std::vector<uint16_t> vt(rows);
+    // V tiles of 16 positions, [position / 16][dim][position % 16] -> [position][dim]
+    const size_t tiled = (static_cast<size_t>(n) + 15) / 16 * 16 * hd;
+    std::vector<uint16_t> vt(tiled);
     for (uint32_t h = 0; h < p.n_head_kv; ++h) {
         const size_t base = (static_cast<size_t>(layer) * p.n_head_kv + h) * stride * hd;
         hip_check(hipMemcpy(k + h * rows, s.k_ + base, rows * sizeof(uint16_t), hipMemcpyDeviceToHost), "read K cache");
-        // V^T [dim][stride] -> [position][dim]
-        hip_check(hipMemcpy2D(vt.data(), n * sizeof(uint16_t), s.v_ + base, stride * sizeof(uint16_t),
-                              n * sizeof(uint16_t), hd, hipMemcpyDeviceToHost), "read V cache");
-        for (size_t d = 0; d < hd; ++d) {
-            for (size_t i = 0; i < n; ++i) v[h * rows + i * hd + d] = vt[d * n + i];
+        hip_check(hipMemcpy(vt.data(), s.v_ + base, tiled * sizeof(uint16_t), hipMemcpyDeviceToHost), "read V cache");
+        for (size_t i = 0; i < n; ++i) {
+            for (size_t d = 0; d < hd; ++d) v[h * rows + i * hd + d] = vt[(i & ~size_t{15}) * hd + d * 16 + (i & 15)];
         }
     }
 }
@@ -746,17 +746,21 @@ void Engine::import_kv(Session& s, uint32_t n, const uint16_t* k, const uint16_t
     if (n == 0 || n > s.capacity_) fail(Status::InvalidArgument, "imported cache rows exceed the session capacity");
     hip_check(hipStreamSynchronize(stream_), "synchronize before cache import");
     const size_t hd = p.head_dim, rows = static_cast<size_t>(n) * hd, stride = s.stride_;
-    std::vector<uint16_t> vt(rows);
+    // [position][dim] -> V tiles of 16 positions, [position / 16][dim][position % 16]
+    // (positions past n in the last tile are zeros: never read below the session length)
+    const size_t tiled = (static_cast<size_t>(n) + 15) / 16 * 16 * hd;
+    std::vector<uint16_t> vt(tiled);
     for (uint32_t l = 0; l < resident_layers(); ++l) {
         for (uint32_t h = 0; h < p.n_head_kv; ++h) {
             const size_t idx = static_cast<size_t>(l) * p.n_head_kv + h;
             hip_check(hipMemcpy(s.k_ + idx * stride * hd, k + idx * rows, rows * sizeof(uint16_t),
                                 hipMemcpyHostToDevice), "import K cache");
+            std::fill(vt.begin(), vt.end(), uint16_t{0});
             for (size_t i = 0; i < n; ++i) {
-                for (size_t d = 0; d < hd; ++d) vt[d * n + i] = v[idx * rows + i * hd + d];
+                for (size_t d = 0; d < hd; ++d) vt[(i & ~size_t{15}) * hd + d * 16 + (i & 15)] = v[idx * rows + i * hd + d];
             }
-            hip_check(hipMemcpy2D(s.v_ + idx * stride * hd, stride * sizeof(uint16_t), vt.data(), n * sizeof(uint16_t),
-                                  n * sizeof(uint16_t), hd, hipMemcpyHostToDevice), "import V cache");
+            hip_check(hipMemcpy(s.v_ + idx * stride * hd, vt.data(), tiled * sizeof(uint16_t), hipMemcpyHostToDevice),
+                      "import V cache");
         }
     }
     s.position_ = n;

@@ -82,7 +82,7 @@ private:
     uint32_t position_ = 0;
     uint32_t prefill_position_ = 0;
     uint16_t* k_ = nullptr;  // [resident layer][kv head][stride][head_dim]
-    uint16_t* v_ = nullptr;  // [resident layer][kv head][head_dim][stride] (transposed)
+    uint16_t* v_ = nullptr;  // [resident layer][kv head][stride / 16][head_dim][16] (16-position tiles)
     uint64_t kv_bytes_ = 0;
     PrefillMetrics prefill_metrics_;
 };

@@ -1202,8 +1202,10 @@ __device__ __forceinline__ void qkv_store(const GemvArgs& a, int t, int gr, floa
     } else {
         const int g = gr - Hq - kv;
         const int head = g / hd, dcol = g % hd;
-        // V is stored transposed: [layer][kv head][dim][position]
-        const size_t at = ((static_cast<size_t>(o.layer) * o.n_head_kv + head) * hd + dcol) * sd.capacity + pos;
+        // V is stored in 16-position tiles, transposed within a tile:
+        // [layer][kv head][position / 16][dim][position % 16]
+        const size_t at = ((static_cast<size_t>(o.layer) * o.n_head_kv + head) * sd.capacity + (pos & ~15)) * hd +
+                          static_cast<size_t>(dcol) * 16 + (pos & 15);
         as_global(sd.v)[at] = f2h(va);
     }
 }
@@ -2335,13 +2337,15 @@ __device__ __forceinline__ void attn_load_tile(global_ptr<const uint16_t> kc, gl
 #pragma unroll
         for (int c = 0; c < HD / 32; ++c) kr[c] = load_u4(krow + qq * (HD / 4) + 8 * c);
     }
-    // V is stored transposed ([dim][position]): the lane's two dims come from two rows
+    // V is stored in 16-position tiles ([position / 16][dim][position % 16]): the
+    // lane's two dims come from two rows of the key's tile
     const int d0 = min(2 * lane, hd - 1), d1 = min(2 * lane + 1, hd - 1);
 #pragma unroll
     for (int u = 0; u < kAttnTile; ++u) {
         const int kj = min(t0 + u, capacity - 1);
-        const uint32_t lo = vc[static_cast<size_t>(d0) * capacity + kj];
-        const uint32_t hi = vc[static_cast<size_t>(d1) * capacity + kj];
+        const size_t tile = static_cast<size_t>(kj & ~15) * hd + (kj & 15);
+        const uint32_t lo = vc[tile + static_cast<size_t>(d0) * 16];
+        const uint32_t hi = vc[tile + static_cast<size_t>(d1) * 16];
         vv[u] = 2 * lane < hd ? (lo | (hi << 16)) : 0u;
     }
 }
@@ -2548,8 +2552,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
 // takes 16-key tiles:
 //   S^T[16 keys][16 rows] = K[16 keys][hd] . Q^T[hd][16 rows]     (16x16x32 f16)
 //   O^T[hd][16 rows]     += V^T[hd][16 keys] . P^T[16 keys][16 rows] (16x16x16 f16)
-// K is read as stored (position-major rows) and V from its transposed cache
-// ([dim][position]), so every operand is a contiguous per-lane load. The
+// K is read as stored (position-major rows) and V from its tile-blocked cache
+// (per 16 positions, [dim][position]), so every operand is a contiguous
+// per-lane load and a tile's V is one contiguous block. The
 // queries (scaled by hd^-1/2) and the probabilities enter as f16 hi + lo
 // pairs, which keeps the products at about 22 bits. Lane l holds row l % 16
 // of the S^T and O^T fragments, so a row's online-softmax state lives in the
@@ -2569,9 +2574,10 @@ __device__ __forceinline__ void attn_mfma_load(global_ptr<const uint16_t> kc, gl
     global_ptr<const uint16_t> krow = kc + static_cast<size_t>(tl + r) * HD + 8 * grp;
 #pragma unroll
     for (int s = 0; s < HD / 32; ++s) kr[s] = *(global_ptr<const u32x4>) (krow + 32 * s);
+    // the tile's V block (HD dims x 16 positions, 4 KB at HD 128) is contiguous
 #pragma unroll
     for (int d = 0; d < HD / 16; ++d) {
-        vr[d] = *(global_ptr<const u32x2>) (vt + static_cast<size_t>(16 * d + r) * capacity + tl + 4 * grp);
+        vr[d] = *(global_ptr<const u32x2>) (vt + static_cast<size_t>(tl) * HD + (16 * d + r) * 16 + 4 * grp);
     }
 }
 
