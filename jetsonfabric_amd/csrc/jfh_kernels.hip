@@ -2171,6 +2171,232 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide_rg(GemvArgs a, int32_t n
                                          &red[0][0][0][0]);
 }
 
+// The wide Q4_K matmul for steps with many row groups (the gate / up matrix
+// of a prefill chunk): the sub-block scales are folded into the weight
+// operand, each wave owns one 16-row group over the whole of K, and the
+// work-group's waves share every activation tile through LDS.
+//
+// Scale fold: a Q4_K scale sc (6 bits) times a code (4 bits) does not fit an
+// int8, but sc = 8 sh + sl with sh, sl < 8 does: sl * code and sh * code are
+// at most 105, so two chains of v_mfma_i32_16x16x64_i8 give every (row,
+// token) the tile's totals L = sum_j sl_j dot_j and H = sum_j sh_j dot_j, and
+// L + 8 H is the integer total sum_j sc_j dot_j of the decode dot. Lane (i,
+// G) brings row i's codes of sub-block pair G (chunks 0, 1: the low nibbles,
+// sub-block 2 G; chunks 2, 3: the high ones, 2 G + 1), each word folded with
+// its sub-block's sl or sh by one packed 16-bit multiply (the byte products
+// stay below 256, so no carry crosses a byte), against token i's activation
+// bytes 64 G .. 64 G + 63 at the same positions. The folded operands are made
+// once per K tile and serve every token tile of the work-group. The min sums
+// sum_j m_j S_j (exact integers below 2^24) come from two
+// v_mfma_f32_16x16x4f32 (K = lane group G: sub-blocks 2 G, 2 G + 1). With the
+// weights as the first operand D gives lane (i, G) rows 4 G + r of token i.
+//
+// Order: the decode matmul's wave w sums the tiles w, w + 8, ... with one
+// q4k_term_f step each and the eight partials are added in wave order. A wave
+// here walks the tiles in that order (0, 8, 16, ..., then 1, 9, ..., ...),
+// keeps the running partial of the current chain and adds it to the total
+// when the chain ends, so every row equals the decode row bit for bit with no
+// cross-wave reduction.
+//
+// Staging: the work-group's token rows of the next K tile (codes, 16-value
+// sums, scales) are loaded into registers while the current tile runs, then
+// written to the other of two LDS buffers; one barrier per tile.
+constexpr int kStageRow = 272;  // bytes per staged token row: 256 codes + 16 bytes of padding (banks)
+
+template <int NW, int TP>
+__global__ __launch_bounds__(NW * kWave) void k_mm_wide_q4k(GemvArgs a, int32_t n_rg, int32_t tpw) {
+    constexpr int NTHR = NW * kWave;
+    constexpr int NTOK = 16 * TP;
+    constexpr uint32_t TB = tile_bytes(11);
+    constexpr uint32_t M4 = 0x0F0F0F0Fu;
+    constexpr int CODE_CHUNKS = NTOK * 16;  // 16-byte pieces of a staged tile's codes
+    static_assert(CODE_CHUNKS % NTHR == 0, "whole code pieces per thread");
+    constexpr int CPT = CODE_CHUNKS / NTHR;
+    constexpr int VSTRIDE = 16 * NW + 1;  // epilogue row stride (floats)
+    __shared__ __align__(16) uint8_t codes[2][NTOK * kStageRow];
+    __shared__ __align__(16) f32x4 sums[2][NTOK][2];  // the 32-value code sums of the tile's eight sub-blocks
+    __shared__ float scales[2][NTOK];
+    static_assert(sizeof(float) * NTOK * VSTRIDE <= sizeof(codes), "epilogue values alias the staging buffers");
+    float* vals = reinterpret_cast<float*>(&codes[0][0]);
+    const int n_tok = a.n_tok, n_tt = (n_tok + 15) / 16, n_grp = (n_tt + tpw - 1) / tpw;
+    const int n_sets = (n_rg + NW - 1) / NW;
+    // work-group k runs on XCD k % 8: the token groups of one row-group set share an XCD (and its L2)
+    const int q = static_cast<int>(blockIdx.x) >> 3;
+    const int grp = q % n_grp, set = (q / n_grp) * 8 + static_cast<int>(blockIdx.x & 7u);
+    if (set >= n_sets) return;
+    const int K = static_cast<int>(a.mat.cols), nb = K / 256;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+    const int i = lane & 15, G = lane >> 4;
+    const int tt0 = grp * tpw, ntl = min(TP, min(n_tt, tt0 + tpw) - tt0);
+    const int t0 = 16 * tt0, nt = min(16 * (tt0 + ntl), n_tok) - t0;
+    const GemvArgs out = token_slice(a, t0, nt);
+    const Act8 xq = a.xq;
+    const int rg = set * NW + wave;
+    const bool active = rg < n_rg;  // waves past the matrix stage and wait but compute nothing
+    const uint8_t* base = a.mat.data + static_cast<size_t>(min(rg, n_rg - 1)) * nb * TB;
+
+    // staging loads of K tile b into registers (token rows past the step repeat its last row)
+    struct Stage {
+        u32x4 c[CPT];
+        u32x4 s;
+        float d;
+    };
+    // element offsets are unsigned 32-bit (rows of at most kWideRows tokens)
+    auto stage_load = [&](int b) {
+        Stage st;
+#pragma unroll
+        for (int u = 0; u < CPT; ++u) {
+            const uint32_t e = threadIdx.x + u * NTHR, tk = e >> 4, part = e & 15;
+            const uint32_t tok = static_cast<uint32_t>(min(t0 + static_cast<int>(tk), n_tok - 1));
+            st.c[u] = *reinterpret_cast<const u32x4*>(xq.q + (tok * static_cast<uint32_t>(K) + 256u * b + 16u * part));
+        }
+        if (threadIdx.x < 2 * NTOK) {
+            const uint32_t tok = static_cast<uint32_t>(min(t0 + static_cast<int>(threadIdx.x >> 1), n_tok - 1));
+            st.s = *reinterpret_cast<const u32x4*>(xq.s + (tok * static_cast<uint32_t>(K / 16) + 16u * b + 8u * (threadIdx.x & 1)));
+        }
+        if (threadIdx.x < NTOK) {
+            const uint32_t tok = static_cast<uint32_t>(min(t0 + static_cast<int>(threadIdx.x), n_tok - 1));
+            st.d = xq.d[tok * static_cast<uint32_t>(nb) + b];
+        }
+        return st;
+    };
+    // the 16-value sums, pairwise: sub-block sums as exact floats
+    auto sub_sum = [](uint32_t w) {
+        return static_cast<float>(static_cast<int16_t>(w & 0xFFFFu) + (static_cast<int32_t>(w) >> 16));
+    };
+    auto stage_store = [&](const Stage& st, int buf) {
+#pragma unroll
+        for (int u = 0; u < CPT; ++u) {
+            const int e = threadIdx.x + u * NTHR, tk = e >> 4, part = e & 15;
+            *reinterpret_cast<u32x4*>(&codes[buf][tk * kStageRow + 16 * part]) = st.c[u];
+        }
+        if (threadIdx.x < 2 * NTOK) {
+            sums[buf][threadIdx.x >> 1][threadIdx.x & 1] =
+                f32x4{sub_sum(st.s.x), sub_sum(st.s.y), sub_sum(st.s.z), sub_sum(st.s.w)};
+        }
+        if (threadIdx.x < NTOK) scales[buf][threadIdx.x] = st.d;
+    };
+    // the lane's share of a weight tile: rows 4 G + r's scales, row i's field pair and code words
+    struct Raw {
+        uint32_t dd[4];
+        uint2 fw;
+        u32x4 w0, w1;
+    };
+    auto load_raw = [&](int b) {
+        const uint8_t* t = base + static_cast<size_t>(b) * TB;
+        Raw r;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r.dd[j] = *reinterpret_cast<const uint32_t*>(t + 16 * (4 * G + j));
+        r.fw = *reinterpret_cast<const uint2*>(t + 16 * i + 4 + 4 * ((3 * G) >> 2));
+        r.w0 = *reinterpret_cast<const u32x4*>(t + 256 + 16 * lane);
+        r.w1 = *reinterpret_cast<const u32x4*>(t + 1280 + 16 * lane);
+        return r;
+    };
+    // the tile after b in the decode waves' order
+    auto next_tile = [&](int b) { return b + 8 < nb ? b + 8 : (b & 7) + 1; };
+
+    float total[TP][4], chain[TP][4];
+#pragma unroll
+    for (int tl = 0; tl < TP; ++tl) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) total[tl][j] = chain[tl][j] = 0.0F;
+    }
+    stage_store(stage_load(0), 0);
+    Raw cur = load_raw(0);
+    __syncthreads();
+    int b = 0;
+    for (int s = 0; s < nb; ++s) {
+        const int buf = s & 1;
+        const int bn = s + 1 < nb ? next_tile(b) : b;  // clamped: issued unconditionally
+        const Stage st = stage_load(bn);
+        const Raw nxt = load_raw(bn);
+        if (active) {
+            // lane group G's 24-bit field of row i: sc 2G | sc 2G+1 | m 2G | m 2G+1
+            const uint32_t f = __builtin_amdgcn_alignbyte(cur.fw.y, cur.fw.x, (3 * G) & 3);
+            const uint32_t sca = f & 63u, scb = (f >> 6) & 63u;
+            const float ma = static_cast<float>((f >> 12) & 63u), mb = static_cast<float>((f >> 18) & 63u);
+            const u16x2 la = {static_cast<uint16_t>(sca & 7u), static_cast<uint16_t>(sca & 7u)};
+            const u16x2 ha = {static_cast<uint16_t>(sca >> 3), static_cast<uint16_t>(sca >> 3)};
+            const u16x2 lb = {static_cast<uint16_t>(scb & 7u), static_cast<uint16_t>(scb & 7u)};
+            const u16x2 hb = {static_cast<uint16_t>(scb >> 3), static_cast<uint16_t>(scb >> 3)};
+            auto fold = [](uint32_t c, u16x2 sv) {
+                return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, c) * sv);
+            };
+            float d[4], dmin[4];  // rows 4 G + j
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                d[j] = h2f(cur.dd[j]);
+                dmin[j] = h2f(cur.dd[j] >> 16);
+            }
+            u32x4 BL[4], BH[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t l0 = cur.w0[k] & M4, l1 = cur.w1[k] & M4;
+                const uint32_t h0 = (cur.w0[k] >> 4) & M4, h1 = (cur.w1[k] >> 4) & M4;
+                BL[0][k] = fold(l0, la);
+                BL[1][k] = fold(l1, la);
+                BL[2][k] = fold(h0, lb);
+                BL[3][k] = fold(h1, lb);
+                BH[0][k] = fold(l0, ha);
+                BH[1][k] = fold(l1, ha);
+                BH[2][k] = fold(h0, hb);
+                BH[3][k] = fold(h1, hb);
+            }
+#pragma unroll
+            for (int tl = 0; tl < TP; ++tl) {
+                if (tl < ntl) {
+                    const int r = 16 * tl + i;
+                    const u32x4* src = reinterpret_cast<const u32x4*>(&codes[buf][r * kStageRow + 64 * G]);
+                    const float2 xs = reinterpret_cast<const float2*>(&sums[buf][r][0])[G];
+                    const float xd = scales[buf][r];
+                    i32x4 DL = {0, 0, 0, 0}, DH = {0, 0, 0, 0};
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) {
+                        const i32x4 av = __builtin_bit_cast(i32x4, src[m]);
+                        DL = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, BL[m]), av, DL, 0, 0, 0);
+                        DH = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, BH[m]), av, DH, 0, 0, 0);
+                    }
+                    // token r's 32-value code sums of sub-blocks 2G, 2G + 1
+                    f32x4 ms = {0.0F, 0.0F, 0.0F, 0.0F};
+                    ms = __builtin_amdgcn_mfma_f32_16x16x4f32(ma, xs.x, ms, 0, 0, 0);
+                    ms = __builtin_amdgcn_mfma_f32_16x16x4f32(mb, xs.y, ms, 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        chain[tl][j] = q4k_term_f(chain[tl][j], xd, d[j], dmin[j], DL[j] + 8 * DH[j], ms[j]);
+                }
+            }
+            if (b + 8 >= nb) {
+                // the chain of tiles b mod 8 ends: its partial joins the total in wave order
+#pragma unroll
+                for (int tl = 0; tl < TP; ++tl) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        total[tl][j] += chain[tl][j];
+                        chain[tl][j] = 0.0F;
+                    }
+                }
+            }
+        }
+        if (s + 1 < nb) stage_store(st, buf ^ 1);
+        cur = nxt;
+        b = bn;
+        __syncthreads();
+    }
+    // the staging buffers are free (the loop ends on a barrier): rows and tokens to the epilogue
+    if (active) {
+#pragma unroll
+        for (int tl = 0; tl < TP; ++tl) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) vals[(16 * tl + i) * VSTRIDE + 16 * wave + 4 * G + j] = total[tl][j];
+        }
+    }
+    __syncthreads();
+    const int row0 = set * NW * 16;
+    const int nrows = min(16 * NW, static_cast<int>(a.mat.rows) - row0);
+    gemv_epilogue<NTHR, kNoLogits>(out, row0, nrows, [&](int j, int tk) { return vals[tk * VSTRIDE + j]; }, nullptr);
+}
+
 // Float weights (F32/F16, small models): one wave per row, lanes over K,
 // float activations (RMS-normalized in the prologue when a gain is given).
 constexpr int kFloatThreads = 256;
@@ -3152,6 +3378,8 @@ void launch_quantize_norm(const float* x, int32_t stride, const int32_t* gather,
 constexpr int kWideMinWgs = 512;
 constexpr int kWideRgMinWgs = 256;  // one work-group per CU
 constexpr int kWideLogitsWgs = 1024;
+constexpr int kWideQ4kWaves = 4;
+constexpr int kWideQ4kMinWgs = 256;
 
 bool wide_matmul_supported(uint32_t type) { return type == 7 || type == 9 || type == 11 || type == 13; }
 
@@ -3185,6 +3413,19 @@ void launch_gemv_wide(const GemvArgs& a_in, hipStream_t stream) {
     int tpw = min(n_tt, kWideTpw);
     while (tpw > 1 && n_rg * ((n_tt + tpw - 1) / tpw) < kWideMinWgs) --tpw;
     const bool merged = a.mode == kLogits;  // the head kernel: the only one with the argmax epilogue
+    if (a.mat.type == 11 && !merged) {
+        // Q4_K matrices with many row groups: whole-K waves over all of the
+        // step's token tiles, while that still leaves kWideQ4kMinWgs work-groups
+        const int n_sets = (n_rg + kWideQ4kWaves - 1) / kWideQ4kWaves;
+        if (n_tt <= 4 && n_sets >= kWideQ4kMinWgs) {
+            const dim3 g((n_sets + 7) / 8 * 8), b(kWideQ4kWaves * kWave);
+            if (n_tt > 2) launch(k_mm_wide_q4k<kWideQ4kWaves, 4>, g, b, 0, stream, a, n_rg, n_tt);
+            else if (n_tt == 2) launch(k_mm_wide_q4k<kWideQ4kWaves, 2>, g, b, 0, stream, a, n_rg, n_tt);
+            else launch(k_mm_wide_q4k<kWideQ4kWaves, 1>, g, b, 0, stream, a, n_rg, n_tt);
+            check(hipGetLastError(), "wide matmul launch");
+            return;
+        }
+    }
     // K-quant layer matrices: one token tile and several row groups per work-group, every
     // activation load shared by the row groups: four (Q4_K only: the other formats'
     // operands take the registers) while kWideMinWgs work-groups remain, else two while

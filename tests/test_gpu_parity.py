@@ -148,6 +148,65 @@ def test_wide_matmul_over_row_group_sets_equals_single_rows(wide_typed):
         assert np.allclose(wide, ref, rtol=1e-4, atol=2e-5 * scale), f"{n_tok} rows: max err {np.abs(wide - ref).max():.3e}"
 
 
+# A Q4_K gate/up matrix of 16384 rows (256 sets of four row groups) over K =
+# 2560 (ten tiles: the decode waves' chains of two and one tiles): steps of
+# 9..64 rows run the whole-K-wave kernel that folds the sub-block scales into
+# the weight operand and shares each activation tile through LDS.
+WIDE_Q4 = jf.ModelConfig(n_layer=1, n_embd=2560, n_ff=8192, n_head=20, n_head_kv=4, n_vocab=4096, n_ctx=256)
+
+
+@pytest.fixture(scope="module")
+def wide_q4():
+    model = _model(WIDE_Q4, jf.Q4_K, jf.Q4_K, jf.Q6_K, seed=77, bias=True)
+    engine = jf.NativeEngine(model)
+    yield model, engine, jo.OracleModel.from_model(model)
+    engine.close()
+
+
+def test_folded_scale_wide_matmul_equals_single_rows(wide_q4):
+    """Every row of a 9..64-row step through the folded-scale kernel equals the
+    same row computed alone (the decode path), bit for bit, and the step
+    matches the oracle's matmul on the same int8 rows."""
+    model, engine, _ = wide_q4
+    name = "blk.0.ffn_gate.weight"
+    info = model.tensor(name)
+    cols, rows = info["shape"]
+    for n_tok in (9, 17, 33, 48, 64):
+        rng = np.random.default_rng(500 + n_tok)
+        x = rng.standard_normal((n_tok, cols)).astype(np.float32)
+        wide = engine.matmul(name, x, rows)
+        for r in range(n_tok):
+            single = engine.matmul(name, x[r:r + 1], rows)
+            assert np.array_equal(wide[r].view(np.uint32), single[0].view(np.uint32)), f"{n_tok} rows: row {r}"
+        ref = jo.matmul(jf.Q4_K, info["data"], cols, rows, x, jo.MODE_Q8)
+        scale = np.abs(ref).max()
+        assert np.allclose(wide, ref, rtol=1e-4, atol=2e-5 * scale), f"{n_tok} rows: max err {np.abs(wide - ref).max():.3e}"
+
+
+def test_folded_scale_prefill_matches_oracle_and_token_by_token(wide_q4):
+    """A 150-token prompt (chunks of 64, 64 and 22 rows: the SwiGLU gate/up
+    matrix on the folded-scale kernel) matches the oracle's logits, and a
+    session fed the prompt one token at a time reaches the same greedy
+    continuation."""
+    model, engine, om = wide_q4
+    prompt = _prompt(150, WIDE_Q4.n_vocab, 31)
+    s = engine.create_session(200)
+    ref = om.session(200, jo.MODE_Q8)
+    tok, lg = s.prefill_greedy(prompt, logits=True)
+    _, rl = ref.forward(prompt, 1)
+    assert_logits_match(rl[0], lg, tok, "chunked prefill")
+    one = engine.create_session(200)
+    first = one.prefill_greedy(prompt[:1])
+    for t in prompt[1:]:
+        first = one.decode_greedy(t)
+    assert first == tok
+    a, b = [tok], [first]
+    for _ in range(4):
+        a.append(s.decode_greedy(a[-1]))
+        b.append(one.decode_greedy(b[-1]))
+    assert a == b
+
+
 def test_tiny_fixture_known_answer():
     cfg = jf.ModelConfig(**tiny_fixture.CONFIG)
     model = jf.Model.build(cfg, tiny_fixture.tensors())
