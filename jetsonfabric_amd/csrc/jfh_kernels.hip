@@ -2397,6 +2397,140 @@ __global__ __launch_bounds__(NW * kWave) void k_mm_wide_q4k(GemvArgs a, int32_t 
     gemv_epilogue<NTHR, kNoLogits>(out, row0, nrows, [&](int j, int tk) { return vals[tk * VSTRIDE + j]; }, nullptr);
 }
 
+// The wide Q4_K matmul for steps with fewer row groups (the down, output
+// and qkv matrices of a prefill chunk): the decode matmul's eight waves (wave
+// w takes the K tiles w, w + 8, ...), R consecutive row groups and one
+// 16-token tile per work-group, and the folded-scale tile arithmetic of
+// k_mm_wide_q4k. A wave loads its K tile's activations (lane (i, G): token
+// i's bytes 64 G .. 64 G + 63, its code sums and scale) once and runs them
+// against the R row groups' folded weight operands, the next weight tile in
+// flight while one runs; the waves' partials are summed in wave order through
+// LDS, so every row equals the decode row bit for bit.
+template <int R>
+__global__ __launch_bounds__(kMmThreads) void k_mm_wide_q4r(GemvArgs a, int32_t n_rg) {
+    constexpr int W = kMmWaves;
+    constexpr uint32_t TB = tile_bytes(11);
+    constexpr uint32_t M4 = 0x0F0F0F0Fu;
+    __shared__ float red[W][16][16 * R];  // [wave][token][row]
+    __shared__ float vals[16][16 * R];
+    const int n_tok = a.n_tok, n_tt = (n_tok + 15) / 16;
+    // work-group k runs on XCD k % 8: the token tiles of one row-group set share an XCD (and its L2)
+    const int q = static_cast<int>(blockIdx.x) >> 3;
+    const int tt = q % n_tt, set = (q / n_tt) * 8 + static_cast<int>(blockIdx.x & 7u);
+    const int rg0 = set * R;
+    if (rg0 >= n_rg) return;
+    const int nrg = min(R, n_rg - rg0);
+    const int K = static_cast<int>(a.mat.cols), nb = K / 256;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+    const int i = lane & 15, G = lane >> 4;
+    const int t0 = 16 * tt, nt = min(16, n_tok - t0);
+    const GemvArgs out = token_slice(a, t0, nt);
+    const Act8 xq = a.xq;
+    // the lane's token (rows past the step repeat its last row; never stored)
+    const uint32_t tok = static_cast<uint32_t>(min(t0 + i, n_tok - 1));
+    const uint8_t* base = a.mat.data + static_cast<size_t>(rg0) * nb * TB;
+    struct Raw {
+        uint32_t dd[4];
+        uint2 fw;
+        u32x4 w0, w1;
+    };
+    auto load_raw = [&](int rr, int b) {
+        const uint8_t* t = base + (static_cast<size_t>(rr) * nb + b) * TB;
+        Raw r;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r.dd[j] = *reinterpret_cast<const uint32_t*>(t + 16 * (4 * G + j));
+        r.fw = *reinterpret_cast<const uint2*>(t + 16 * i + 4 + 4 * ((3 * G) >> 2));
+        r.w0 = *reinterpret_cast<const u32x4*>(t + 256 + 16 * lane);
+        r.w1 = *reinterpret_cast<const u32x4*>(t + 1280 + 16 * lane);
+        return r;
+    };
+    auto sub_sum = [](uint32_t w) {
+        return static_cast<float>(static_cast<int16_t>(w & 0xFFFFu) + (static_cast<int32_t>(w) >> 16));
+    };
+    float acc[R][4];
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[rr][j] = 0.0F;
+    }
+    Raw cur = load_raw(0, min(wave, nb - 1));
+    for (int b = wave; b < nb; b += W) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(xq.q + (tok * static_cast<uint32_t>(K) + 256u * b + 64u * G));
+        u32x4 xa[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) xa[m] = src[m];
+        const uint2 sw = *reinterpret_cast<const uint2*>(xq.s + (tok * static_cast<uint32_t>(K / 16) + 16u * b + 4u * G));
+        const float xd = xq.d[tok * static_cast<uint32_t>(nb) + b];
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) {
+            // the next weight tile (the next row group's, else the wave's next K tile's first; clamped)
+            const Raw nxt = rr + 1 < nrg ? load_raw(rr + 1, b) : load_raw(0, min(b + W, nb - 1));
+            if (rr < nrg) {
+                float d[4], dmin[4];  // rows 4 G + j
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    d[j] = h2f(cur.dd[j]);
+                    dmin[j] = h2f(cur.dd[j] >> 16);
+                }
+                // lane group G's 24-bit field of row i: sc 2G | sc 2G+1 | m 2G | m 2G+1
+                const uint32_t f = __builtin_amdgcn_alignbyte(cur.fw.y, cur.fw.x, (3 * G) & 3);
+                const uint32_t sca = f & 63u, scb = (f >> 6) & 63u;
+                const float ma = static_cast<float>((f >> 12) & 63u), mb = static_cast<float>((f >> 18) & 63u);
+                const u16x2 la = {static_cast<uint16_t>(sca & 7u), static_cast<uint16_t>(sca & 7u)};
+                const u16x2 ha = {static_cast<uint16_t>(sca >> 3), static_cast<uint16_t>(sca >> 3)};
+                const u16x2 lb = {static_cast<uint16_t>(scb & 7u), static_cast<uint16_t>(scb & 7u)};
+                const u16x2 hb = {static_cast<uint16_t>(scb >> 3), static_cast<uint16_t>(scb >> 3)};
+                auto fold = [](uint32_t c, u16x2 sv) {
+                    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, c) * sv);
+                };
+                i32x4 DL = {0, 0, 0, 0}, DH = {0, 0, 0, 0};
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const u32x4 w = m & 1 ? cur.w1 : cur.w0;
+                    const u16x2 sl = m < 2 ? la : lb, sh = m < 2 ? ha : hb;
+                    u32x4 bl, bh;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const uint32_t c = m < 2 ? w[k] & M4 : (w[k] >> 4) & M4;
+                        bl[k] = fold(c, sl);
+                        bh[k] = fold(c, sh);
+                    }
+                    const i32x4 av = __builtin_bit_cast(i32x4, xa[m]);
+                    DL = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, bl), av, DL, 0, 0, 0);
+                    DH = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, bh), av, DH, 0, 0, 0);
+                }
+                // token i's 32-value code sums of sub-blocks 2G, 2G + 1
+                f32x4 ms = {0.0F, 0.0F, 0.0F, 0.0F};
+                ms = __builtin_amdgcn_mfma_f32_16x16x4f32(ma, sub_sum(sw.x), ms, 0, 0, 0);
+                ms = __builtin_amdgcn_mfma_f32_16x16x4f32(mb, sub_sum(sw.y), ms, 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[rr][j] = q4k_term_f(acc[rr][j], xd, d[j], dmin[j], DL[j] + 8 * DH[j], ms[j]);
+            }
+            cur = nxt;
+        }
+    }
+    // per row group: the sum over waves in wave order
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) red[wave][i][16 * rr + 4 * G + j] = acc[rr][j];
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < 16 * 16 * nrg; e += kMmThreads) {
+        const int tk = e / (16 * nrg), r = e - tk * 16 * nrg;
+        float v = 0.0F;
+#pragma unroll
+        for (int w2 = 0; w2 < W; ++w2) v += red[w2][tk][r];
+        vals[tk][r] = v;
+    }
+    __syncthreads();
+    const int row0 = rg0 * 16;
+    const int nrows = min(16 * nrg, static_cast<int>(a.mat.rows) - row0);
+    gemv_epilogue<kMmThreads, kNoLogits>(out, row0, nrows, [&](int j, int tk) { return vals[tk][j]; }, nullptr);
+}
+
 // Float weights (F32/F16, small models): one wave per row, lanes over K,
 // float activations (RMS-normalized in the prologue when a gain is given).
 constexpr int kFloatThreads = 256;
@@ -3422,6 +3556,14 @@ void launch_gemv_wide(const GemvArgs& a_in, hipStream_t stream) {
             if (n_tt > 2) launch(k_mm_wide_q4k<kWideQ4kWaves, 4>, g, b, 0, stream, a, n_rg, n_tt);
             else if (n_tt == 2) launch(k_mm_wide_q4k<kWideQ4kWaves, 2>, g, b, 0, stream, a, n_rg, n_tt);
             else launch(k_mm_wide_q4k<kWideQ4kWaves, 1>, g, b, 0, stream, a, n_rg, n_tt);
+            check(hipGetLastError(), "wide matmul launch");
+            return;
+        }
+        // fewer row groups: two row groups and one token tile per work-group, the decode
+        // waves' K split, while one work-group per CU remains
+        if ((n_rg + 1) / 2 * n_tt >= kWideRgMinWgs) {
+            const dim3 g(((n_rg + 1) / 2 + 7) / 8 * 8 * n_tt), b(kMmThreads);
+            launch(k_mm_wide_q4r<2>, g, b, 0, stream, a, n_rg);
             check(hipGetLastError(), "wide matmul launch");
             return;
         }
