@@ -293,7 +293,7 @@ def main() -> int:
         f"drafts accepted {head['accepted']}/{head['drafted']}")
 
     # ---- batch-1 decode, verify, prefill and the per-kernel profiles
-    capacity = context + args.warmup + args.steps + 2 * k + 72
+    capacity = context + args.warmup + args.steps + 2 * k + 8 + engine.prefill_chunk
     session = engine.create_session(capacity)
     prompt = uniform_prompt(context, cfg.n_vocab, args.seed)
     t0 = time.perf_counter()
@@ -322,9 +322,9 @@ def main() -> int:
     vprof = session.profile_step(cont[:1 + k], iterations=args.profile_iters)
     verify_bytes = sum(p["bytes"] for p in vprof)
     log("verify profile (ms/step): " + ", ".join(f"{p['kernel']} {p['ms']:.3f}" for p in vprof[:8]))
-    chunk = uniform_prompt(64, cfg.n_vocab, args.seed + 3)
+    chunk = uniform_prompt(engine.prefill_chunk, cfg.n_vocab, args.seed + 3)
     pprof = session.profile_step(chunk, iterations=1, all_logits=False)
-    log("prefill chunk (64 rows) profile (ms): " + ", ".join(f"{p['kernel']} {p['ms']:.3f}" for p in pprof[:8]))
+    log(f"prefill chunk ({len(chunk)} rows) profile (ms): " + ", ".join(f"{p['kernel']} {p['ms']:.3f}" for p in pprof[:8]))
     session.close()
 
     # the headline's batched step driven directly (no runner threads)

@@ -1958,13 +1958,14 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide(GemvArgs a, int32_t n_rg
     using T = WideTile<TYPE>;
     constexpr int W = kMmWaves;
     constexpr uint32_t TB = tile_bytes(TYPE);
+    constexpr int NTOK = 16 * kWideTpw;  // a work-group's token rows
     __shared__ float red[W][4][16][16];  // [wave][lane group][token][row] of one token tile
-    __shared__ float vals[kWideRows][16];
+    __shared__ float vals[NTOK][16];
     __shared__ u32x4 stage_s[W][16][2];
     __shared__ float stage_d[W][A32 ? 16 * 8 : 16];  // scales [token] (A32: [token][8])
-    __shared__ unsigned long long best[kWideRows];
-    float* lv = &red[0][0][0][0];  // the epilogue's scratch (kWideRows x 16 floats) once red is read
-    static_assert(sizeof(red) >= sizeof(float) * kWideRows * 16, "epilogue scratch");
+    __shared__ unsigned long long best[NTOK];
+    float* lv = &red[0][0][0][0];  // the epilogue's scratch (NTOK x 16 floats) once red is read
+    static_assert(sizeof(red) >= sizeof(float) * NTOK * 16, "epilogue scratch");
     const int n_tok = a.n_tok, n_tt = (n_tok + 15) / 16, n_grp = (n_tt + tpw - 1) / tpw;
     // work-group k runs on XCD k % 8: the token groups of one row group share an XCD (and its L2)
     const int q = static_cast<int>(blockIdx.x) >> 3;
@@ -1977,7 +1978,7 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide(GemvArgs a, int32_t n_rg
     const int tt0 = grp * tpw, ntl = min(n_tt, tt0 + tpw) - tt0;
     const int t0 = 16 * tt0, nt = min(16 * (tt0 + ntl), n_tok) - t0;
     const GemvArgs out = token_slice(a, t0, nt);
-    if (MERGED && threadIdx.x < kWideRows) best[threadIdx.x] = 0ull;
+    if (MERGED && threadIdx.x < NTOK) best[threadIdx.x] = 0ull;
     const Act8 xq = a.xq;
     auto load_act = [&](int tt, int b) { return wide_load_act<T::kSums, A32>(xq, tt, b, n_tok, K, lane); };
     for (int rr = 0; rr < (MERGED ? rpw : 1); ++rr) {
@@ -2067,7 +2068,7 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide_rg(GemvArgs a, int32_t n
     constexpr int W = kMmWaves;
     constexpr uint32_t TB = tile_bytes(TYPE);
     __shared__ float red[W][TP][16][16];  // [wave][token tile][token][row] of one row group
-    __shared__ float vals[kWideRows][16 * R];
+    __shared__ float vals[16 * TP][16 * R];
     __shared__ u32x4 stage_s[W][TP][16][2];
     __shared__ float stage_d[W][TP][A32 ? 16 * 8 : 16];  // scales [token] (A32: [token][8])
     const int n_tok = a.n_tok, n_tt = (n_tok + 15) / 16, n_grp = (n_tt + tpw - 1) / tpw;
@@ -3534,7 +3535,7 @@ int32_t wide_min_rows(uint32_t type) {
 void launch_gemv_wide(const GemvArgs& a_in, hipStream_t stream) {
     if (!wide_matmul_supported(a_in.mat.type) || a_in.xq.q == nullptr || a_in.xq.K != static_cast<int32_t>(a_in.mat.cols) ||
         a_in.mat.cols % kActBlock != 0 || a_in.n_tok < 1 || a_in.n_tok > kWideRows) {
-        throw std::invalid_argument("wide matmul takes Q4_K / Q6_K / Q8_0 / Q2_K weights and up to 64 pre-quantized token rows");
+        throw std::invalid_argument("wide matmul takes Q4_K / Q6_K / Q8_0 / Q2_K weights and up to kWideRows pre-quantized token rows");
     }
     if ((a_in.mode == kSwiGLU && a_in.mat.rows % (2 * kGluGroup) != 0) || (a_in.mode == kQKV && a_in.mat.rows % 2 != 0) ||
         (a_in.mode == kLogits && a_in.best == nullptr)) {
@@ -3551,11 +3552,13 @@ void launch_gemv_wide(const GemvArgs& a_in, hipStream_t stream) {
         // Q4_K matrices with many row groups: whole-K waves over all of the
         // step's token tiles, while that still leaves kWideQ4kMinWgs work-groups
         const int n_sets = (n_rg + kWideQ4kWaves - 1) / kWideQ4kWaves;
-        if (n_tt <= 4 && n_sets >= kWideQ4kMinWgs) {
-            const dim3 g((n_sets + 7) / 8 * 8), b(kWideQ4kWaves * kWave);
-            if (n_tt > 2) launch(k_mm_wide_q4k<kWideQ4kWaves, 4>, g, b, 0, stream, a, n_rg, n_tt);
-            else if (n_tt == 2) launch(k_mm_wide_q4k<kWideQ4kWaves, 2>, g, b, 0, stream, a, n_rg, n_tt);
-            else launch(k_mm_wide_q4k<kWideQ4kWaves, 1>, g, b, 0, stream, a, n_rg, n_tt);
+        if (n_sets >= kWideQ4kMinWgs) {
+            // up to four token tiles per work-group; longer steps run as several token groups
+            const int tpw4 = min(n_tt, 4), n_grp4 = (n_tt + tpw4 - 1) / tpw4;
+            const dim3 g((n_sets + 7) / 8 * 8 * n_grp4), b(kWideQ4kWaves * kWave);
+            if (tpw4 > 2) launch(k_mm_wide_q4k<kWideQ4kWaves, 4>, g, b, 0, stream, a, n_rg, tpw4);
+            else if (tpw4 == 2) launch(k_mm_wide_q4k<kWideQ4kWaves, 2>, g, b, 0, stream, a, n_rg, tpw4);
+            else launch(k_mm_wide_q4k<kWideQ4kWaves, 1>, g, b, 0, stream, a, n_rg, tpw4);
             check(hipGetLastError(), "wide matmul launch");
             return;
         }

@@ -10,7 +10,8 @@
 
 namespace jfh::gpu {
 
-constexpr int kMaxRows = 64;
+// Token rows of one step (a prefill chunk is at most this long).
+constexpr int kMaxRows = 128;
 // Token groups of at least this many rows (int8 or RMS-normalized input) of
 // the quantized formats (Q4_K, Q6_K, Q8_0, Q2_K) run as token quads on matrix
 // cores.
@@ -174,7 +175,7 @@ void launch_quantize_norm(const float* x, int32_t stride, const int32_t* gather,
                           int32_t n_rows, const Act8& out, hipStream_t stream);
 // Token rows of one matrix-core matmul launch (steps with more rows than the
 // decode matmul's 8-row groups).
-constexpr int kWideRows = 64;
+constexpr int kWideRows = kMaxRows;
 // Whether launch_gemv_wide takes matrices of this type.
 bool wide_matmul_supported(uint32_t type);
 // Fewest token rows from which launch_gemv_wide outruns the token-quad

@@ -49,9 +49,9 @@ def test_stage_engines_hold_their_layer_ranges(staged):
     assert sum(e.weight_bytes for e in stages) == full.weight_bytes
 
 
-@pytest.mark.parametrize("n_prompt", [5, 100])
+@pytest.mark.parametrize("n_prompt", [5, 200])
 def test_three_stage_pipeline_equals_full_model(staged, n_prompt):
-    """Prefill in chunks (100 rows > the 64-row chunk) and six decode steps
+    """Prefill in chunks (200 rows > the 128-row chunk) and six decode steps
     through three stages give the full model's greedy ids; the middle
     stage's output equals what the last stage reads, row for row."""
     full, stages = staged
