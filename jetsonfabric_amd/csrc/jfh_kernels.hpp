@@ -11,7 +11,7 @@
 namespace jfh::gpu {
 
 // Token rows of one step (a prefill chunk is at most this long).
-constexpr int kMaxRows = 128;
+constexpr int kMaxRows = 256;
 // Token groups of at least this many rows (int8 or RMS-normalized input) of
 // the quantized formats (Q4_K, Q6_K, Q8_0, Q2_K) run as token quads on matrix
 // cores.

@@ -92,7 +92,7 @@ def test_matmul_matches_oracle(typed, n_tok):
         assert jo.nrmse(exact, gpu) < 1e-2
 
 
-@pytest.mark.parametrize("n_tok", [3, 4, 5, 8, 9, 16, 17, 33, 64, 100, 128])
+@pytest.mark.parametrize("n_tok", [3, 4, 5, 8, 9, 16, 17, 33, 64, 100, 128, 256])
 def test_wide_matmul_rows_equal_single_rows(typed, n_tok):
     """Steps of 3 or more int8 rows run every quantized format on matrix cores
     (token quads below the format's wide threshold, 9 rows for Q4_K / Q8_0 and
@@ -109,7 +109,7 @@ def test_wide_matmul_rows_equal_single_rows(typed, n_tok):
             assert np.array_equal(wide[r].view(np.uint32), single[0].view(np.uint32)), f"{name} row {r}"
 
 
-# A gate/up matrix of 8192 rows (512 row groups): steps of 9..128 rows run the
+# A gate/up matrix of 8192 rows (512 row groups): steps of 9..256 rows run the
 # wide K-quant matmuls that share activation loads between row groups (Q4_K on
 # the folded-scale tile, Q6_K and Q2_K with two or four row groups per
 # work-group).
@@ -128,7 +128,7 @@ def wide_typed(request):
 
 def test_wide_matmul_over_row_group_sets_equals_single_rows(wide_typed):
     """The wide matmul that shares each activation load between two or four
-    row groups per work-group: every row of a wide step (9, 17, 33, 64 and 128 rows;
+    row groups per work-group: every row of a wide step (9, 17, 33, 64, 128 and 256 rows;
     Q6_K and Q2_K run token quads below 17) equals the same row computed alone
     (the decode path), bit for bit, and the step matches the oracle's matmul on
     the same int8 rows."""
@@ -136,7 +136,7 @@ def test_wide_matmul_over_row_group_sets_equals_single_rows(wide_typed):
     name = "blk.0.ffn_gate.weight"
     info = model.tensor(name)
     cols, rows = info["shape"]
-    for n_tok in ([9] if t == jf.Q4_K else []) + [17, 33, 64, 128]:
+    for n_tok in ([9] if t == jf.Q4_K else []) + [17, 33, 64, 128, 256]:
         rng = np.random.default_rng(300 + n_tok)
         x = rng.standard_normal((n_tok, cols)).astype(np.float32)
         wide = engine.matmul(name, x, rows)
@@ -151,10 +151,10 @@ def test_wide_matmul_over_row_group_sets_equals_single_rows(wide_typed):
 
 # A Q4_K gate/up matrix of 16384 rows (256 sets of four row groups) over K =
 # 2560 (ten tiles: the decode waves' chains of two and one tiles): steps of
-# 9..128 rows run the whole-K-wave kernel that folds the sub-block scales into
+# 9..256 rows run the whole-K-wave kernel that folds the sub-block scales into
 # the weight operand and shares each activation tile through LDS (steps of more
 # than 64 rows as two token groups).
-WIDE_Q4 = jf.ModelConfig(n_layer=1, n_embd=2560, n_ff=8192, n_head=20, n_head_kv=4, n_vocab=4096, n_ctx=256)
+WIDE_Q4 = jf.ModelConfig(n_layer=1, n_embd=2560, n_ff=8192, n_head=20, n_head_kv=4, n_vocab=4096, n_ctx=512)
 
 
 @pytest.fixture(scope="module")
@@ -166,14 +166,14 @@ def wide_q4():
 
 
 def test_folded_scale_wide_matmul_equals_single_rows(wide_q4):
-    """Every row of a 9..128-row step through the folded-scale kernel equals the
+    """Every row of a 9..256-row step through the folded-scale kernel equals the
     same row computed alone (the decode path), bit for bit, and the step
     matches the oracle's matmul on the same int8 rows."""
     model, engine, _ = wide_q4
     name = "blk.0.ffn_gate.weight"
     info = model.tensor(name)
     cols, rows = info["shape"]
-    for n_tok in (9, 17, 33, 48, 64, 80, 128):
+    for n_tok in (9, 17, 33, 48, 64, 80, 128, 200, 256):
         rng = np.random.default_rng(500 + n_tok)
         x = rng.standard_normal((n_tok, cols)).astype(np.float32)
         wide = engine.matmul(name, x, rows)
@@ -186,18 +186,18 @@ def test_folded_scale_wide_matmul_equals_single_rows(wide_q4):
 
 
 def test_folded_scale_prefill_matches_oracle_and_token_by_token(wide_q4):
-    """A 150-token prompt (chunks of 128 and 22 rows: the SwiGLU gate/up
+    """A 300-token prompt (chunks of 256 and 44 rows: the SwiGLU gate/up
     matrix on the folded-scale kernel) matches the oracle's logits, and a
     session fed the prompt one token at a time reaches the same greedy
     continuation."""
     model, engine, om = wide_q4
-    prompt = _prompt(150, WIDE_Q4.n_vocab, 31)
-    s = engine.create_session(200)
-    ref = om.session(200, jo.MODE_Q8)
+    prompt = _prompt(300, WIDE_Q4.n_vocab, 31)
+    s = engine.create_session(350)
+    ref = om.session(350, jo.MODE_Q8)
     tok, lg = s.prefill_greedy(prompt, logits=True)
     _, rl = ref.forward(prompt, 1)
     assert_logits_match(rl[0], lg, tok, "chunked prefill")
-    one = engine.create_session(200)
+    one = engine.create_session(350)
     first = one.prefill_greedy(prompt[:1])
     for t in prompt[1:]:
         first = one.decode_greedy(t)
@@ -239,17 +239,17 @@ def test_forward_matches_oracle(q4k):
 
 
 def test_chunked_prefill_matches_oracle_and_token_by_token(q4k):
-    """A 150-token prompt is prefilled in chunks of up to 128 rows (matrix-core
+    """A 300-token prompt is prefilled in chunks of up to 256 rows (matrix-core
     matmuls); its logits match the oracle's, and a session fed the same
     prompt one token at a time reaches the same greedy continuation."""
     model, engine, om = q4k
-    prompt = _prompt(150, SMALL.n_vocab, 12)
-    s = engine.create_session(200)
-    ref = om.session(200, jo.MODE_Q8)
+    prompt = _prompt(300, SMALL.n_vocab, 12)
+    s = engine.create_session(350)
+    ref = om.session(350, jo.MODE_Q8)
     tok, lg = s.prefill_greedy(prompt, logits=True)
     _, rl = ref.forward(prompt, 1)
     assert_logits_match(rl[0], lg, tok, "chunked prefill")
-    one = engine.create_session(200)
+    one = engine.create_session(350)
     first = one.prefill_greedy(prompt[:1])
     for t in prompt[1:]:
         first = one.decode_greedy(t)

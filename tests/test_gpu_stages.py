@@ -49,16 +49,16 @@ def test_stage_engines_hold_their_layer_ranges(staged):
     assert sum(e.weight_bytes for e in stages) == full.weight_bytes
 
 
-@pytest.mark.parametrize("n_prompt", [5, 200])
+@pytest.mark.parametrize("n_prompt", [5, 300])
 def test_three_stage_pipeline_equals_full_model(staged, n_prompt):
-    """Prefill in chunks (200 rows > the 128-row chunk) and six decode steps
+    """Prefill in chunks (300 rows > the 256-row chunk) and six decode steps
     through three stages give the full model's greedy ids; the middle
     stage's output equals what the last stage reads, row for row."""
     full, stages = staged
     prompt = _prompt(n_prompt)
-    ref = full.create_session(256)
+    ref = full.create_session(320)
     tok = ref.prefill_greedy(prompt)
-    s = [e.create_session(256) for e in stages]
+    s = [e.create_session(320) for e in stages]
     a0 = s[0].prefill_stage(tokens=prompt)
     assert a0.shape == (n_prompt, CFG.n_embd) and a0.dtype == np.float32 and np.isfinite(a0).all()
     a1 = s[1].prefill_stage(activations=a0)

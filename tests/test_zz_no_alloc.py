@@ -103,10 +103,10 @@ def test_noalloc_matmul_equals_the_allocating_one(engine, tensor):
 
 def test_noalloc_rejects_staging_beyond_the_scratch(engine):
     hip = _Hip()
-    # the head's full output rows for 128 tokens (the row limit): 128 x 8192 x 4 B = 4 MiB fits; a larger
+    # the head's full output rows for 256 tokens (the row limit): 256 x 8192 x 4 B = 8 MiB fits; a larger
     # model's would not, so ask for more rows than the scratch holds through the widest tensor the engine has
     rows, cols = TENSORS["output.weight"]
-    n_tok = 128
+    n_tok = 256
     need = n_tok * rows * 4
     assert need <= SCRATCH_BYTES  # this engine's largest call fits
     x = np.zeros((n_tok, cols), dtype=np.float32)
@@ -114,7 +114,7 @@ def test_noalloc_rejects_staging_beyond_the_scratch(engine):
     assert np.array_equal(got, engine.matmul("output.weight", x, rows))
     # a call beyond the engine's row limit is rejected before any work
     with pytest.raises(jf.JfhError):
-        _noalloc(hip, engine, "output.weight", np.zeros((129, cols), dtype=np.float32), rows)
+        _noalloc(hip, engine, "output.weight", np.zeros((257, cols), dtype=np.float32), rows)
 
 
 def test_noalloc_rejects_a_call_larger_than_the_scratch():
