@@ -2655,7 +2655,7 @@ constexpr int kAttnTile = 16;
 constexpr int kAttnWgKeys = kAttnTile * (kAttnThreads / kWave);
 constexpr int kAttnMaxSplits = 32;
 
-constexpr int kAttnPrefillKeys = 256;
+constexpr int kAttnPrefillKeys = 512;
 // Work-groups of the matrix-core attention resident at once: two per CU
 // (four waves each at its two waves per SIMD) on 256 CUs.
 constexpr int kAttnResidentWgs = 512;
@@ -3665,7 +3665,7 @@ void launch_attention(const float* q, const StepDev* step, int32_t max_len, int3
     // consecutive splits when the step's (split, kv head x query group,
     // sequence) work-groups would exceed one resident round: every split keeps
     // its own partial, so the results do not depend on spw. (Prefill chunks,
-    // whose splits already hold 256 keys or more, run one split per
+    // whose splits already hold kAttnPrefillKeys keys or more, run one split per
     // work-group: two per work-group made 64-row chunks 16 -> 20 us.)
     int spw = 1;
     if (mfma && max_len <= kQuadGroupRows) {
