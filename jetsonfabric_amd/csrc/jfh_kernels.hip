@@ -2200,11 +2200,14 @@ __global__ __launch_bounds__(kMmThreads) void k_mm_wide_rg(GemvArgs a, int32_t n
 // cross-wave reduction.
 //
 // Staging: the work-group's token rows of the next K tile (codes, 16-value
-// sums, scales) are loaded after the current tile's work and written to the
-// other of two LDS buffers; one barrier per tile. A wave loads its weight
-// tile when the tile starts: no register is held across a tile for the next
-// one, so four work-groups fit on a CU (128 VGPRs, 39 KB of LDS each), whose
-// waves hide each other's load latency.
+// sums, scales) are written to the other of two LDS buffers; one barrier per
+// tile. With four token tiles per work-group (long steps) the next tile's
+// staging loads are issued after the current tile's work and a wave loads
+// its weight tile when the tile starts: no register is held across a tile
+// for the next one, so four work-groups fit on a CU (128 VGPRs, 39 KB of LDS
+// each), whose waves hide each other's load latency. With one or two token
+// tiles (9..32-row steps) a tile's work is short, and both loads are issued
+// one tile ahead.
 constexpr int kStageRow = 272;  // bytes per staged token row: 256 codes + 16 bytes of padding (banks)
 
 template <int NW, int TP>
@@ -2306,13 +2309,24 @@ __global__ __launch_bounds__(NW * kWave) void k_mm_wide_q4k(GemvArgs a, int32_t 
 #pragma unroll
         for (int j = 0; j < 4; ++j) total[tl][j] = chain[tl][j] = 0.0F;
     }
+    // one or two token tiles: the next tile's loads are issued before this tile's work (a short
+    // tile hides little latency); four: after it, so that no register is held across a tile
+    constexpr bool AHEAD = TP < 4;
     stage_store(stage_load(0), 0);
+    Raw ahead{};
+    if constexpr (AHEAD) ahead = load_raw(0);
     __syncthreads();
     int b = 0;
     for (int s = 0; s < nb; ++s) {
         const int buf = s & 1;
         const int bn = s + 1 < nb ? next_tile(b) : b;  // clamped: issued unconditionally
-        const Raw cur = load_raw(b);
+        Stage st{};
+        Raw nxt{};
+        if constexpr (AHEAD) {
+            st = stage_load(bn);
+            nxt = load_raw(bn);
+        }
+        const Raw cur = AHEAD ? ahead : load_raw(b);
         if (active) {
             // lane group G's 24-bit field of row i: sc 2G | sc 2G+1 | m 2G | m 2G+1
             const uint32_t f = __builtin_amdgcn_alignbyte(cur.fw.y, cur.fw.x, (3 * G) & 3);
@@ -2381,8 +2395,13 @@ __global__ __launch_bounds__(NW * kWave) void k_mm_wide_q4k(GemvArgs a, int32_t 
             }
         }
         // the next tile's staging loads after this tile's work (their registers are not held across it)
-        __builtin_amdgcn_sched_barrier(0);
-        if (s + 1 < nb) stage_store(stage_load(bn), buf ^ 1);
+        if constexpr (AHEAD) {
+            if (s + 1 < nb) stage_store(st, buf ^ 1);
+            ahead = nxt;
+        } else {
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 1 < nb) stage_store(stage_load(bn), buf ^ 1);
+        }
         b = bn;
         __syncthreads();
     }
