@@ -292,7 +292,9 @@ jfh_status jfh_session_rollback(jfh_session * session, uint32_t n);
  * continuous_batching_executor.cpp:60-100). lengths[i] rows for sessions[i],
  * tokens concatenated; out_tokens receives sum(lengths) ids, out_accepted one
  * count per session (may be NULL), logits (may be NULL) sum(lengths) *
- * n_vocab floats, the rows in the order of out_tokens. */
+ * n_vocab floats, the rows in the order of out_tokens. A step holds at most
+ * 256 token rows (JFH_STATUS_INVALID_ARGUMENT beyond); prefills are split into
+ * chunks of jfh_engine_info.prefill_chunk rows. */
 jfh_status jfh_engine_step_batch(jfh_engine * engine, jfh_session * const * sessions, uint32_t count,
                                  const int32_t * tokens, const uint32_t * lengths, int32_t * out_tokens,
                                  uint32_t * out_accepted, float * logits);
