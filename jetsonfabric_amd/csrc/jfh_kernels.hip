@@ -409,44 +409,46 @@ __device__ void finish_norm(int n_tok, int nb, int K, float eps, const float* ss
 #pragma clang fp contract(on)
 
 // Copies values [c0, c0 + nb*256) of pre-quantized rows into the LDS chunk.
-// Batch b of a thread holds code pieces tid + (4 b + u) NTHR (uint4, u < 4),
+// Batch b of a thread holds code pieces tid + (P b + u) NTHR (uint4, u < P),
 // sum piece tid + b NTHR (uint4 of 8 int16) and block scale tid + b NTHR (A32:
 // scale piece tid + b NTHR, a uint4 of four 32-value block scales); indices
 // are clamped so that every load is issued unconditionally. As with
 // stage_f32, the first batch is loaded ahead of the weights.
-using StageA8Regs = u32x4[6];
+template <int P>
+using StageA8Regs = u32x4[P + 2];
 
-template <int NTHR, bool A32>
-__device__ __forceinline__ void stage_act8_load(const Act8& xq, int n_tok, int c0, int nb, int batch, StageA8Regs& r) {
+template <int NTHR, int P, bool A32>
+__device__ __forceinline__ void stage_act8_load(const Act8& xq, int n_tok, int c0, int nb, int batch,
+                                                StageA8Regs<P>& r) {
     const int tid = threadIdx.x, n16 = nb * 16, nq = n_tok * n16, ns = n_tok * nb * 2, nd = n_tok * nb;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int i = min(tid + (4 * batch + u) * NTHR, nq - 1);
+    for (int u = 0; u < P; ++u) {
+        const int i = min(tid + (P * batch + u) * NTHR, nq - 1);
         const int t = i / n16, k = i - t * n16;
         r[u] = *reinterpret_cast<const u32x4*>(xq.q + static_cast<size_t>(t) * xq.K + c0 + 16 * k);
     }
     {
         const int i = min(tid + batch * NTHR, ns - 1);
         const int t = i / (2 * nb), k = i - t * 2 * nb;
-        r[4] = *reinterpret_cast<const u32x4*>(xq.s + static_cast<size_t>(t) * (xq.K / 16) + c0 / 16 + 8 * k);
+        r[P] = *reinterpret_cast<const u32x4*>(xq.s + static_cast<size_t>(t) * (xq.K / 16) + c0 / 16 + 8 * k);
         if constexpr (A32) {
-            r[5] = *reinterpret_cast<const u32x4*>(xq.d + static_cast<size_t>(t) * (xq.K / 32) + c0 / 32 + 4 * k);
+            r[P + 1] = *reinterpret_cast<const u32x4*>(xq.d + static_cast<size_t>(t) * (xq.K / 32) + c0 / 32 + 4 * k);
         }
     }
     if constexpr (!A32) {
         const int i = min(tid + batch * NTHR, nd - 1);
         const int t = i / nb, b = i - t * nb;
-        r[5].x = __float_as_uint(xq.d[static_cast<size_t>(t) * (xq.K / 256) + c0 / 256 + b]);
+        r[P + 1].x = __float_as_uint(xq.d[static_cast<size_t>(t) * (xq.K / 256) + c0 / 256 + b]);
     }
 }
 
-template <int NTHR, bool A32>
-__device__ __forceinline__ void stage_act8_store(int n_tok, int nb, int batch, const StageA8Regs& r, int8_t* sq,
+template <int NTHR, int P, bool A32>
+__device__ __forceinline__ void stage_act8_store(int n_tok, int nb, int batch, const StageA8Regs<P>& r, int8_t* sq,
                                                  float* sd, int16_t* ss, int chunk) {
     const int tid = threadIdx.x, n16 = nb * 16, nq = n_tok * n16, ns = n_tok * nb * 2, nd = n_tok * nb;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int i = tid + (4 * batch + u) * NTHR;
+    for (int u = 0; u < P; ++u) {
+        const int i = tid + (P * batch + u) * NTHR;
         if (i < nq) {
             const int t = i / n16, k = i - t * n16;
             reinterpret_cast<u32x4*>(sq + t * chunk)[k] = r[u];
@@ -455,26 +457,26 @@ __device__ __forceinline__ void stage_act8_store(int n_tok, int nb, int batch, c
     const int i = tid + batch * NTHR;
     if (i < ns) {
         const int t = i / (2 * nb), k = i - t * 2 * nb;
-        reinterpret_cast<u32x4*>(ss + t * (chunk / 16))[k] = r[4];
-        if constexpr (A32) reinterpret_cast<u32x4*>(sd + t * (chunk / 32))[k] = r[5];
+        reinterpret_cast<u32x4*>(ss + t * (chunk / 16))[k] = r[P];
+        if constexpr (A32) reinterpret_cast<u32x4*>(sd + t * (chunk / 32))[k] = r[P + 1];
     }
     if constexpr (!A32) {
         if (i < nd) {
             const int t = i / nb, b = i - t * nb;
-            sd[t * (chunk / 256) + b] = __uint_as_float(r[5].x);
+            sd[t * (chunk / 256) + b] = __uint_as_float(r[P + 1].x);
         }
     }
 }
 
-template <int NTHR, bool A32>
+template <int NTHR, int P, bool A32>
 __device__ __forceinline__ void stage_act8(const Act8& xq, int n_tok, int c0, int nb, int8_t* sq, float* sd,
-                                           int16_t* ss, int chunk, const StageA8Regs& first) {
+                                           int16_t* ss, int chunk, const StageA8Regs<P>& first) {
     const int nq = n_tok * nb * 16, ns = n_tok * nb * 2;
-    stage_act8_store<NTHR, A32>(n_tok, nb, 0, first, sq, sd, ss, chunk);
-    for (int batch = 1; batch * 4 * NTHR < nq || batch * NTHR < ns; ++batch) {
-        StageA8Regs r;
-        stage_act8_load<NTHR, A32>(xq, n_tok, c0, nb, batch, r);
-        stage_act8_store<NTHR, A32>(n_tok, nb, batch, r, sq, sd, ss, chunk);
+    stage_act8_store<NTHR, P, A32>(n_tok, nb, 0, first, sq, sd, ss, chunk);
+    for (int batch = 1; batch * P * NTHR < nq || batch * NTHR < ns; ++batch) {
+        StageA8Regs<P> r;
+        stage_act8_load<NTHR, P, A32>(xq, n_tok, c0, nb, batch, r);
+        stage_act8_store<NTHR, P, A32>(n_tok, nb, batch, r, sq, sd, ss, chunk);
     }
 }
 
@@ -1340,6 +1342,10 @@ __global__ __launch_bounds__(kMmThreads) void k_mm(GemvArgs a, MmGeom geo) {
     constexpr bool GAIN = IN == kInNormed;
     constexpr int DB = A32 ? 8 : 1;  // activation scales per 256 values
     constexpr int NB = GAIN ? kStageBatch : kStageBatchFloat;  // blocks per wave of a float staging batch
+    // int8 code pieces per thread of a staging batch (a later batch waits
+    // behind the weight tiles in flight): five take two rows of the down
+    // projection (2 x 18944 values) in one batch, six take five in two
+    constexpr int A8P = NT == 4 ? 5 : NT == 8 ? 6 : 4;
     // int8 or normalized rows of a format with a token-quad tile, in token quads, run on matrix cores;
     // Q2_K token groups on the folded-scale tile (token-major: lane group G holds tokens 4 G .. 4 G + 3)
     constexpr bool FOLD = TYPE == 9 && (A8 || GAIN) && NT % 4 == 0;
@@ -1419,8 +1425,8 @@ __global__ __launch_bounds__(kMmThreads) void k_mm(GemvArgs a, MmGeom geo) {
     // the first staging batch is requested before the weights (loads complete
     // in issue order, so the activations do not wait behind weight tiles)
     f32x4 f0[2 * NB];
-    StageA8Regs q0;
-    if constexpr (A8) stage_act8_load<kMmThreads, A32>(a.xq, n_tok, 0, nbcur, 0, q0);
+    StageA8Regs<A8P> q0;
+    if constexpr (A8) stage_act8_load<kMmThreads, A8P, A32>(a.xq, n_tok, 0, nbcur, 0, q0);
     else stage_f32_load<kMmThreads, NB, GAIN>(a.x, n_tok, 0, nbcur, wave, f0);
     prefetch(0);
     // the residual the epilogue adds to is fetched with the first weights
@@ -1440,7 +1446,7 @@ __global__ __launch_bounds__(kMmThreads) void k_mm(GemvArgs a, MmGeom geo) {
         if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(zero)[threadIdx.x] = 0u;
     }
     if constexpr (A8) {
-        stage_act8<kMmThreads, A32>(a.xq, n_tok, 0, nbcur, sq, sd, ss, chunk, q0);
+        stage_act8<kMmThreads, A8P, A32>(a.xq, n_tok, 0, nbcur, sq, sd, ss, chunk, q0);
     } else {
         stage_f32<kMmThreads, NB, GAIN, A32>(a.x, n_tok, 0, nbcur, sq, sd, ss, ssq, chunk, f0);
         if constexpr (GAIN) finish_norm<kMmThreads, A32>(n_tok, nbcur, K, a.x.eps, ssq, sd, chunk);
@@ -1525,11 +1531,11 @@ __global__ __launch_bounds__(kMmThreads) void k_mm(GemvArgs a, MmGeom geo) {
         pr = per_rg(nbcur);
         total = pr * rgn;
         if constexpr (A8) {
-            StageA8Regs qn;
-            stage_act8_load<kMmThreads, A32>(a.xq, n_tok, c0b * 256, nbcur, 0, qn);
+            StageA8Regs<A8P> qn;
+            stage_act8_load<kMmThreads, A8P, A32>(a.xq, n_tok, c0b * 256, nbcur, 0, qn);
             prefetch(c0b);
             __syncthreads();  // every wave is done with the previous pass's activations
-            stage_act8<kMmThreads, A32>(a.xq, n_tok, c0b * 256, nbcur, sq, sd, ss, chunk, qn);
+            stage_act8<kMmThreads, A8P, A32>(a.xq, n_tok, c0b * 256, nbcur, sq, sd, ss, chunk, qn);
         } else {
             f32x4 fn[2 * NB];
             stage_f32_load<kMmThreads, NB, GAIN>(a.x, n_tok, c0b * 256, nbcur, wave, fn);
