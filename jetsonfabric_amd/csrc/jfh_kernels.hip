@@ -3601,7 +3601,8 @@ void launch_gemv_wide(const GemvArgs& a_in, hipStream_t stream) {
     // K-quant layer matrices: one token tile and several row groups per work-group, every
     // activation load shared by the row groups: four (Q4_K only: the other formats'
     // operands take the registers) while kWideMinWgs work-groups remain, else two while
-    // one work-group per CU remains (64-row chunks of 7B: gate_up 4, qkv, o and down 2)
+    // one work-group per CU remains (Q6_K and Q2_K matrices, and Q4_K ones too small for
+    // the folded-scale kernels above)
     int rgs = 1;
     if (!merged && a.mat.type != 7) {
         if (a.mat.type == 11 && (n_rg + 3) / 4 * n_tt >= kWideMinWgs) rgs = 4;

@@ -153,7 +153,7 @@ def test_wide_matmul_over_row_group_sets_equals_single_rows(wide_typed):
 # 2560 (ten tiles: the decode waves' chains of two and one tiles): steps of
 # 9..256 rows run the whole-K-wave kernel that folds the sub-block scales into
 # the weight operand and shares each activation tile through LDS (steps of more
-# than 64 rows as two token groups).
+# than 64 rows as several token groups of four 16-token tiles).
 WIDE_Q4 = jf.ModelConfig(n_layer=1, n_embd=2560, n_ff=8192, n_head=20, n_head_kv=4, n_vocab=4096, n_ctx=512)
 
 
