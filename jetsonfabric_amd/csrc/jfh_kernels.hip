@@ -3300,7 +3300,8 @@ void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStre
 }
 
 // Host-side geometry. Rows are staged in one pass or in passes of kMmChunk
-// values; either way every row's partial sums are added in the same order
+// values (longer balanced passes for a grid of one work-group per CU, when
+// they fit the LDS); either way every row's partial sums are added in the same order
 // for 1 and for 8 tokens, so a draft-verify step reproduces serial decode bit
 // for bit. The per-wave row partials take at most kMmPartBytes of LDS, and
 // the row groups per work-group follow from kMmTargetWgs (mm_geom).
@@ -3346,7 +3347,21 @@ MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds, bool a32) {
     int rgw = rgw_for(chunk);
     // A grid of at most one work-group per CU may use the whole LDS for one pass.
     const size_t one_pass = (n_rg + rgw - 1) / rgw <= kMmTargetWgs ? kMmMaxLds : kMmOnePassLds;
-    if (!normed && K > kMmChunk && mm_lds_bytes(nt, n, K, rgw, K, db) > one_pass) chunk = kMmChunk;
+    if (!normed && K > kMmChunk && mm_lds_bytes(nt, n, K, rgw, K, db) > one_pass) {
+        chunk = kMmChunk;
+        // One work-group per CU: fewer, longer passes when they fit the LDS
+        // (the passes balanced, in whole rounds of the waves' tiles).
+        if ((n_rg + rgw_for(chunk) - 1) / rgw_for(chunk) <= kMmTargetWgs) {
+            const int round = 256 * kMmWaves;
+            for (int passes = 2; passes * kMmChunk < K; ++passes) {
+                const int c = ((K + passes - 1) / passes + round - 1) / round * round;
+                if (mm_lds_bytes(nt, n, c, rgw_for(c), K, db) <= kMmMaxLds) {
+                    chunk = c;
+                    break;
+                }
+            }
+        }
+    }
     rgw = rgw_for(chunk);
     if (!normed && mm_lds_bytes(nt, n, chunk, rgw, K, db) > kMmMaxLds) {
         // wide token groups: shorter passes, in whole rounds of the waves' tiles, until the staging fits
