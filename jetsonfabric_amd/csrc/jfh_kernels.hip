@@ -1365,10 +1365,12 @@ __global__ __launch_bounds__(kMmThreads) void k_mm(GemvArgs a, MmGeom geo) {
     int16_t* ss = reinterpret_cast<int16_t*>(sd + ((n_tok * nbc * DB + 3) & ~3));  // 16-byte aligned
     // Row partials. One pass over K: each wave stores its finished row-group
     // sums with the four lane groups already combined, [rgw][W][16 rows][NT].
-    // Several passes: every lane keeps running sums, [rgw][W][64 lanes][NT].
+    // Several passes: every lane keeps running sums, [rgw][W][64 lanes][PS]
+    // (the folded Q2_K tile keeps four per lane: lane group G's tokens 4 G + q).
+    constexpr int PS = FOLD ? 4 : NT;
     const bool single = NT <= 2 || nbc >= nb;  // one- and two-token groups always run one pass (mm_geom)
     float* part = reinterpret_cast<float*>(ss + n_tok * (chunk / 16));
-    float* ssq = part + (single ? rgw * W * 16 * NT : rgw * W * 64 * NT);  // [n_tok][nbc] sums of squares (normed)
+    float* ssq = part + (single ? rgw * W * 16 * NT : rgw * W * 64 * PS);  // [n_tok][nbc] sums of squares (normed)
     float* lv = ssq + n_tok * nbc;  // [rgw * 16 * NT]
     // 64 zero bytes (16-byte aligned) for the masked operand slots of TileQ4Quad
     int8_t* zero = reinterpret_cast<int8_t*>(lds_raw) +
@@ -1441,7 +1443,7 @@ __global__ __launch_bounds__(kMmThreads) void k_mm(GemvArgs a, MmGeom geo) {
         y_pre = *src;
     }
     // zero partials (waves without tiles, when the row has fewer blocks than waves, add nothing)
-    for (int i = threadIdx.x; i < (single ? rgw * W * 16 * NT : rgw * W * 64 * NT); i += kMmThreads) part[i] = 0.0F;
+    for (int i = threadIdx.x; i < (single ? rgw * W * 16 * NT : rgw * W * 64 * PS); i += kMmThreads) part[i] = 0.0F;
     if constexpr (QUAD) {
         if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(zero)[threadIdx.x] = 0u;
     }
@@ -1457,14 +1459,14 @@ __global__ __launch_bounds__(kMmThreads) void k_mm(GemvArgs a, MmGeom geo) {
         if (total > 0) {
             float acc[NT];
             int cm = 0;                                             // tile of the row group being computed
-            float* slot = part + (wave * 64 + lane) * NT;          // the lane's running sums of that row group
+            float* slot = part + (wave * 64 + lane) * PS;          // the lane's running sums of that row group
             float* done = part + (wave * 16 + (lane & 15)) * NT;   // its finished sums (one pass)
             const int8_t* xq0 = sq + wave * 256 + 64 * grp;         // its activation slice
             // one item of the wave's stream (its tile cm of the current row group) from slot u of the ring
             auto consume = [&](const Regs& tile_regs) {
                 if (cm == 0) {
 #pragma unroll
-                    for (int t = 0; t < NT; ++t) acc[t] = single ? 0.0F : slot[t];
+                    for (int t = 0; t < NT; ++t) acc[t] = single || t >= PS ? 0.0F : slot[t];
                 }
                 const int bl = wave + W * cm;
                 XLds x;
@@ -1504,8 +1506,8 @@ __global__ __launch_bounds__(kMmThreads) void k_mm(GemvArgs a, MmGeom geo) {
                         done += W * 16 * NT;
                     } else {
 #pragma unroll
-                        for (int t = 0; t < NT; ++t) slot[t] = acc[t];
-                        slot += W * 64 * NT;
+                        for (int t = 0; t < PS; ++t) slot[t] = acc[t];
+                        slot += W * 64 * PS;
                     }
                 }
             };
@@ -1559,7 +1561,7 @@ __global__ __launch_bounds__(kMmThreads) void k_mm(GemvArgs a, MmGeom geo) {
             float p[4];
             if constexpr (FOLD) {
                 // token t's running sum sits in lane group t / 4, slot t % 4 alone
-                v += part[((r * W + w) * 64 + i + 16 * (t >> 2)) * NT + (t & 3)];
+                v += part[((r * W + w) * 64 + i + 16 * (t >> 2)) * PS + (t & 3)];
                 continue;
             }
 #pragma unroll
@@ -3313,11 +3315,13 @@ constexpr size_t kMmMaxLds = 160 * 1024;
 
 // LDS of k_mm: staging of n rows (db activation scales per 256 values), row
 // partials and epilogue values of nt token slots
-size_t mm_lds_bytes(int nt, int n, int chunk, int rgw, int K, int db) {
+// ps: running sums per lane of a several-pass matmul (nt; 4 for the folded Q2_K tile).
+size_t mm_lds_bytes(int nt, int ps, int n, int chunk, int rgw, int K, int db) {
     const size_t nbc = static_cast<size_t>(chunk) / 256;
-    const size_t part_rows = chunk >= K ? 16 : 64;  // one pass: combined lane groups (see k_mm)
+    // one pass: combined lane groups, nt sums per row; several: ps per lane (see k_mm)
+    const size_t part = chunk >= K ? 16 * static_cast<size_t>(nt) : 64 * static_cast<size_t>(ps);
     return static_cast<size_t>(n) * chunk + (n * nbc * db + 3) / 4 * 16 + static_cast<size_t>(n) * chunk / 8 +
-           static_cast<size_t>(rgw) * kMmWaves * part_rows * nt * 4 + n * nbc * 4 +
+           static_cast<size_t>(rgw) * kMmWaves * part * 4 + n * nbc * 4 +
            static_cast<size_t>(rgw) * 16 * nt * 4 + 16 + 64;  // + the aligned zero bytes
 }
 
@@ -3331,9 +3335,12 @@ MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds, bool a32) {
     // work-groups per CU.
     const int wgs = n_rg <= 2 * kMmTargetWgs ? kMmTargetWgs : 2 * kMmTargetWgs;
     const int want = (n_rg + wgs - 1) / wgs;
+    // running sums per lane of several passes: four on the folded Q2_K tile (int8 or normalized token groups)
+    const bool fold = a.mat.type == 9 && (a.xq.q != nullptr || a.x.gain != nullptr) && nt % 4 == 0;
+    const int ps = fold ? 4 : nt;
     // row groups per work-group within kMmPartBytes of row partials
     auto rgw_for = [&](int chunk) {
-        const int cap = kMmPartBytes / (kMmWaves * (chunk >= K ? 16 : 64) * nt * 4);
+        const int cap = kMmPartBytes / (kMmWaves * (chunk >= K ? 16 * nt : 64 * ps) * 4);
         return std::max(1, std::min(want, cap));
     };
     // The whole row is staged in one pass when it fits (a normalized input
@@ -3347,7 +3354,7 @@ MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds, bool a32) {
     int rgw = rgw_for(chunk);
     // A grid of at most one work-group per CU may use the whole LDS for one pass.
     const size_t one_pass = (n_rg + rgw - 1) / rgw <= kMmTargetWgs ? kMmMaxLds : kMmOnePassLds;
-    if (!normed && K > kMmChunk && mm_lds_bytes(nt, n, K, rgw, K, db) > one_pass) {
+    if (!normed && K > kMmChunk && mm_lds_bytes(nt, ps, n, K, rgw, K, db) > one_pass) {
         chunk = kMmChunk;
         // One work-group per CU: fewer, longer passes when they fit the LDS
         // (the passes balanced, in whole rounds of the waves' tiles).
@@ -3355,7 +3362,7 @@ MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds, bool a32) {
             const int round = 256 * kMmWaves;
             for (int passes = 2; passes * kMmChunk < K; ++passes) {
                 const int c = ((K + passes - 1) / passes + round - 1) / round * round;
-                if (mm_lds_bytes(nt, n, c, rgw_for(c), K, db) <= kMmMaxLds) {
+                if (mm_lds_bytes(nt, ps, n, c, rgw_for(c), K, db) <= kMmMaxLds) {
                     chunk = c;
                     break;
                 }
@@ -3363,18 +3370,18 @@ MmGeom mm_geom(const GemvArgs& a, int nt, size_t& lds, bool a32) {
         }
     }
     rgw = rgw_for(chunk);
-    if (!normed && mm_lds_bytes(nt, n, chunk, rgw, K, db) > kMmMaxLds) {
+    if (!normed && mm_lds_bytes(nt, ps, n, chunk, rgw, K, db) > kMmMaxLds) {
         // wide token groups: shorter passes, in whole rounds of the waves' tiles, until the staging fits
         const int round = 256 * kMmWaves;
         chunk = std::min(chunk, kMmChunk) / round * round;
         rgw = rgw_for(chunk);
-        while (chunk > round && mm_lds_bytes(nt, n, chunk, rgw, K, db) > kMmMaxLds) chunk -= round;
+        while (chunk > round && mm_lds_bytes(nt, ps, n, chunk, rgw, K, db) > kMmMaxLds) chunk -= round;
     }
     if (nt <= 2 && chunk < K) throw std::invalid_argument("one- and two-token matmul rows must fit one pass");
     MmGeom g;
     g.rgw = rgw;
     g.chunk = chunk;
-    lds = mm_lds_bytes(nt, n, chunk, rgw, K, db);
+    lds = mm_lds_bytes(nt, ps, n, chunk, rgw, K, db);
     if (lds > kMmMaxLds) throw std::invalid_argument("matmul staging does not fit the LDS");
     return g;
 }
